@@ -1,0 +1,168 @@
+/*
+ * moss_offload.h - C ABI of the MI355X activation-offload engine.
+ *
+ * The engine replaces the per-tensor work that MOSS-Image's saved-tensor hooks do in
+ * training/activation_offload.py (reference repository RyukoMatoiFan/MOSS-Image):
+ *
+ *   pack   (activation_offload.py:116-134)  pinned torch.empty + copy_(non_blocking) + Event
+ *   unpack (activation_offload.py:136-147)  wait_event + _restore_layout
+ *   _restore_layout (activation_offload.py:64-77)  empty_strided + copy_ + as_strided
+ *
+ * The reference is pure Python and exposes no foreign-function interface of its own; the
+ * Python shim in moss-image_amd/moss_offload binds this header through ctypes and keeps the
+ * reference's Python API (activation_cpu_offload, _offload_view, _restore_layout).
+ *
+ * Conventions
+ *   - Every function returns 0 on success and a non-zero status otherwise (a hipError_t value,
+ *     or MO_E_* below). mo_last_error() returns a thread-local message for the last failure.
+ *   - Device pointers and streams cross the boundary as uint64_t (data_ptr(), cuda_stream).
+ *   - No C++ exception crosses the boundary. All engine calls are serialised by an engine mutex.
+ *
+ * Payload format (shared by every entry point)
+ *   A tensor's payload is its logical elements in STORAGE order: dimensions of size > 1 sorted
+ *   by stride, largest first, so the copy reads and writes memory in address order and never
+ *   transposes. Restoring into a tensor with the same strides is the exact inverse. Each
+ *   payload starts at a 256-byte aligned offset of its staging buffer.
+ */
+#ifndef MOSS_OFFLOAD_H
+#define MOSS_OFFLOAD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MO_ABI_VERSION 1
+#define MO_MAX_DIMS 8
+
+/* Error codes outside the hipError_t range. */
+#define MO_E_INVALID 1001   /* bad argument, descriptor or handle          */
+#define MO_E_LAYOUT 1002    /* overlapping / negative-stride layout         */
+#define MO_E_HOST_OOM 1003  /* pinned host pool limit reached               */
+#define MO_E_STATE 1004     /* call not valid in the engine's current state */
+
+/* Flags for mo_config.flags. */
+#define MO_FLAG_TIMING 0x1       /* time every D2H/H2D copy with HIP events       */
+#define MO_FLAG_KERNEL_COPY 0x2  /* move D2H/H2D with a copy kernel, not the DMA */
+
+/*
+ * A strided tensor view on the device. `ptr` is the address of logical element (0,...,0),
+ * which is the lowest address because all strides are non-negative. Strides are in
+ * elements. This is the information the reference reads at activation_offload.py:40-61
+ * (shape, stride) plus data_ptr() and element_size().
+ */
+typedef struct mo_tensor {
+  uint64_t ptr;
+  uint32_t elem_bytes; /* 1, 2, 4, 8 or 16 */
+  uint32_t ndim;       /* 0..MO_MAX_DIMS */
+  int64_t size[MO_MAX_DIMS];
+  int64_t stride[MO_MAX_DIMS];
+} mo_tensor;
+
+/* Engine configuration (mo_create). Zero fields take the defaults in brackets. */
+typedef struct mo_config {
+  uint64_t stage_slot_bytes;    /* [64 MiB] device staging slot size (forward arena)   */
+  uint32_t stage_slots;         /* [4] slots in the forward staging ring               */
+  uint32_t restore_slots;       /* [4] slots in the backward restore ring              */
+  uint64_t host_limit_bytes;    /* [0 = no limit] cap on pinned host memory             */
+  uint64_t host_chunk_bytes;    /* [1 GiB] granularity of hipHostMalloc reservations   */
+  uint32_t flags;               /* MO_FLAG_*                                          */
+  uint32_t copy_kernel_blocks;  /* [64] workgroups of the copy kernel (KERNEL_COPY)  */
+} mo_config;
+
+/* Where one packed tensor lives: its group (one block's saves) and index in the group. */
+typedef struct mo_ref {
+  uint64_t group;
+  uint32_t entry;
+  uint32_t reserved;
+} mo_ref;
+
+typedef struct mo_stats {
+  uint64_t groups_created, groups_live, entries_live;
+  uint64_t bytes_packed, bytes_unpacked;  /* payload bytes through pack / unpack kernels */
+  uint64_t bytes_d2h, bytes_h2d;          /* bytes over the host link                  */
+  uint64_t pack_launches, unpack_launches, d2h_copies, h2d_copies;
+  uint64_t host_bytes_in_use, host_bytes_peak, host_bytes_reserved;
+  uint64_t stage_slot_waits;   /* compute stream told to wait for a staging slot's D2H */
+  uint64_t stage_slot_busy;    /* ... while that D2H was still running (a likely stall) */
+  uint64_t prefetch_issued;    /* segments fetched ahead of their unpack              */
+  uint64_t prefetch_hits;      /* segments already resident when unpack asked          */
+  uint64_t restore_fetches;    /* segments fetched on demand by unpack                 */
+  double d2h_ms, h2d_ms;       /* summed copy durations (MO_FLAG_TIMING), completed only */
+  uint64_t timed_d2h_bytes, timed_h2d_bytes;
+} mo_stats;
+
+typedef struct mo_engine mo_engine;
+
+/* ---- library ---------------------------------------------------------------------------- */
+int mo_abi_version(void);
+const char* mo_last_error(void);
+
+/* ---- kernels alone (microbenchmarks, parity tests, _restore_layout) ---------------------- */
+
+/* Payload layout of n tensors: offsets[i] (256-byte aligned) and the total bytes. Host only. */
+int mo_payload_layout(const mo_tensor* tensors, int n, uint64_t* offsets, uint64_t* total_bytes);
+
+/* Pack kernel: gather n tensor views into `payload` at `offsets` (NULL = mo_payload_layout).
+ * Replaces the device side of cpu.copy_(source) at activation_offload.py:124. */
+int mo_gather(const mo_tensor* tensors, int n, uint64_t payload, const uint64_t* offsets,
+              uint64_t stream);
+
+/* Unpack kernel: scatter payloads back into n tensor views with the same strides.
+ * Replaces restored.copy_(payload) at activation_offload.py:75-76. */
+int mo_scatter(const mo_tensor* tensors, int n, uint64_t payload, const uint64_t* offsets,
+               uint64_t stream);
+
+/* Copy `bytes` between device and pinned host memory with the engine's link-copy kernel
+ * (direction 0 = device->host, 1 = host->device). Measures the copy-kernel alternative to
+ * the DMA engines. */
+int mo_link_copy(uint64_t dst, uint64_t src, uint64_t bytes, int direction, uint32_t blocks,
+                 uint64_t stream);
+
+/* ---- engine (the activation_cpu_offload hook pair, activation_offload.py:80-149) --------- */
+int mo_create(int device, const mo_config* config, mo_engine** out);
+int mo_destroy(mo_engine* engine);
+
+/* Pack n saved tensors into the open group (a new group opens if none is). Each tensor is
+ * gathered into the staging ring on `stream` and refs[i] says where it went. Replaces
+ * pack(), activation_offload.py:116-134. */
+int mo_pack(mo_engine* engine, const mo_tensor* tensors, int n, uint64_t stream, mo_ref* refs);
+
+/* Close the open group: the compute stream records an event, the D2H stream waits for it and
+ * streams the group's staging segments into pinned host memory. *group receives the id
+ * (UINT64_MAX if no group was open). Replaces the Event().record at activation_offload.py:125. */
+int mo_commit(mo_engine* engine, uint64_t stream, uint64_t* group);
+
+/* Enqueue H2D copies of a committed group into free restore slots (as many segments as fit),
+ * so a later mo_unpack finds them resident. Never blocks the host. */
+int mo_prefetch(mo_engine* engine, uint64_t group, uint64_t stream);
+
+/* Restore entries of a group: dst[i] is the device address for entry i (0 = skip it), laid out
+ * with the strides the entry was packed with. H2D copies any missing segment, makes `stream`
+ * wait for it, and launches the unpack kernel on `stream`. Replaces unpack(),
+ * activation_offload.py:136-147. */
+int mo_unpack(mo_engine* engine, uint64_t group, const uint64_t* dst, uint32_t n,
+              uint64_t stream);
+
+/* Drop a group: its pinned host memory returns to the pool once every copy using it ended. */
+int mo_release(mo_engine* engine, uint64_t group);
+
+/* Number of entries in a group and whether its D2H completed (host query, non-blocking). */
+int mo_group_info(mo_engine* engine, uint64_t group, uint32_t* entries, uint64_t* payload_bytes,
+                  int* d2h_complete);
+
+/* Block the host until every copy the engine enqueued has finished. */
+int mo_synchronize(mo_engine* engine);
+
+int mo_get_stats(mo_engine* engine, mo_stats* stats);
+int mo_reset_stats(mo_engine* engine);
+
+/* Release pinned chunks that hold no live payload. */
+int mo_trim(mo_engine* engine);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOSS_OFFLOAD_H */

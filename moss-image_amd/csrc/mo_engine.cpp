@@ -1,0 +1,931 @@
+// Activation-offload engine: staging ring, pinned host pool, copy streams, restore ring and
+// the C ABI declared in include/moss_offload.h.
+//
+// Forward (replaces activation_offload.py:116-134, one pinned tensor + copy per save):
+//   mo_pack gathers each saved tensor into the open segment of the device staging ring on the
+//   caller's compute stream. A segment closes when its slot fills or the group (one block's
+//   saves) is committed: the compute stream records an event, the D2H stream waits for it and
+//   copies the whole segment into pinned host memory in one transfer. Before a slot is
+//   refilled, the compute stream waits (on the GPU, never on the host) for the slot's last D2H.
+// Backward (replaces activation_offload.py:136-147, wait_event + _restore_layout):
+//   mo_prefetch copies a group's segments into free restore slots on the H2D stream ahead of
+//   use. mo_unpack fetches whatever is missing, makes the compute stream wait for the H2D, and
+//   scatters each entry into its destination with the unpack kernel.
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+#include <deque>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/moss_offload.h"
+#include "mo_internal.h"
+
+namespace mo {
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  g_error = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+  return (int)e;
+}
+
+#define MO_HIP(call)                              \
+  do {                                            \
+    hipError_t _e = (call);                       \
+    if (_e != hipSuccess) return hip_fail(_e, #call); \
+  } while (0)
+
+constexpr uint64_t kNone = UINT64_MAX;
+constexpr uint64_t kMinPiece = 1ull << 20;  // do not start a piece in less slot space than this
+constexpr uint64_t kPieceAlign = 4096;      // split pieces at page multiples
+constexpr uint64_t kHostAlign = 4096;
+
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(int device) {
+    if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+    if (prev_ != device) (void)hipSetDevice(device);
+    dev_ = device;
+  }
+  ~DeviceGuard() {
+    if (prev_ >= 0 && prev_ != dev_) (void)hipSetDevice(prev_);
+  }
+
+ private:
+  int prev_ = -1, dev_ = -1;
+};
+
+// ------------------------------------------------------------------------------------------
+// Pinned host pool: hipHostMalloc chunks, first-fit with coalescing, page-aligned blocks.
+class HostPool {
+ public:
+  struct Chunk {
+    char* base = nullptr;
+    char* dev = nullptr;  // device-visible alias (for the copy kernel)
+    uint64_t size = 0;
+    uint64_t used = 0;
+    std::map<uint64_t, uint64_t> free;  // offset -> size
+  };
+
+  void configure(uint64_t limit, uint64_t chunk) {
+    limit_ = limit;
+    chunk_ = chunk;
+  }
+  ~HostPool() { release_all(); }
+
+  int alloc(uint64_t bytes, char** out) {
+    bytes = align_up(bytes ? bytes : 1, kHostAlign);
+    for (auto& c : chunks_) {
+      for (auto it = c->free.begin(); it != c->free.end(); ++it) {
+        if (it->second >= bytes) {
+          const uint64_t off = it->first, sz = it->second;
+          c->free.erase(it);
+          if (sz > bytes) c->free.emplace(off + bytes, sz - bytes);
+          c->used += bytes;
+          account(bytes);
+          *out = c->base + off;
+          return 0;
+        }
+      }
+    }
+    const uint64_t size = align_up(std::max(bytes, chunk_), 2ull << 20);
+    if (limit_ && reserved_ + size > limit_) {
+      return fail(MO_E_HOST_OOM, "pinned host pool limit reached: reserved " + std::to_string(reserved_) +
+                                     " B + " + std::to_string(size) + " B > limit " + std::to_string(limit_) +
+                                     " B (raise host_limit_bytes or offload less)");
+    }
+    void* p = nullptr;
+    hipError_t e = hipHostMalloc(&p, size, hipHostMallocDefault);
+    if (e != hipSuccess || !p) {
+      return fail(MO_E_HOST_OOM, std::string("hipHostMalloc of ") + std::to_string(size) +
+                                     " B failed: " + hipGetErrorString(e) + " (pinned host memory exhausted)");
+    }
+    void* dp = nullptr;
+    if (hipHostGetDevicePointer(&dp, p, 0) != hipSuccess) dp = p;
+    auto c = std::make_unique<Chunk>();
+    c->base = (char*)p;
+    c->dev = (char*)dp;
+    c->size = size;
+    if (size > bytes) c->free.emplace(bytes, size - bytes);
+    c->used = bytes;
+    reserved_ += size;
+    account(bytes);
+    *out = c->base;
+    chunks_.push_back(std::move(c));
+    return 0;
+  }
+
+  void free(char* p, uint64_t bytes) {
+    bytes = align_up(bytes ? bytes : 1, kHostAlign);
+    for (auto& c : chunks_) {
+      if (p >= c->base && p < c->base + c->size) {
+        uint64_t off = (uint64_t)(p - c->base), sz = bytes;
+        auto next = c->free.lower_bound(off);
+        if (next != c->free.end() && off + sz == next->first) {
+          sz += next->second;
+          next = c->free.erase(next);
+        }
+        if (next != c->free.begin()) {
+          auto prev = std::prev(next);
+          if (prev->first + prev->second == off) {
+            off = prev->first;
+            sz += prev->second;
+            c->free.erase(prev);
+          }
+        }
+        c->free.emplace(off, sz);
+        c->used -= bytes;
+        in_use_ -= bytes;
+        return;
+      }
+    }
+  }
+
+  char* device_alias(char* p) const {
+    for (auto& c : chunks_)
+      if (p >= c->base && p < c->base + c->size) return c->dev + (p - c->base);
+    return p;
+  }
+
+  void trim() {
+    for (auto it = chunks_.begin(); it != chunks_.end();) {
+      if ((*it)->used == 0) {
+        (void)hipHostFree((*it)->base);
+        reserved_ -= (*it)->size;
+        it = chunks_.erase(it);
+      } else {
+        ++it;
+      }
+    }
+  }
+
+  void release_all() {
+    for (auto& c : chunks_) (void)hipHostFree(c->base);
+    chunks_.clear();
+    reserved_ = in_use_ = 0;
+  }
+
+  uint64_t in_use() const { return in_use_; }
+  uint64_t peak() const { return peak_; }
+  uint64_t reserved() const { return reserved_; }
+
+ private:
+  void account(uint64_t b) {
+    in_use_ += b;
+    peak_ = std::max(peak_, in_use_);
+  }
+  std::vector<std::unique_ptr<Chunk>> chunks_;
+  uint64_t limit_ = 0, chunk_ = 1ull << 30;
+  uint64_t reserved_ = 0, in_use_ = 0, peak_ = 0;
+};
+
+// ------------------------------------------------------------------------------------------
+struct Piece {
+  uint32_t entry;
+  uint64_t first;    // byte offset within the entry's payload
+  uint64_t nbytes;
+  uint64_t seg_off;  // byte offset within the segment
+};
+
+struct Segment {
+  int stage_slot = -1;
+  uint64_t stage_off = 0;
+  uint64_t bytes = 0;
+  std::vector<Piece> pieces;
+  char* host = nullptr;
+  hipEvent_t d2h_done = nullptr;
+  hipEvent_t h2d_done = nullptr;
+  bool committed = false;
+  bool h2d_issued = false;
+  bool prefetched = false;
+  int restore_slot = -1;
+  uint64_t restore_gen = 0;
+};
+
+struct Entry {
+  Canon canon;
+};
+
+struct Group {
+  uint64_t id = 0;
+  bool open = true;
+  uint64_t payload_bytes = 0;
+  std::vector<Entry> entries;
+  std::vector<Segment> segs;
+};
+
+struct StageSlot {
+  char* dev = nullptr;
+  uint64_t used = 0;
+  hipEvent_t free_ev = nullptr;
+  bool free_recorded = false;
+};
+
+struct RestoreSlot {
+  char* dev = nullptr;
+  uint64_t group = kNone;
+  uint32_t seg = 0;
+  uint64_t gen = 0;
+  uint64_t tick = 0;
+  bool consumed = true;  // scattered at least once since fetched (or empty)
+  hipEvent_t ready = nullptr;
+  hipEvent_t consumed_ev = nullptr;
+  bool consumed_recorded = false;
+};
+
+struct PendingFree {
+  char* host;
+  uint64_t bytes;
+  hipEvent_t ev[2];
+};
+
+struct Timing {
+  hipEvent_t start, end;
+  uint64_t bytes;
+  bool d2h;
+};
+
+}  // namespace
+
+struct Engine {
+  int device = 0;
+  mo_config cfg{};
+  std::mutex mu;
+  hipStream_t d2h = nullptr, h2d = nullptr;
+  hipEvent_t ev_tmp = nullptr;
+  std::vector<StageSlot> stage;
+  std::vector<RestoreSlot> restore;
+  int stage_cur = 0;
+  HostPool pool;
+  std::unordered_map<uint64_t, std::unique_ptr<Group>> groups;
+  Group* open_group = nullptr;
+  int open_seg = -1;  // index into open_group->segs, or -1
+  uint64_t next_group = 0;
+  uint64_t gen_counter = 0, tick = 0;
+  std::vector<hipEvent_t> event_pool, timing_pool;
+  std::deque<PendingFree> pending;
+  std::deque<Timing> timings;
+  mo_stats st{};
+
+  // ---- events ----
+  int new_event(hipEvent_t* ev) {
+    if (!event_pool.empty()) {
+      *ev = event_pool.back();
+      event_pool.pop_back();
+      return 0;
+    }
+    MO_HIP(hipEventCreateWithFlags(ev, hipEventDisableTiming));
+    return 0;
+  }
+  void recycle(hipEvent_t ev) {
+    if (ev) event_pool.push_back(ev);
+  }
+  int timing_begin(hipStream_t s, Timing& t) {
+    t.start = t.end = nullptr;
+    if (!(cfg.flags & MO_FLAG_TIMING)) return 0;
+    for (hipEvent_t* e : {&t.start, &t.end}) {
+      if (!timing_pool.empty()) {
+        *e = timing_pool.back();
+        timing_pool.pop_back();
+      } else {
+        MO_HIP(hipEventCreate(e));
+      }
+    }
+    MO_HIP(hipEventRecord(t.start, s));
+    return 0;
+  }
+  int timing_end(hipStream_t s, Timing& t) {
+    if (!t.start) return 0;
+    MO_HIP(hipEventRecord(t.end, s));
+    timings.push_back(t);
+    return 0;
+  }
+  void process_timings(bool wait) {
+    while (!timings.empty()) {
+      Timing& t = timings.front();
+      if (wait) (void)hipEventSynchronize(t.end);
+      else if (hipEventQuery(t.end) != hipSuccess) break;
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, t.start, t.end) == hipSuccess) {
+        if (t.d2h) {
+          st.d2h_ms += ms;
+          st.timed_d2h_bytes += t.bytes;
+        } else {
+          st.h2d_ms += ms;
+          st.timed_h2d_bytes += t.bytes;
+        }
+      }
+      timing_pool.push_back(t.start);
+      timing_pool.push_back(t.end);
+      timings.pop_front();
+    }
+  }
+
+  // ---- deferred host frees ----
+  void process_pending(bool wait) {
+    for (auto it = pending.begin(); it != pending.end();) {
+      bool done = true;
+      for (hipEvent_t e : it->ev) {
+        if (!e) continue;
+        if (wait) (void)hipEventSynchronize(e);
+        else if (hipEventQuery(e) != hipSuccess) done = false;
+      }
+      if (done) {
+        pool.free(it->host, it->bytes);
+        recycle(it->ev[0]);
+        recycle(it->ev[1]);
+        it = pending.erase(it);
+      } else {
+        ++it;
+      }
+    }
+  }
+
+  // ---- link copies ----
+  int copy(char* dst, const char* src, uint64_t bytes, bool to_host, hipStream_t s) {
+    Timing t{};
+    t.bytes = bytes;
+    t.d2h = to_host;
+    if (int rc = timing_begin(s, t)) return rc;
+    if (cfg.flags & MO_FLAG_KERNEL_COPY) {
+      char* d = to_host ? pool.device_alias(dst) : dst;
+      const char* sp = to_host ? src : pool.device_alias((char*)src);
+      int rc = launch_link_copy(d, sp, bytes, cfg.copy_kernel_blocks, s);
+      if (rc) return hip_fail((hipError_t)rc, "link copy kernel launch");
+    } else {
+      MO_HIP(hipMemcpyAsync(dst, src, bytes, to_host ? hipMemcpyDeviceToHost : hipMemcpyHostToDevice, s));
+    }
+    return timing_end(s, t);
+  }
+
+  // ---- forward ----
+  int close_segment(Launcher& L, hipStream_t stream) {
+    if (!open_group || open_seg < 0) return 0;
+    if (int rc = L.flush()) return hip_fail((hipError_t)rc, "pack kernel launch");
+    Segment& seg = open_group->segs[open_seg];
+    StageSlot& slot = stage[seg.stage_slot];
+    seg.bytes = slot.used - seg.stage_off;
+    open_seg = -1;
+    if (int rc = pool.alloc(seg.bytes, &seg.host)) return rc;
+    MO_HIP(hipEventRecord(ev_tmp, stream));
+    MO_HIP(hipStreamWaitEvent(d2h, ev_tmp, 0));
+    if (int rc = copy(seg.host, slot.dev + seg.stage_off, seg.bytes, true, d2h)) return rc;
+    if (int rc = new_event(&seg.d2h_done)) return rc;
+    MO_HIP(hipEventRecord(seg.d2h_done, d2h));
+    MO_HIP(hipEventRecord(slot.free_ev, d2h));
+    slot.free_recorded = true;
+    seg.committed = true;
+    st.d2h_copies++;
+    st.bytes_d2h += seg.bytes;
+    return 0;
+  }
+
+  int advance_slot(hipStream_t stream) {
+    stage_cur = (stage_cur + 1) % (int)stage.size();
+    StageSlot& s = stage[stage_cur];
+    if (s.free_recorded) {
+      if (hipEventQuery(s.free_ev) != hipSuccess) st.stage_slot_busy++;
+      MO_HIP(hipStreamWaitEvent(stream, s.free_ev, 0));
+      st.stage_slot_waits++;
+    }
+    s.used = 0;
+    return 0;
+  }
+
+  int pack(const mo_tensor* ts, int n, hipStream_t stream, mo_ref* refs) {
+    process_pending(false);
+    std::vector<Canon> canons(n);
+    std::string err;
+    for (int i = 0; i < n; ++i) {
+      if (int rc = canonicalize(ts[i], canons[i], err)) return fail(rc, "mo_pack: tensor " + std::to_string(i) + ": " + err);
+    }
+    if (!open_group) {
+      auto g = std::make_unique<Group>();
+      g->id = next_group++;
+      open_group = g.get();
+      groups.emplace(g->id, std::move(g));
+      open_seg = -1;
+      st.groups_created++;
+    }
+    Group& g = *open_group;
+    Launcher L(true, stream);
+    const uint64_t slot_bytes = cfg.stage_slot_bytes;
+    for (int i = 0; i < n; ++i) {
+      const Canon& c = canons[i];
+      const uint32_t idx = (uint32_t)g.entries.size();
+      g.entries.push_back(Entry{c});
+      g.payload_bytes += c.nbytes;
+      refs[i].group = g.id;
+      refs[i].entry = idx;
+      refs[i].reserved = 0;
+      uint64_t remaining = c.nbytes, first = 0;
+      while (remaining > 0) {
+        StageSlot& s = stage[stage_cur];
+        const uint64_t pos = align_up(s.used, kPayloadAlign);
+        const uint64_t space = pos < slot_bytes ? slot_bytes - pos : 0;
+        if (space == 0 || (space < remaining && space < kMinPiece)) {
+          if (int rc = close_segment(L, stream)) return rc;
+          if (int rc = advance_slot(stream)) return rc;
+          continue;
+        }
+        if (open_seg < 0 || g.segs[open_seg].stage_slot != stage_cur) {
+          if (open_seg >= 0) {
+            if (int rc = close_segment(L, stream)) return rc;
+          }
+          Segment seg;
+          seg.stage_slot = stage_cur;
+          seg.stage_off = pos;
+          g.segs.push_back(std::move(seg));
+          open_seg = (int)g.segs.size() - 1;
+        }
+        Segment& seg = g.segs[open_seg];
+        uint64_t take = std::min(remaining, space);
+        if (take < remaining) take = take / kPieceAlign * kPieceAlign;
+        KDesc kd;
+        if (int rc = make_kdesc(c, c.base, first, take, (uint64_t)(s.dev + pos), kd, err)) return fail(rc, "mo_pack: " + err);
+        L.add(kd);
+        seg.pieces.push_back(Piece{idx, first, take, pos - seg.stage_off});
+        s.used = pos + take;
+        first += take;
+        remaining -= take;
+        st.bytes_packed += take;
+      }
+    }
+    if (int rc = L.flush()) return hip_fail((hipError_t)rc, "pack kernel launch");
+    st.pack_launches += L.launches();
+    return 0;
+  }
+
+  int commit(hipStream_t stream, uint64_t* gid) {
+    *gid = kNone;
+    if (!open_group) return 0;
+    Launcher L(true, stream);
+    if (int rc = close_segment(L, stream)) return rc;
+    open_group->open = false;
+    *gid = open_group->id;
+    open_group = nullptr;
+    open_seg = -1;
+    return 0;
+  }
+
+  // ---- backward ----
+  Group* find(uint64_t gid) {
+    auto it = groups.find(gid);
+    return it == groups.end() ? nullptr : it->second.get();
+  }
+
+  bool resident(const Group& g, uint32_t si) const {
+    const Segment& seg = g.segs[si];
+    if (seg.restore_slot < 0) return false;
+    const RestoreSlot& r = restore[seg.restore_slot];
+    return r.group == g.id && r.seg == si && r.gen == seg.restore_gen;
+  }
+
+  // Choose a restore slot to fill with segment `si` of group `g`.
+  // for_prefetch: only take slots that are empty or already consumed (never waste a prefetch).
+  int pick_slot(const Group& g, uint32_t si, bool for_prefetch) {
+    int best = -1;
+    for (int k = 0; k < (int)restore.size(); ++k) {
+      const RestoreSlot& r = restore[k];
+      const bool empty = r.group == kNone;
+      const bool future_of_g = r.group == g.id && r.seg > si && !r.consumed;
+      if (future_of_g) continue;
+      if (for_prefetch && !empty && !r.consumed) continue;
+      if (best < 0) {
+        best = k;
+        continue;
+      }
+      const RestoreSlot& b = restore[best];
+      const bool bempty = b.group == kNone;
+      if (empty && !bempty) best = k;
+      else if (empty == bempty && r.tick < b.tick) best = k;
+    }
+    if (best < 0 && !for_prefetch) {
+      // Every slot holds a later, unconsumed segment of g: evict the furthest one.
+      uint32_t far = 0;
+      for (int k = 0; k < (int)restore.size(); ++k)
+        if (restore[k].seg >= far) {
+          far = restore[k].seg;
+          best = k;
+        }
+    }
+    return best;
+  }
+
+  int fetch(Group& g, uint32_t si, int k) {
+    Segment& seg = g.segs[si];
+    RestoreSlot& r = restore[k];
+    if (!seg.committed || !seg.host)
+      return fail(MO_E_STATE, "group " + std::to_string(g.id) + " segment " + std::to_string(si) +
+                                  " has no host copy (its D2H was never issued)");
+    if (r.consumed_recorded) MO_HIP(hipStreamWaitEvent(h2d, r.consumed_ev, 0));
+    if (seg.d2h_done) MO_HIP(hipStreamWaitEvent(h2d, seg.d2h_done, 0));
+    if (int rc = copy(r.dev, seg.host, seg.bytes, false, h2d)) return rc;
+    MO_HIP(hipEventRecord(r.ready, h2d));
+    if (!seg.h2d_done) {
+      if (int rc = new_event(&seg.h2d_done)) return rc;
+    }
+    MO_HIP(hipEventRecord(seg.h2d_done, h2d));
+    seg.h2d_issued = true;
+    r.group = g.id;
+    r.seg = si;
+    r.gen = ++gen_counter;
+    r.tick = ++tick;
+    r.consumed = false;
+    seg.restore_slot = k;
+    seg.restore_gen = r.gen;
+    st.h2d_copies++;
+    st.bytes_h2d += seg.bytes;
+    return 0;
+  }
+
+  int prefetch(uint64_t gid) {
+    process_pending(false);
+    Group* g = find(gid);
+    if (!g) return fail(MO_E_INVALID, "mo_prefetch: unknown group " + std::to_string(gid));
+    if (g->open) return 0;
+    for (uint32_t si = 0; si < g->segs.size(); ++si) {
+      if (resident(*g, si)) continue;
+      const int k = pick_slot(*g, si, true);
+      if (k < 0) break;
+      if (int rc = fetch(*g, si, k)) return rc;
+      g->segs[si].prefetched = true;
+      st.prefetch_issued++;
+    }
+    return 0;
+  }
+
+  int unpack(uint64_t gid, const uint64_t* dst, uint32_t n, hipStream_t stream) {
+    process_pending(false);
+    Group* g = find(gid);
+    if (!g) return fail(MO_E_INVALID, "mo_unpack: unknown group " + std::to_string(gid));
+    if (n != g->entries.size())
+      return fail(MO_E_INVALID, "mo_unpack: group " + std::to_string(gid) + " has " +
+                                    std::to_string(g->entries.size()) + " entries, got " + std::to_string(n));
+    if (g->open) {
+      uint64_t id;
+      if (int rc = commit(stream, &id)) return rc;
+    }
+    std::string err;
+    for (uint32_t si = 0; si < g->segs.size(); ++si) {
+      Segment& seg = g->segs[si];
+      bool any = false;
+      for (const Piece& p : seg.pieces) any = any || dst[p.entry] != 0;
+      if (!any) continue;
+      int k = seg.restore_slot;
+      if (resident(*g, si)) {
+        if (seg.prefetched) st.prefetch_hits++;
+      } else {
+        k = pick_slot(*g, si, false);
+        if (k < 0) return fail(MO_E_STATE, "mo_unpack: no restore slot available");
+        if (int rc = fetch(*g, si, k)) return rc;
+        st.restore_fetches++;
+      }
+      seg.prefetched = false;
+      RestoreSlot& r = restore[k];
+      MO_HIP(hipStreamWaitEvent(stream, r.ready, 0));
+      Launcher L(false, stream);
+      for (const Piece& p : seg.pieces) {
+        if (!dst[p.entry]) continue;
+        KDesc kd;
+        const Canon& c = g->entries[p.entry].canon;
+        if (dst[p.entry] % c.eb != 0) return fail(MO_E_INVALID, "mo_unpack: misaligned destination");
+        if (int rc = make_kdesc(c, dst[p.entry], p.first, p.nbytes, (uint64_t)(r.dev + p.seg_off), kd, err))
+          return fail(rc, "mo_unpack: " + err);
+        L.add(kd);
+        st.bytes_unpacked += p.nbytes;
+      }
+      if (int rc = L.flush()) return hip_fail((hipError_t)rc, "unpack kernel launch");
+      st.unpack_launches += L.launches();
+      MO_HIP(hipEventRecord(r.consumed_ev, stream));
+      r.consumed_recorded = true;
+      r.consumed = true;
+      r.tick = ++tick;
+    }
+    return 0;
+  }
+
+  int release(uint64_t gid) {
+    Group* g = find(gid);
+    if (!g) return fail(MO_E_INVALID, "mo_release: unknown group " + std::to_string(gid));
+    if (g == open_group) {
+      // Pack kernels were enqueued but no D2H: abandon the staging space.
+      open_group = nullptr;
+      open_seg = -1;
+    }
+    for (Segment& seg : g->segs) {
+      if (seg.host) {
+        pending.push_back(PendingFree{seg.host, seg.bytes, {seg.d2h_done, seg.h2d_done}});
+      } else {
+        recycle(seg.d2h_done);
+        recycle(seg.h2d_done);
+      }
+      if (seg.restore_slot >= 0) {
+        RestoreSlot& r = restore[seg.restore_slot];
+        if (r.group == g->id && r.gen == seg.restore_gen) {
+          r.group = kNone;
+          r.consumed = true;
+        }
+      }
+    }
+    groups.erase(gid);
+    process_pending(false);
+    return 0;
+  }
+
+  int synchronize() {
+    MO_HIP(hipStreamSynchronize(d2h));
+    MO_HIP(hipStreamSynchronize(h2d));
+    process_pending(true);
+    process_timings(true);
+    return 0;
+  }
+
+  void fill_stats(mo_stats* out) {
+    process_timings(false);
+    st.groups_live = groups.size();
+    uint64_t e = 0;
+    for (auto& kv : groups) e += kv.second->entries.size();
+    st.entries_live = e;
+    st.host_bytes_in_use = pool.in_use();
+    st.host_bytes_peak = pool.peak();
+    st.host_bytes_reserved = pool.reserved();
+    *out = st;
+  }
+
+  int init(int dev, const mo_config* c) {
+    device = dev;
+    if (c) cfg = *c;
+    if (!cfg.stage_slot_bytes) cfg.stage_slot_bytes = 64ull << 20;
+    if (!cfg.stage_slots) cfg.stage_slots = 4;
+    if (!cfg.restore_slots) cfg.restore_slots = 4;
+    if (!cfg.host_chunk_bytes) cfg.host_chunk_bytes = 1ull << 30;
+    if (!cfg.copy_kernel_blocks) cfg.copy_kernel_blocks = 64;
+    if (cfg.stage_slot_bytes < 2 * kMinPiece || cfg.stage_slot_bytes % kPieceAlign)
+      return fail(MO_E_INVALID, "stage_slot_bytes must be a multiple of 4096 and at least 2 MiB");
+    if (cfg.stage_slots < 2 || cfg.restore_slots < 2) return fail(MO_E_INVALID, "need at least 2 stage and 2 restore slots");
+    pool.configure(cfg.host_limit_bytes, cfg.host_chunk_bytes);
+    DeviceGuard guard(device);
+    MO_HIP(hipStreamCreateWithFlags(&d2h, hipStreamNonBlocking));
+    MO_HIP(hipStreamCreateWithFlags(&h2d, hipStreamNonBlocking));
+    MO_HIP(hipEventCreateWithFlags(&ev_tmp, hipEventDisableTiming));
+    stage.resize(cfg.stage_slots);
+    for (auto& s : stage) {
+      MO_HIP(hipMalloc(&s.dev, cfg.stage_slot_bytes));
+      MO_HIP(hipEventCreateWithFlags(&s.free_ev, hipEventDisableTiming));
+    }
+    restore.resize(cfg.restore_slots);
+    for (auto& r : restore) {
+      MO_HIP(hipMalloc(&r.dev, cfg.stage_slot_bytes));
+      MO_HIP(hipEventCreateWithFlags(&r.ready, hipEventDisableTiming));
+      MO_HIP(hipEventCreateWithFlags(&r.consumed_ev, hipEventDisableTiming));
+    }
+    return 0;
+  }
+
+  void teardown() {
+    DeviceGuard guard(device);
+    (void)hipDeviceSynchronize();
+    for (auto& kv : groups)
+      for (Segment& seg : kv.second->segs) {
+        if (seg.d2h_done) (void)hipEventDestroy(seg.d2h_done);
+        if (seg.h2d_done) (void)hipEventDestroy(seg.h2d_done);
+      }
+    groups.clear();
+    for (auto& p : pending)
+      for (hipEvent_t e : p.ev)
+        if (e) (void)hipEventDestroy(e);
+    pending.clear();
+    for (auto& t : timings) {
+      (void)hipEventDestroy(t.start);
+      (void)hipEventDestroy(t.end);
+    }
+    timings.clear();
+    for (hipEvent_t e : event_pool) (void)hipEventDestroy(e);
+    for (hipEvent_t e : timing_pool) (void)hipEventDestroy(e);
+    event_pool.clear();
+    timing_pool.clear();
+    for (auto& s : stage) {
+      if (s.dev) (void)hipFree(s.dev);
+      if (s.free_ev) (void)hipEventDestroy(s.free_ev);
+    }
+    for (auto& r : restore) {
+      if (r.dev) (void)hipFree(r.dev);
+      if (r.ready) (void)hipEventDestroy(r.ready);
+      if (r.consumed_ev) (void)hipEventDestroy(r.consumed_ev);
+    }
+    stage.clear();
+    restore.clear();
+    pool.release_all();
+    if (ev_tmp) (void)hipEventDestroy(ev_tmp);
+    if (d2h) (void)hipStreamDestroy(d2h);
+    if (h2d) (void)hipStreamDestroy(h2d);
+  }
+};
+
+// ------------------------------------------------------------------------------------------
+// kernels alone
+
+static int build_layout(const mo_tensor* ts, int n, std::vector<Canon>& cs, std::vector<uint64_t>& offs,
+                        uint64_t* total) {
+  cs.resize(n);
+  offs.resize(n);
+  std::string err;
+  uint64_t pos = 0;
+  for (int i = 0; i < n; ++i) {
+    if (int rc = canonicalize(ts[i], cs[i], err)) return fail(rc, "tensor " + std::to_string(i) + ": " + err);
+    pos = align_up(pos, kPayloadAlign);
+    offs[i] = pos;
+    pos += cs[i].nbytes;
+  }
+  *total = pos;
+  return 0;
+}
+
+static int run_copy(bool pack, const mo_tensor* ts, int n, uint64_t payload, const uint64_t* offsets,
+                    uint64_t stream) {
+  if (n < 0 || (n > 0 && !ts)) return fail(MO_E_INVALID, "bad tensor array");
+  std::vector<Canon> cs;
+  std::vector<uint64_t> offs;
+  uint64_t total = 0;
+  if (int rc = build_layout(ts, n, cs, offs, &total)) return rc;
+  if (offsets)
+    for (int i = 0; i < n; ++i) offs[i] = offsets[i];
+  Launcher L(pack, (hipStream_t)stream);
+  std::string err;
+  for (int i = 0; i < n; ++i) {
+    if (cs[i].nbytes == 0) continue;
+    KDesc kd;
+    if (int rc = make_kdesc(cs[i], cs[i].base, 0, cs[i].nbytes, payload + offs[i], kd, err))
+      return fail(rc, "tensor " + std::to_string(i) + ": " + err);
+    L.add(kd);
+  }
+  if (int rc = L.flush()) return hip_fail((hipError_t)rc, pack ? "pack kernel launch" : "unpack kernel launch");
+  return 0;
+}
+
+}  // namespace mo
+
+// ------------------------------------------------------------------------------------------
+// C ABI
+
+struct mo_engine {
+  mo::Engine e;
+};
+
+#define MO_GUARD_BEGIN try {
+#define MO_GUARD_END                                               \
+  }                                                                \
+  catch (const std::exception& ex) {                               \
+    return mo::fail(MO_E_STATE, std::string("internal error: ") + ex.what()); \
+  }                                                                \
+  catch (...) {                                                    \
+    return mo::fail(MO_E_STATE, "internal error");                 \
+  }
+
+#define MO_ENGINE_CALL(engine, expr)                         \
+  MO_GUARD_BEGIN                                             \
+  if (!(engine)) return mo::fail(MO_E_INVALID, "null engine"); \
+  std::lock_guard<std::mutex> lock((engine)->e.mu);          \
+  mo::DeviceGuard guard((engine)->e.device);                 \
+  return (expr);                                             \
+  MO_GUARD_END
+
+extern "C" {
+
+int mo_abi_version(void) { return MO_ABI_VERSION; }
+
+const char* mo_last_error(void) { return mo::g_error.c_str(); }
+
+int mo_payload_layout(const mo_tensor* tensors, int n, uint64_t* offsets, uint64_t* total_bytes) {
+  MO_GUARD_BEGIN
+  if (n < 0 || (n > 0 && (!tensors || !offsets)) || !total_bytes) return mo::fail(MO_E_INVALID, "bad arguments");
+  std::vector<mo::Canon> cs;
+  std::vector<uint64_t> offs;
+  if (int rc = mo::build_layout(tensors, n, cs, offs, total_bytes)) return rc;
+  for (int i = 0; i < n; ++i) offsets[i] = offs[i];
+  return 0;
+  MO_GUARD_END
+}
+
+int mo_gather(const mo_tensor* tensors, int n, uint64_t payload, const uint64_t* offsets, uint64_t stream) {
+  MO_GUARD_BEGIN
+  return mo::run_copy(true, tensors, n, payload, offsets, stream);
+  MO_GUARD_END
+}
+
+int mo_scatter(const mo_tensor* tensors, int n, uint64_t payload, const uint64_t* offsets, uint64_t stream) {
+  MO_GUARD_BEGIN
+  return mo::run_copy(false, tensors, n, payload, offsets, stream);
+  MO_GUARD_END
+}
+
+int mo_link_copy(uint64_t dst, uint64_t src, uint64_t bytes, int direction, uint32_t blocks, uint64_t stream) {
+  MO_GUARD_BEGIN
+  (void)direction;
+  int rc = mo::launch_link_copy((void*)dst, (const void*)src, bytes, blocks, (hipStream_t)stream);
+  if (rc) return mo::hip_fail((hipError_t)rc, "link copy kernel launch");
+  return 0;
+  MO_GUARD_END
+}
+
+int mo_create(int device, const mo_config* config, mo_engine** out) {
+  MO_GUARD_BEGIN
+  if (!out) return mo::fail(MO_E_INVALID, "null output");
+  *out = nullptr;
+  auto* h = new mo_engine();
+  int rc = h->e.init(device, config);
+  if (rc) {
+    const std::string msg = mo::g_error;
+    h->e.teardown();
+    delete h;
+    mo::g_error = msg;
+    return rc;
+  }
+  *out = h;
+  return 0;
+  MO_GUARD_END
+}
+
+int mo_destroy(mo_engine* engine) {
+  MO_GUARD_BEGIN
+  if (!engine) return 0;
+  {
+    std::lock_guard<std::mutex> lock(engine->e.mu);
+    engine->e.teardown();
+  }
+  delete engine;
+  return 0;
+  MO_GUARD_END
+}
+
+int mo_pack(mo_engine* engine, const mo_tensor* tensors, int n, uint64_t stream, mo_ref* refs) {
+  if (n < 0 || (n > 0 && (!tensors || !refs))) return mo::fail(MO_E_INVALID, "mo_pack: bad arguments");
+  MO_ENGINE_CALL(engine, engine->e.pack(tensors, n, (hipStream_t)stream, refs));
+}
+
+int mo_commit(mo_engine* engine, uint64_t stream, uint64_t* group) {
+  if (!group) return mo::fail(MO_E_INVALID, "mo_commit: null output");
+  MO_ENGINE_CALL(engine, engine->e.commit((hipStream_t)stream, group));
+}
+
+int mo_prefetch(mo_engine* engine, uint64_t group, uint64_t stream) {
+  (void)stream;
+  MO_ENGINE_CALL(engine, engine->e.prefetch(group));
+}
+
+int mo_unpack(mo_engine* engine, uint64_t group, const uint64_t* dst, uint32_t n, uint64_t stream) {
+  if (n > 0 && !dst) return mo::fail(MO_E_INVALID, "mo_unpack: null destination array");
+  MO_ENGINE_CALL(engine, engine->e.unpack(group, dst, n, (hipStream_t)stream));
+}
+
+int mo_release(mo_engine* engine, uint64_t group) { MO_ENGINE_CALL(engine, engine->e.release(group)); }
+
+int mo_group_info(mo_engine* engine, uint64_t group, uint32_t* entries, uint64_t* payload_bytes, int* d2h_complete) {
+  MO_GUARD_BEGIN
+  if (!engine) return mo::fail(MO_E_INVALID, "null engine");
+  std::lock_guard<std::mutex> lock(engine->e.mu);
+  mo::DeviceGuard guard(engine->e.device);
+  mo::Group* g = engine->e.find(group);
+  if (!g) return mo::fail(MO_E_INVALID, "mo_group_info: unknown group " + std::to_string(group));
+  if (entries) *entries = (uint32_t)g->entries.size();
+  if (payload_bytes) *payload_bytes = g->payload_bytes;
+  if (d2h_complete) {
+    int done = g->open ? 0 : 1;
+    for (auto& seg : g->segs)
+      if (seg.d2h_done && hipEventQuery(seg.d2h_done) != hipSuccess) done = 0;
+    *d2h_complete = done;
+  }
+  return 0;
+  MO_GUARD_END
+}
+
+int mo_synchronize(mo_engine* engine) { MO_ENGINE_CALL(engine, engine->e.synchronize()); }
+
+int mo_get_stats(mo_engine* engine, mo_stats* stats) {
+  if (!stats) return mo::fail(MO_E_INVALID, "null stats");
+  MO_ENGINE_CALL(engine, (engine->e.fill_stats(stats), 0));
+}
+
+int mo_reset_stats(mo_engine* engine) {
+  MO_ENGINE_CALL(engine, (engine->e.process_timings(false), engine->e.st = mo_stats{}, 0));
+}
+
+int mo_trim(mo_engine* engine) {
+  MO_ENGINE_CALL(engine, (engine->e.process_pending(false), engine->e.pool.trim(), 0));
+}
+
+}  // extern "C"

@@ -1,0 +1,295 @@
+// Pack / unpack kernels for gfx950 (MI355X).
+//
+// One launch moves up to kMaxDesc "pieces" (a byte range of one tensor's payload) between
+// strided tensor views and a dense staging payload. The payload is in storage order, so the
+// tensor side is walked in address order too; nothing is transposed. The work is pure data
+// movement and HBM-bound: every path aims at 128-bit coalesced loads and stores.
+//
+//   CONTIG  the piece is one contiguous run and 16-byte aligned: 64-bit-free address math,
+//           kUnroll x 16 B in flight per lane.
+//   RUNS    contiguous runs whose length, start and strides are multiples of 16 B: each
+//           16-byte chunk is located with fast division over the canonical dimensions.
+//   ELEM    anything else (misaligned bases, odd run lengths, element-strided innermost
+//           dimension): elements are gathered one by one into LDS and the tile is written
+//           to the payload with 128-bit stores (pack), or read from the payload with 128-bit
+//           loads into LDS and scattered from there (unpack).
+//
+// Grid: one 256-lane workgroup per 16 KiB tile of payload; tiles of all pieces of the
+// launch are numbered consecutively and a workgroup finds its piece with a scalar search.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "mo_internal.h"
+
+namespace mo {
+
+// ------------------------------------------------------------------------------------------
+// device helpers
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, uint32_t m, uint32_t s) {
+  const uint64_t t = __umulhi(m, n);
+  return (uint32_t)((t + n) >> s);
+}
+
+// Address offset (bytes, relative to the tensor base) of unit `u` of a piece's tensor side.
+// A unit is a 16-byte chunk (RUNS) or an element (ELEM). inner: units per innermost run.
+__device__ __forceinline__ uint64_t unit_offset(const KDesc& d, uint32_t u) {
+  uint32_t q = fdiv(u, d.inner.m, d.inner.s);
+  uint64_t off = (uint64_t)(u - q * d.inner.d) * d.inner_stride;
+  const uint32_t nouter = d.nouter;
+#pragma unroll
+  for (int k = 0; k < kMaxOuter; ++k) {
+    if (k < (int)nouter) {
+      const uint32_t q2 = fdiv(q, d.outer[k].m, d.outer[k].s);
+      off += (uint64_t)(q - q2 * d.outer[k].d) * d.ostride[k];
+      q = q2;
+    }
+  }
+  return off;
+}
+
+__device__ __forceinline__ void copy_elem(char* dst, const char* src, uint32_t eb) {
+  switch (eb) {
+    case 1: *(uint8_t*)dst = *(const uint8_t*)src; break;
+    case 2: *(uint16_t*)dst = *(const uint16_t*)src; break;
+    case 4: *(uint32_t*)dst = *(const uint32_t*)src; break;
+    case 8: *(uint64_t*)dst = *(const uint64_t*)src; break;
+    default: *(uint4*)dst = *(const uint4*)src; break;
+  }
+}
+
+__device__ __forceinline__ uint4 ld16(const char* p) { return *(const uint4*)p; }
+__device__ __forceinline__ void st16(char* p, uint4 v) { *(uint4*)p = v; }
+
+template <bool kPack>
+__global__ __launch_bounds__(kThreads) void copy_kernel(const LaunchArgs args) {
+  __shared__ uint4 lds[kTileBytes / 16];
+  const uint32_t tile = blockIdx.x;
+  uint32_t i = 0;
+  while (i + 1 < args.ndesc && args.d[i + 1].tile0 <= tile) ++i;
+  const KDesc& d = args.d[i];
+  const uint32_t tid = threadIdx.x;
+  const uint64_t tile_off = (uint64_t)(tile - d.tile0) * kTileBytes;  // bytes into the piece
+  const uint64_t left = d.nbytes - tile_off;
+  const uint32_t tile_bytes = left < kTileBytes ? (uint32_t)left : kTileBytes;
+  char* const payload = (char*)d.payload + tile_off;
+  char* const tensor = (char*)d.tensor;
+  const uint32_t eb = d.eb;
+
+  if (d.path == kPathContig) {
+    char* const t = tensor + d.first + tile_off;
+    const char* src = kPack ? t : payload;
+    char* dst = kPack ? payload : t;
+    if (tile_bytes == kTileBytes) {
+      uint4 v[kUnroll];
+#pragma unroll
+      for (int k = 0; k < kUnroll; ++k) v[k] = ld16(src + (size_t)(k * kThreads + tid) * 16);
+#pragma unroll
+      for (int k = 0; k < kUnroll; ++k) st16(dst + (size_t)(k * kThreads + tid) * 16, v[k]);
+    } else {
+      const uint32_t nvec = tile_bytes / 16;
+      for (uint32_t c = tid; c < nvec; c += kThreads) st16(dst + (size_t)c * 16, ld16(src + (size_t)c * 16));
+      for (uint32_t b = nvec * 16 + tid * eb; b < tile_bytes; b += kThreads * eb) copy_elem(dst + b, src + b, eb);
+    }
+    return;
+  }
+
+  if (d.path == kPathRuns) {
+    const uint32_t c0 = (uint32_t)(tile_off / 16);
+    const uint32_t nchunk = tile_bytes / 16;
+    const uint32_t first = (uint32_t)d.first;
+    uint4 v[kUnroll];
+    uint64_t toff[kUnroll];
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+      const uint32_t c = k * kThreads + tid;
+      if (c < nchunk) {
+        toff[k] = unit_offset(d, first + c0 + c);
+        v[k] = kPack ? ld16(tensor + toff[k]) : ld16(payload + (size_t)c * 16);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+      const uint32_t c = k * kThreads + tid;
+      if (c < nchunk) {
+        if (kPack) st16(payload + (size_t)c * 16, v[k]);
+        else st16(tensor + toff[k], v[k]);
+      }
+    }
+    return;
+  }
+
+  // ELEM: LDS-staged element gather / scatter.
+  char* const sbuf = (char*)lds;
+  const uint32_t nelem = tile_bytes / eb;
+  const uint32_t e0 = (uint32_t)d.first + (uint32_t)(tile_off / eb);
+  const uint32_t nvec = tile_bytes / 16;
+  if (kPack) {
+    for (uint32_t j = tid; j < nelem; j += kThreads)
+      copy_elem(sbuf + (size_t)j * eb, tensor + unit_offset(d, e0 + j), eb);
+    __syncthreads();
+    for (uint32_t c = tid; c < nvec; c += kThreads) st16(payload + (size_t)c * 16, lds[c]);
+    for (uint32_t b = nvec * 16 + tid * eb; b < tile_bytes; b += kThreads * eb) copy_elem(payload + b, sbuf + b, eb);
+  } else {
+    for (uint32_t c = tid; c < nvec; c += kThreads) lds[c] = ld16(payload + (size_t)c * 16);
+    for (uint32_t b = nvec * 16 + tid * eb; b < tile_bytes; b += kThreads * eb) copy_elem(sbuf + b, payload + b, eb);
+    __syncthreads();
+    for (uint32_t j = tid; j < nelem; j += kThreads)
+      copy_elem(tensor + unit_offset(d, e0 + j), sbuf + (size_t)j * eb, eb);
+  }
+}
+
+// Device <-> pinned-host copy through the shader engines instead of a DMA engine.
+// Each lane keeps kLinkUnroll 16-byte transfers in flight; the grid strides over the buffer.
+constexpr int kLinkUnroll = 8;
+
+__global__ __launch_bounds__(kThreads) void link_copy_kernel(char* __restrict__ dst, const char* __restrict__ src,
+                                                             uint64_t nbytes) {
+  const uint64_t nvec = nbytes / 16;
+  const uint64_t lanes = (uint64_t)gridDim.x * kThreads;
+  const uint64_t step = lanes * kLinkUnroll;
+  uint64_t base = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  for (; base + (kLinkUnroll - 1) * lanes < nvec; base += step) {
+    uint4 v[kLinkUnroll];
+#pragma unroll
+    for (int k = 0; k < kLinkUnroll; ++k) v[k] = ld16(src + (base + k * lanes) * 16);
+#pragma unroll
+    for (int k = 0; k < kLinkUnroll; ++k) st16(dst + (base + k * lanes) * 16, v[k]);
+  }
+  for (; base < nvec; base += lanes) st16(dst + base * 16, ld16(src + base * 16));
+  if (blockIdx.x == 0) {
+    for (uint64_t b = nvec * 16 + threadIdx.x; b < nbytes; b += kThreads) dst[b] = src[b];
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// host: piece -> kernel descriptor
+
+// Fill `kd` for the byte range [first, first + nbytes) of the payload of tensor `c`, whose
+// tensor side starts at `tensor_base` (a restored tensor has the same strides as the packed
+// one but another base). `payload` is the device address of the piece's payload bytes.
+int make_kdesc(const Canon& c, uint64_t tensor_base, uint64_t first, uint64_t nbytes, uint64_t payload,
+               KDesc& kd, std::string& err) {
+  kd = KDesc();
+  kd.tensor = tensor_base;
+  kd.payload = payload;
+  kd.nbytes = nbytes;
+  kd.eb = (uint8_t)c.eb;
+  if (payload % 16 != 0 || first % 16 != 0) {
+    err = "piece payload and offset must be 16-byte aligned";
+    return MO_E_INVALID;
+  }
+  // Canonical dims, innermost last. Treat a unit-stride innermost dim as a contiguous run.
+  const int nd = c.nd;
+  const bool inner_contig = nd == 0 || (uint64_t)c.stride[nd - 1] == c.eb;
+  const uint64_t run_bytes = nd == 0 ? c.eb : (inner_contig ? (uint64_t)c.size[nd - 1] * c.eb : c.eb);
+  const int nouter = inner_contig ? (nd > 0 ? nd - 1 : 0) : nd;  // dims outside the run
+  if (nouter == 0 && tensor_base % 16 == 0) {
+    kd.path = kPathContig;
+    kd.first = first;
+    return 0;
+  }
+  bool runs16 = run_bytes % 16 == 0 && tensor_base % 16 == 0;
+  for (int k = 0; k < nouter && runs16; ++k) runs16 = c.stride[k] % 16 == 0;
+  if (runs16) {
+    if (nouter > kMaxOuter) {
+      err = "too many canonical dimensions for one descriptor";
+      return MO_E_STATE;
+    }
+    const uint64_t run_chunks = run_bytes / 16;
+    const uint64_t total_chunks = c.nbytes / 16;
+    if (run_chunks >= (1ull << 32) || total_chunks >= (1ull << 32)) {
+      err = "tensor too large for 32-bit chunk indexing";
+      return MO_E_INVALID;
+    }
+    kd.path = kPathRuns;
+    kd.first = first / 16;
+    const FastDiv f = make_fastdiv((uint32_t)run_chunks);
+    kd.inner = KFastDiv{f.d, f.m, f.s};
+    kd.inner_stride = 16;
+    kd.nouter = (uint8_t)nouter;
+    for (int k = 0; k < nouter; ++k) {  // kernel order: innermost outer dim first
+      const int dim = nouter - 1 - k;
+      const FastDiv g = make_fastdiv((uint32_t)c.size[dim]);
+      kd.outer[k] = KFastDiv{g.d, g.m, g.s};
+      kd.ostride[k] = (uint64_t)c.stride[dim];
+    }
+    return 0;
+  }
+  // ELEM path: units are elements. Innermost canonical dim is the "inner" run.
+  if (c.numel >= (1ull << 32)) {
+    err = "tensor too large for 32-bit element indexing";
+    return MO_E_INVALID;
+  }
+  const int eouter = nd > 0 ? nd - 1 : 0;
+  if (eouter > kMaxOuter) {
+    err = "too many canonical dimensions for one descriptor";
+    return MO_E_STATE;
+  }
+  kd.path = kPathElem;
+  kd.first = first / c.eb;
+  if (nd == 0) {
+    kd.inner = KFastDiv{1, 1, 0};
+    kd.inner_stride = c.eb;
+    kd.nouter = 0;
+    return 0;
+  }
+  const FastDiv f = make_fastdiv((uint32_t)c.size[nd - 1]);
+  kd.inner = KFastDiv{f.d, f.m, f.s};
+  kd.inner_stride = (uint64_t)c.stride[nd - 1];
+  kd.nouter = (uint8_t)eouter;
+  for (int k = 0; k < eouter; ++k) {
+    const int dim = eouter - 1 - k;
+    const FastDiv g = make_fastdiv((uint32_t)c.size[dim]);
+    kd.outer[k] = KFastDiv{g.d, g.m, g.s};
+    kd.ostride[k] = (uint64_t)c.stride[dim];
+  }
+  return 0;
+}
+
+// ------------------------------------------------------------------------------------------
+// host: batched launches
+
+void Launcher::add(const KDesc& kd) {
+  if (kd.nbytes == 0) return;
+  if (args_.ndesc == kMaxDesc) flush();
+  KDesc& slot = args_.d[args_.ndesc];
+  slot = kd;
+  slot.tile0 = tiles_;
+  const uint64_t t = (kd.nbytes + kTileBytes - 1) / kTileBytes;
+  tiles_ += (uint32_t)t;
+  bytes_ += kd.nbytes;
+  args_.ndesc++;
+  if (tiles_ > kMaxTilesPerLaunch) flush();
+}
+
+int Launcher::flush() {
+  if (args_.ndesc == 0) return 0;
+  if (status_ == 0) {
+    if (pack_) {
+      hipLaunchKernelGGL(copy_kernel<true>, dim3(tiles_), dim3(kThreads), 0, stream_, args_);
+    } else {
+      hipLaunchKernelGGL(copy_kernel<false>, dim3(tiles_), dim3(kThreads), 0, stream_, args_);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) status_ = (int)e;
+    launches_++;
+  }
+  args_.ndesc = 0;
+  tiles_ = 0;
+  return status_;
+}
+
+int launch_link_copy(void* dst, const void* src, uint64_t bytes, uint32_t blocks, hipStream_t stream) {
+  if (bytes == 0) return 0;
+  if (blocks == 0) blocks = 64;
+  const uint64_t max_blocks = (bytes / 16 + kThreads - 1) / kThreads;
+  if (blocks > max_blocks) blocks = (uint32_t)(max_blocks ? max_blocks : 1);
+  hipLaunchKernelGGL(link_copy_kernel, dim3(blocks), dim3(kThreads), 0, stream, (char*)dst, (const char*)src, bytes);
+  return (int)hipGetLastError();
+}
+
+}  // namespace mo

@@ -1,0 +1,180 @@
+"""ctypes binding of ``include/moss_offload.h``.
+
+The library is loaded lazily and only after ``torch`` is imported, so it binds to the HIP
+runtime torch already mapped (one runtime per process; torch's streams are valid handles for
+the engine). There is no fallback: if the library is missing, every offload entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must be imported before the library, see module docstring)
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
+
+MO_ABI_VERSION = 1
+MO_MAX_DIMS = 8
+
+MO_E_INVALID = 1001
+MO_E_LAYOUT = 1002
+MO_E_HOST_OOM = 1003
+MO_E_STATE = 1004
+
+MO_FLAG_TIMING = 0x1
+MO_FLAG_KERNEL_COPY = 0x2
+
+NO_GROUP = (1 << 64) - 1
+
+
+class MoTensor(ctypes.Structure):
+    _fields_ = [
+        ("ptr", ctypes.c_uint64),
+        ("elem_bytes", ctypes.c_uint32),
+        ("ndim", ctypes.c_uint32),
+        ("size", ctypes.c_int64 * MO_MAX_DIMS),
+        ("stride", ctypes.c_int64 * MO_MAX_DIMS),
+    ]
+
+
+class MoConfig(ctypes.Structure):
+    _fields_ = [
+        ("stage_slot_bytes", ctypes.c_uint64),
+        ("stage_slots", ctypes.c_uint32),
+        ("restore_slots", ctypes.c_uint32),
+        ("host_limit_bytes", ctypes.c_uint64),
+        ("host_chunk_bytes", ctypes.c_uint64),
+        ("flags", ctypes.c_uint32),
+        ("copy_kernel_blocks", ctypes.c_uint32),
+    ]
+
+
+class MoRef(ctypes.Structure):
+    _fields_ = [("group", ctypes.c_uint64), ("entry", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+class MoStats(ctypes.Structure):
+    _fields_ = [
+        (name, ctypes.c_uint64)
+        for name in (
+            "groups_created",
+            "groups_live",
+            "entries_live",
+            "bytes_packed",
+            "bytes_unpacked",
+            "bytes_d2h",
+            "bytes_h2d",
+            "pack_launches",
+            "unpack_launches",
+            "d2h_copies",
+            "h2d_copies",
+            "host_bytes_in_use",
+            "host_bytes_peak",
+            "host_bytes_reserved",
+            "stage_slot_waits",
+            "stage_slot_busy",
+            "prefetch_issued",
+            "prefetch_hits",
+            "restore_fetches",
+        )
+    ] + [
+        ("d2h_ms", ctypes.c_double),
+        ("h2d_ms", ctypes.c_double),
+        ("timed_d2h_bytes", ctypes.c_uint64),
+        ("timed_h2d_bytes", ctypes.c_uint64),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class EngineError(RuntimeError):
+    """A non-zero status from the engine library, with its message."""
+
+    def __init__(self, call: str, status: int, message: str) -> None:
+        super().__init__(f"{call} failed with status {status}: {message}")
+        self.status = status
+
+
+_P = ctypes.POINTER
+_u64 = ctypes.c_uint64
+
+# name -> (restype, argtypes); mirrors include/moss_offload.h
+SIGNATURES: dict[str, tuple] = {
+    "mo_abi_version": (ctypes.c_int, []),
+    "mo_last_error": (ctypes.c_char_p, []),
+    "mo_payload_layout": (ctypes.c_int, [_P(MoTensor), ctypes.c_int, _P(_u64), _P(_u64)]),
+    "mo_gather": (ctypes.c_int, [_P(MoTensor), ctypes.c_int, _u64, _P(_u64), _u64]),
+    "mo_scatter": (ctypes.c_int, [_P(MoTensor), ctypes.c_int, _u64, _P(_u64), _u64]),
+    "mo_link_copy": (ctypes.c_int, [_u64, _u64, _u64, ctypes.c_int, ctypes.c_uint32, _u64]),
+    "mo_create": (ctypes.c_int, [ctypes.c_int, _P(MoConfig), _P(ctypes.c_void_p)]),
+    "mo_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "mo_pack": (ctypes.c_int, [ctypes.c_void_p, _P(MoTensor), ctypes.c_int, _u64, _P(MoRef)]),
+    "mo_commit": (ctypes.c_int, [ctypes.c_void_p, _u64, _P(_u64)]),
+    "mo_prefetch": (ctypes.c_int, [ctypes.c_void_p, _u64, _u64]),
+    "mo_unpack": (ctypes.c_int, [ctypes.c_void_p, _u64, _P(_u64), ctypes.c_uint32, _u64]),
+    "mo_release": (ctypes.c_int, [ctypes.c_void_p, _u64]),
+    "mo_group_info": (
+        ctypes.c_int,
+        [ctypes.c_void_p, _u64, _P(ctypes.c_uint32), _P(_u64), _P(ctypes.c_int)],
+    ),
+    "mo_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
+    "mo_get_stats": (ctypes.c_int, [ctypes.c_void_p, _P(MoStats)]),
+    "mo_reset_stats": (ctypes.c_int, [ctypes.c_void_p]),
+    "mo_trim": (ctypes.c_int, [ctypes.c_void_p]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load(path: Path | str | None = None) -> ctypes.CDLL:
+    """Load (once) and return the engine library; raise if it is not built."""
+
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        lib_path = Path(path) if path is not None else LIB_PATH
+        if not lib_path.exists():
+            raise RuntimeError(
+                f"moss_offload native library not found at {lib_path}; build it with "
+                "`python -m moss_offload.build` (hipcc, gfx950). There is no fallback path."
+            )
+        lib = ctypes.CDLL(str(lib_path))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = lib.mo_abi_version()
+        if version != MO_ABI_VERSION:
+            raise RuntimeError(f"moss_offload ABI {version} != expected {MO_ABI_VERSION}; rebuild the library")
+        _lib = lib
+        return lib
+
+
+def check(call: str, status: int) -> None:
+    """Raise :class:`EngineError` for a non-zero status."""
+
+    if status != 0:
+        message = _lib.mo_last_error().decode(errors="replace") if _lib is not None else ""
+        raise EngineError(call, status, message)
+
+
+def describe(tensor: torch.Tensor, out: MoTensor, ptr: int | None = None) -> MoTensor:
+    """Fill ``out`` with the view ``tensor`` (address, element size, sizes, strides)."""
+
+    shape = tensor.shape
+    stride = tensor.stride()
+    ndim = len(shape)
+    if ndim > MO_MAX_DIMS:
+        raise ValueError(f"tensor has {ndim} dims; the engine supports at most {MO_MAX_DIMS}")
+    out.ptr = tensor.data_ptr() if ptr is None else ptr
+    out.elem_bytes = tensor.element_size()
+    out.ndim = ndim
+    for i in range(ndim):
+        out.size[i] = shape[i]
+        out.stride[i] = stride[i]
+    return out

@@ -1,0 +1,245 @@
+"""Drop-in replacement for MOSS-Image's ``training/activation_offload.py``.
+
+Same public surface and decisions as the reference:
+
+- ``activation_cpu_offload(model, enabled, device)`` (reference :80-149) returns
+  ``nullcontext()`` unless ``enabled``, ``device.type == "cuda"`` (true for HIP devices on
+  PyTorch-ROCm) and grad mode is on (:92-93); otherwise a context that installs a
+  saved-tensor ``pack``/``unpack`` hook pair for the model's forward.
+- Parameter-, buffer- and streamer-staging-backed saves stay resident (:95-118), and so do
+  layouts the reference cannot offload (:119-121, :32-61).
+- ``_offload_view`` (:32-61), ``_restore_layout`` (:64-77) and ``_storage_key`` (:27-29) keep
+  their signatures and results.
+
+What changes is the mechanism behind ``pack``/``unpack``: instead of one pinned tensor, one
+``copy_`` on the compute stream and one event per save, saves are gathered by a HIP pack
+kernel into a device staging ring and leave in one DMA per block segment on a dedicated copy
+stream; backward restores whole blocks with one H2D per segment, prefetched one block ahead,
+and a HIP unpack kernel scatters them into freshly allocated tensors with the original
+strides. Block boundaries come from forward hooks on ``model.layers``.
+"""
+
+from __future__ import annotations
+
+from contextlib import nullcontext
+from typing import ContextManager
+
+import torch
+from torch import nn
+
+from . import _native
+from .engine import OffloadEngine, get_engine
+
+try:  # a weak reference to a storage that does not keep it alive
+    from torch.multiprocessing.reductions import StorageWeakRef
+except ImportError:  # pragma: no cover
+    StorageWeakRef = None
+
+
+def _storage_key(tensor: torch.Tensor) -> tuple[str, int | None, int]:
+    """Identity of a tensor's storage: ``(device type, device index, storage data_ptr)``.
+
+    Restates ``training/activation_offload.py:27-29``.
+    """
+
+    device = tensor.device
+    return device.type, device.index, tensor.untyped_storage().data_ptr()
+
+
+def _offload_view(tensor: torch.Tensor) -> tuple[torch.Tensor, tuple[int, ...]] | None:
+    """Return ``(source, payload_shape)`` for a view that can be copied densely, else None.
+
+    Restates ``training/activation_offload.py:32-61``: a negative stride keeps the tensor
+    resident; expanded (stride-0, size > 1) dimensions are narrowed to one element; the
+    remaining dimensions of size > 1, taken in increasing stride order, must each start at or
+    beyond the extent covered by the smaller ones, or the layout overlaps and stays resident.
+    """
+
+    sizes = tuple(tensor.shape)
+    strides = tuple(tensor.stride())
+    payload_shape = list(sizes)
+    source = tensor
+    for dim in range(len(sizes)):
+        stride = strides[dim]
+        if stride < 0:
+            return None
+        if stride == 0 and sizes[dim] > 1:
+            source = source.narrow(dim, 0, 1)
+            payload_shape[dim] = 1
+    extent = 1
+    for stride, size in sorted(
+        (strides[dim], payload_shape[dim]) for dim in range(len(sizes)) if payload_shape[dim] > 1
+    ):
+        if stride < extent:
+            return None
+        extent += (size - 1) * stride
+    return source, tuple(payload_shape)
+
+
+def _restore_layout(
+    payload: torch.Tensor,
+    device: torch.device,
+    shape: tuple[int, ...],
+    stride: tuple[int, ...],
+    payload_shape: tuple[int, ...],
+    *,
+    non_blocking: bool,
+) -> torch.Tensor:
+    """Copy a dense payload into a tensor with the original (padded/expanded) layout.
+
+    Restates ``training/activation_offload.py:64-77``: allocate ``empty_strided(payload_shape,
+    stride)``, fill it from the dense, logically ordered ``payload`` with ``Tensor.copy_`` and
+    return the ``as_strided(shape, stride)`` view. This is the reference's utility, kept for
+    callers and tests that import it; the offload hooks do not use it (their payloads are in
+    storage order and are restored by the engine's unpack kernel).
+    """
+
+    restored = torch.empty_strided(payload_shape, stride, dtype=payload.dtype, device=device)
+    restored.copy_(payload, non_blocking=non_blocking)
+    return restored.as_strided(shape, stride)
+
+
+class _OffloadedTensor:
+    """Handle returned by ``pack`` for an offloaded save (reference :17-24).
+
+    The reference's handle owns a pinned CPU tensor and a CUDA event. This one owns one
+    reference to ``(group, entry)`` in the device engine, which holds the payload in pinned
+    host memory; dropping the handle (the autograd graph freeing the saved variable) drops
+    the reference. ``shape``, ``stride`` and ``payload_shape`` mean what they mean in the
+    reference. ``group is None`` marks a save with no elements.
+    """
+
+    __slots__ = ("engine", "group", "entry", "device", "dtype", "shape", "stride", "payload_shape")
+
+    def __init__(self, engine, group, entry, device, dtype, shape, stride, payload_shape):
+        self.engine = engine
+        self.group = group
+        self.entry = entry
+        self.device = device
+        self.dtype = dtype
+        self.shape = shape
+        self.stride = stride
+        self.payload_shape = payload_shape
+
+    def __del__(self):
+        engine = self.engine
+        if engine is not None and self.group is not None:
+            try:
+                engine.drop(self.group, self.entry)
+            except Exception:  # interpreter shutdown or engine already closed
+                pass
+
+
+class _ActivationOffload:
+    """The context returned for an enabled offload: hooks + block boundaries + dedupe."""
+
+    def __init__(self, model: nn.Module, device: torch.device) -> None:
+        self.model = model
+        self.device = device
+        self.engine: OffloadEngine = get_engine(device)
+        # Reference :95-99: storages of CUDA parameters and buffers stay resident.
+        self.resident_storages = {
+            _storage_key(tensor)
+            for tensor in (*model.parameters(), *model.buffers())
+            if tensor.device.type == "cuda" and tensor.untyped_storage().nbytes()
+        }
+        self.dedupe = self.engine.config.dedupe and StorageWeakRef is not None
+        self._seen: dict[tuple, tuple] = {}
+        self._hooks = torch.autograd.graph.saved_tensors_hooks(self.pack, self.unpack)
+        self._block_handles: list = []
+
+    # ------------------------------------------------------------------ context
+    def __enter__(self):
+        layers = getattr(self.model, "layers", None)
+        if isinstance(layers, (nn.ModuleList, nn.Sequential)):
+            for layer in layers:
+                self._block_handles.append(layer.register_forward_pre_hook(self._boundary))
+                self._block_handles.append(layer.register_forward_hook(self._boundary_post))
+        self._hooks.__enter__()
+        return self
+
+    def __exit__(self, *exc):
+        try:
+            self._hooks.__exit__(*exc)
+        finally:
+            for handle in self._block_handles:
+                handle.remove()
+            self._block_handles.clear()
+            self._seen.clear()
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        last = self.engine.commit(stream)
+        if last is not None and self.engine.config.prefetch and exc[0] is None:
+            # Backward starts with the last group: start bringing it back now.
+            self.engine.prefetch(last, stream)
+        return False
+
+    def _boundary(self, module, args):
+        self.engine.commit(torch.cuda.current_stream(self.device).cuda_stream)
+
+    def _boundary_post(self, module, args, output):
+        self.engine.commit(torch.cuda.current_stream(self.device).cuda_stream)
+
+    # ------------------------------------------------------------------ hooks
+    def is_weight_backed(self, tensor: torch.Tensor) -> bool:
+        """Reference :101-114: parameters, buffers and the streamers' staging buffers."""
+
+        key = _storage_key(tensor)
+        if key in self.resident_storages:
+            return True
+        manager = getattr(self.model, "block_swap_manager", None)
+        owned = getattr(manager, "owned_cuda_buffers", None)
+        if not callable(owned):
+            return False
+        return any(buffer.device.type == "cuda" and _storage_key(buffer) == key for buffer in owned())
+
+    def pack(self, tensor: torch.Tensor):
+        if tensor.device.type != "cuda" or tensor.layout != torch.strided or self.is_weight_backed(tensor):
+            return tensor
+        view = _offload_view(tensor)
+        if view is None or tensor.dim() > _native.MO_MAX_DIMS:
+            return tensor
+        source, payload_shape = view
+        shape, stride = tuple(tensor.shape), tuple(tensor.stride())
+        device = tensor.device
+        if source.numel() == 0:
+            return _OffloadedTensor(None, None, 0, device, tensor.dtype, shape, stride, payload_shape)
+        key = None
+        if self.dedupe:
+            key = (tensor.untyped_storage().data_ptr(), source.storage_offset(), payload_shape, stride, tensor.dtype)
+            hit = self._seen.get(key)
+            if hit is not None:
+                ref, version, gid, idx = hit
+                if not ref.expired() and version == tensor._version and self.engine.acquire(gid, idx):
+                    return _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
+        stream = torch.cuda.current_stream(device).cuda_stream
+        gid, idx = self.engine.pack(source, stream)
+        if key is not None:
+            self._seen[key] = (StorageWeakRef(tensor.untyped_storage()), tensor._version, gid, idx)
+        return _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
+
+    def unpack(self, saved):
+        if isinstance(saved, torch.Tensor):
+            return saved
+        if saved.group is None:
+            restored = torch.empty_strided(saved.payload_shape, saved.stride, dtype=saved.dtype, device=saved.device)
+        else:
+            stream = torch.cuda.current_stream(saved.device).cuda_stream
+            restored = saved.engine.restore(saved.group, saved.entry, stream)
+        return restored.as_strided(saved.shape, saved.stride)
+
+
+def activation_cpu_offload(
+    model: nn.Module,
+    enabled: bool,
+    device: torch.device,
+) -> ContextManager[object]:
+    """Offload tensors saved by autograd to pinned host memory.
+
+    Reference ``training/activation_offload.py:80-149``. Parameter-backed tensors remain
+    resident. HIP events order the asynchronous device-to-host copies before backward
+    restores a tensor.
+    """
+
+    if not enabled or device.type != "cuda" or not torch.is_grad_enabled():
+        return nullcontext()
+    return _ActivationOffload(model, device)

@@ -1,0 +1,304 @@
+"""Host-side policy around the native engine: groups, handle lifetimes, restore and prefetch.
+
+The native engine (``libmoss_offload.so``) owns the device staging ring, pinned host pool,
+copy streams, events and kernels. This layer decides *when* to call it:
+
+- one **group** per block of saves (the context commits at every block boundary),
+- one **handle** per saved tensor; a group is released when its last handle dies, which is
+  when the autograd graph drops the saved variable (backward, ``retain_graph`` or not, or a
+  graph that is never backpropagated),
+- **restore**: the first unpack of a group restores every live entry of that group in one
+  unpack launch and keeps them until asked for (one H2D + one scatter per segment instead of
+  one per tensor),
+- **prefetch**: after a group is restored, the next group backward will need (the youngest
+  older live group: saves are consumed last-in first-out) is fetched on the H2D stream while
+  the current block computes.
+"""
+
+from __future__ import annotations
+
+import bisect
+import ctypes
+import threading
+from dataclasses import dataclass, fields
+
+import torch
+
+from . import _native
+
+
+@dataclass
+class EngineConfig:
+    """Sizes and switches of one device engine (see ``mo_config`` in moss_offload.h)."""
+
+    stage_slot_bytes: int = 64 << 20
+    stage_slots: int = 4
+    restore_slots: int = 4
+    host_limit_bytes: int = 0
+    host_chunk_bytes: int = 1 << 30
+    timing: bool = False
+    kernel_copy: bool = False
+    copy_kernel_blocks: int = 64
+    prefetch: bool = True
+    dedupe: bool = True
+
+    def native(self) -> _native.MoConfig:
+        cfg = _native.MoConfig()
+        cfg.stage_slot_bytes = self.stage_slot_bytes
+        cfg.stage_slots = self.stage_slots
+        cfg.restore_slots = self.restore_slots
+        cfg.host_limit_bytes = self.host_limit_bytes
+        cfg.host_chunk_bytes = self.host_chunk_bytes
+        cfg.flags = (_native.MO_FLAG_TIMING if self.timing else 0) | (
+            _native.MO_FLAG_KERNEL_COPY if self.kernel_copy else 0
+        )
+        cfg.copy_kernel_blocks = self.copy_kernel_blocks
+        return cfg
+
+
+class _EntryState:
+    __slots__ = ("refs", "dtype", "payload_shape", "stride", "nbytes", "restored", "restored_version")
+
+    def __init__(self, dtype, payload_shape, stride, nbytes):
+        self.refs = 0
+        self.dtype = dtype
+        self.payload_shape = payload_shape
+        self.stride = stride
+        self.nbytes = nbytes
+        self.restored: torch.Tensor | None = None
+        self.restored_version = 0
+
+
+class _GroupState:
+    __slots__ = ("gid", "entries", "live", "committed")
+
+    def __init__(self, gid: int):
+        self.gid = gid
+        self.entries: list[_EntryState] = []
+        self.live = 0
+        self.committed = False
+
+
+class OffloadEngine:
+    """One native engine bound to one device."""
+
+    def __init__(self, device: torch.device, config: EngineConfig | None = None) -> None:
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("the offload engine runs on a HIP device")
+        self.index = self.device.index if self.device.index is not None else torch.cuda.current_device()
+        self.config = config or EngineConfig()
+        self._lib = _native.load()
+        handle = ctypes.c_void_p()
+        cfg = self.config.native()
+        _native.check("mo_create", self._lib.mo_create(self.index, ctypes.byref(cfg), ctypes.byref(handle)))
+        self._handle = handle
+        self._lock = threading.RLock()
+        self._groups: dict[int, _GroupState] = {}
+        self._live: list[int] = []  # live group ids, ascending (creation order)
+        self._desc = (_native.MoTensor * 1)()
+        self._ref = (_native.MoRef * 1)()
+        self._gid_out = ctypes.c_uint64()
+
+    # ------------------------------------------------------------------ forward
+    def pack(self, source: torch.Tensor, stream: int) -> tuple[int, int]:
+        """Gather ``source`` into the open group; return ``(group, entry)`` with one reference."""
+
+        with self._lock:
+            _native.describe(source, self._desc[0])
+            _native.check("mo_pack", self._lib.mo_pack(self._handle, self._desc, 1, stream, self._ref))
+            gid, idx = int(self._ref[0].group), int(self._ref[0].entry)
+            group = self._groups.get(gid)
+            if group is None:
+                group = self._groups[gid] = _GroupState(gid)
+                self._live.append(gid)
+            if idx != len(group.entries):
+                raise RuntimeError(f"engine entry index {idx} out of sync with group {gid}")
+            entry = _EntryState(source.dtype, tuple(source.shape), tuple(source.stride()),
+                                source.numel() * source.element_size())
+            entry.refs = 1
+            group.entries.append(entry)
+            group.live += 1
+            return gid, idx
+
+    def commit(self, stream: int) -> int | None:
+        """Close the open group (D2H starts); return its id or None."""
+
+        with self._lock:
+            _native.check("mo_commit", self._lib.mo_commit(self._handle, stream, ctypes.byref(self._gid_out)))
+            gid = int(self._gid_out.value)
+            if gid == _native.NO_GROUP:
+                return None
+            group = self._groups.get(gid)
+            if group is not None:
+                group.committed = True
+            return gid
+
+    def acquire(self, gid: int, idx: int) -> bool:
+        """Add a reference to a live entry (a deduplicated save). False if it is gone."""
+
+        with self._lock:
+            group = self._groups.get(gid)
+            if group is None or idx >= len(group.entries) or group.entries[idx].refs <= 0:
+                return False
+            group.entries[idx].refs += 1
+            group.live += 1
+            return True
+
+    def drop(self, gid: int, idx: int) -> None:
+        """Remove one reference; release the group when none is left."""
+
+        with self._lock:
+            group = self._groups.get(gid)
+            if group is None:
+                return
+            entry = group.entries[idx]
+            entry.refs -= 1
+            group.live -= 1
+            if entry.refs <= 0:
+                entry.restored = None
+            if group.live <= 0:
+                del self._groups[gid]
+                pos = bisect.bisect_left(self._live, gid)
+                if pos < len(self._live) and self._live[pos] == gid:
+                    del self._live[pos]
+                _native.check("mo_release", self._lib.mo_release(self._handle, gid))
+
+    # ------------------------------------------------------------------ backward
+    def restore(self, gid: int, idx: int, stream: int) -> torch.Tensor:
+        """Return entry ``idx`` of group ``gid`` as a fresh device tensor of its packed layout."""
+
+        with self._lock:
+            group = self._groups.get(gid)
+            if group is None:
+                raise RuntimeError(f"offloaded group {gid} was already released")
+            entry = group.entries[idx]
+            cached = self._take_cached(entry)
+            if cached is not None:
+                return cached
+            n = len(group.entries)
+            dst = (ctypes.c_uint64 * n)()
+            for j, other in enumerate(group.entries):
+                if j != idx and (other.refs <= 0 or other.restored is not None):
+                    continue
+                tensor = torch.empty_strided(other.payload_shape, other.stride, dtype=other.dtype, device=self.device)
+                other.restored = tensor
+                other.restored_version = tensor._version
+                if other.nbytes:
+                    dst[j] = tensor.data_ptr()
+            _native.check("mo_unpack", self._lib.mo_unpack(self._handle, gid, dst, n, stream))
+            if self.config.prefetch:
+                nxt = self._predict_next(gid)
+                if nxt is not None:
+                    _native.check("mo_prefetch", self._lib.mo_prefetch(self._handle, nxt, stream))
+            return self._take_cached(entry)
+
+    def prefetch(self, gid: int, stream: int) -> None:
+        with self._lock:
+            if gid in self._groups:
+                _native.check("mo_prefetch", self._lib.mo_prefetch(self._handle, gid, stream))
+
+    @staticmethod
+    def _take_cached(entry: _EntryState) -> torch.Tensor | None:
+        tensor = entry.restored
+        if tensor is None:
+            return None
+        if tensor._version != entry.restored_version:
+            # Someone modified the shared restored copy in place: restore afresh.
+            entry.restored = None
+            return None
+        if entry.refs <= 1:
+            entry.restored = None
+        return tensor
+
+    def _predict_next(self, gid: int) -> int | None:
+        """The group backward needs next: the youngest live group older than ``gid``."""
+
+        pos = bisect.bisect_left(self._live, gid) - 1
+        while pos >= 0:
+            cand = self._groups.get(self._live[pos])
+            if cand is not None and cand.committed and any(
+                e.refs > 0 and e.restored is None and e.nbytes for e in cand.entries
+            ):
+                return cand.gid
+            pos -= 1
+        return None
+
+    # ------------------------------------------------------------------ housekeeping
+    def synchronize(self) -> None:
+        with self._lock:
+            _native.check("mo_synchronize", self._lib.mo_synchronize(self._handle))
+
+    def stats(self) -> dict:
+        with self._lock:
+            out = _native.MoStats()
+            _native.check("mo_get_stats", self._lib.mo_get_stats(self._handle, ctypes.byref(out)))
+            result = out.as_dict()
+            result["py_groups_live"] = len(self._groups)
+            return result
+
+    def reset_stats(self) -> None:
+        with self._lock:
+            _native.check("mo_reset_stats", self._lib.mo_reset_stats(self._handle))
+
+    def trim(self) -> None:
+        with self._lock:
+            _native.check("mo_trim", self._lib.mo_trim(self._handle))
+
+    def live_groups(self) -> int:
+        with self._lock:
+            return len(self._groups)
+
+    def close(self) -> None:
+        with self._lock:
+            if self._handle:
+                _native.check("mo_destroy", self._lib.mo_destroy(self._handle))
+                self._handle = ctypes.c_void_p()
+                self._groups.clear()
+                self._live.clear()
+
+
+_ENGINES: dict[int, OffloadEngine] = {}
+_ENGINES_LOCK = threading.Lock()
+_DEFAULT_CONFIG = EngineConfig()
+
+
+def configure(**overrides) -> EngineConfig:
+    """Set the configuration used by engines created from now on; return it.
+
+    Existing engines keep theirs (see :func:`reset_engines`).
+    """
+
+    global _DEFAULT_CONFIG
+    names = {f.name for f in fields(EngineConfig)}
+    unknown = set(overrides) - names
+    if unknown:
+        raise ValueError(f"unknown engine options: {sorted(unknown)}")
+    values = {f.name: getattr(_DEFAULT_CONFIG, f.name) for f in fields(EngineConfig)}
+    values.update(overrides)
+    _DEFAULT_CONFIG = EngineConfig(**values)
+    return _DEFAULT_CONFIG
+
+
+def get_engine(device: torch.device) -> OffloadEngine:
+    """The engine of ``device``, created on first use with the current configuration."""
+
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    with _ENGINES_LOCK:
+        engine = _ENGINES.get(index)
+        if engine is None:
+            engine = OffloadEngine(torch.device("cuda", index), _DEFAULT_CONFIG)
+            _ENGINES[index] = engine
+        return engine
+
+
+def reset_engines() -> None:
+    """Destroy every engine (no live handles may remain); the next use creates new ones."""
+
+    with _ENGINES_LOCK:
+        for engine in _ENGINES.values():
+            if engine.live_groups():
+                raise RuntimeError("cannot reset an engine that still holds offloaded activations")
+        for engine in _ENGINES.values():
+            engine.close()
+        _ENGINES.clear()
