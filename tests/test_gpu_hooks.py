@@ -1,0 +1,224 @@
+"""The drop-in ``activation_cpu_offload`` on the MOSS DiT harness, on the GPU.
+
+Parity gates, following the reference's own (training/tests/test_packed_cuda.py:173-231):
+the same seeded model is run with hooks off, with the engine, and with the oracle's
+restatement of the reference hooks; outputs and gradients must agree. On top of the
+reference's tolerance checks, every tensor the engine restores is compared bitwise with the
+tensor that was saved, and the forward output with the engine is bitwise equal to the one
+without hooks (the hooks only move data).
+"""
+
+from __future__ import annotations
+
+import copy
+import gc
+
+import pytest
+import torch
+
+import moss_offload
+from moss_offload import dit
+from moss_offload.activation_offload import _ActivationOffload, _OffloadedTensor
+from oracle import reference_hooks
+
+from gpu_util import assert_bitwise, requires_gpu
+
+pytestmark = requires_gpu
+
+
+class _Recording(_ActivationOffload):
+    """Engine context that also checks every restored tensor against a copy of the save."""
+
+    log: dict = {}
+    checked = 0
+
+    def pack(self, tensor):
+        handle = super().pack(tensor)
+        if isinstance(handle, _OffloadedTensor):
+            _Recording.log[id(handle)] = tensor.detach().clone()
+        return handle
+
+    def unpack(self, saved):
+        restored = super().unpack(saved)
+        if isinstance(saved, _OffloadedTensor):
+            expected = _Recording.log[id(saved)]
+            assert restored.shape == expected.shape and restored.stride() == saved.stride
+            assert_bitwise(restored, expected)
+            _Recording.checked += 1
+        return restored
+
+
+def _recording_context(model, enabled, device):
+    if not enabled or device.type != "cuda" or not torch.is_grad_enabled():
+        return moss_offload.activation_cpu_offload(model, enabled, device)
+    return _Recording(model, device)
+
+
+def _tiny(layers=3, checkpointing=False, lora=False, dim=32, ffn=64, heads=4):
+    model = dit.MOSSImageTransformer(
+        dim=dim, ffn_dim=ffn, num_heads=heads, num_layers=layers, text_dim=16, freq_dim=8, latent_channels=4,
+        gradient_checkpointing=checkpointing,
+    )
+    dit.init_weights(model)
+    if lora:
+        dit.inject_lora(model, rank=2, alpha=4.0)
+    return model
+
+
+def _inputs(device, seed=902, shapes=((4, 3, 5),), text=(6,)):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    latents = [torch.randn(1, c, h, w, generator=g).to(device) for c, h, w in shapes]
+    contexts = [torch.randn(1, n, 16, generator=g).to(device) for n in text]
+    return latents, contexts
+
+
+def _run(model, context_factory, enabled, latents, contexts, autocast=False, retain=1):
+    model.activation_offload = enabled
+    model.offload_context = context_factory
+    model.zero_grad(set_to_none=True)
+    t = torch.tensor([500.0], device=latents[0].device)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        outputs = [model(x, t, c) for x, c in zip(latents, contexts)]
+        loss = sum(o.float().square().mean() for o in outputs)
+    for k in range(retain):
+        loss.backward(retain_graph=k + 1 < retain)
+    grads = {n: p.grad.detach().clone() for n, p in model.named_parameters() if p.grad is not None}
+    return [o.detach() for o in outputs], loss.detach(), grads
+
+
+def _compare(actual, expected, rtol, atol, bitwise_outputs=True):
+    outs, loss, grads = actual
+    e_outs, e_loss, e_grads = expected
+    for a, b in zip(outs, e_outs):
+        if bitwise_outputs:
+            assert_bitwise(a, b)
+        else:
+            torch.testing.assert_close(a, b, rtol=rtol, atol=atol)
+    torch.testing.assert_close(loss, e_loss, rtol=rtol, atol=atol)
+    assert grads.keys() == e_grads.keys()
+    for name in grads:
+        torch.testing.assert_close(grads[name], e_grads[name], rtol=rtol, atol=atol, msg=name)
+
+
+@pytest.mark.parametrize("checkpointing", [False, True])
+@pytest.mark.parametrize("lora", [False, True])
+def test_fp32_step_matches_no_offload_and_reference_hooks(checkpointing, lora) -> None:
+    device = torch.device("cuda", 0)
+    torch.manual_seed(903)
+    base = _tiny(checkpointing=checkpointing, lora=lora).to(device).train()
+    latents, contexts = _inputs(device)
+    expected = _run(copy.deepcopy(base), moss_offload.activation_cpu_offload, False, latents, contexts)
+    reference = _run(copy.deepcopy(base), reference_hooks.activation_cpu_offload, True, latents, contexts)
+    _Recording.log, _Recording.checked = {}, 0
+    actual = _run(copy.deepcopy(base), _recording_context, True, latents, contexts)
+    assert _Recording.checked > 0
+    _compare(actual, expected, rtol=5e-5, atol=5e-6)
+    _compare(actual, reference, rtol=5e-5, atol=5e-6)
+
+
+def test_config1_block_fp32_restores_bit_exact() -> None:
+    """BASELINE config 1 on the GPU: hidden 512, 8x64 heads, MLP 2048, 256 image + 64 text."""
+
+    device = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    model = dit.MOSSImageTransformer(
+        dim=512, ffn_dim=2048, num_heads=8, num_layers=1, text_dim=64, freq_dim=32, latent_channels=16,
+    )
+    dit.init_weights(model)
+    model = model.to(device).train()
+    g = torch.Generator(device="cpu").manual_seed(0)
+    latents = [torch.randn(1, 16, 16, 16, generator=g).to(device)]
+    contexts = [torch.randn(1, 64, 64, generator=g).to(device)]
+    expected = _run(copy.deepcopy(model), moss_offload.activation_cpu_offload, False, latents, contexts)
+    _Recording.log, _Recording.checked = {}, 0
+    actual = _run(copy.deepcopy(model), _recording_context, True, latents, contexts)
+    assert _Recording.checked > 30
+    _compare(actual, expected, rtol=5e-5, atol=5e-6)
+
+
+@pytest.mark.parametrize("checkpointing", [False, True])
+def test_bf16_lora_step_within_north_star_tolerance(checkpointing) -> None:
+    device = torch.device("cuda", 0)
+    torch.manual_seed(904)
+    base = _tiny(layers=4, checkpointing=checkpointing, lora=True, dim=64, ffn=256, heads=4).to(device)
+    base = base.to(torch.bfloat16).train()
+    for module in base.modules():
+        if isinstance(module, dit.LoRALinear):
+            module.lora_A.data = module.lora_A.data.float()
+            module.lora_B.data = module.lora_B.data.float()
+    latents, contexts = _inputs(device, shapes=((4, 8, 8),), text=(12,))
+    expected = _run(copy.deepcopy(base), moss_offload.activation_cpu_offload, False, latents, contexts, autocast=True)
+    _Recording.log, _Recording.checked = {}, 0
+    actual = _run(copy.deepcopy(base), _recording_context, True, latents, contexts, autocast=True)
+    assert _Recording.checked > 0
+    _compare(actual, expected, rtol=1e-3, atol=1e-5)
+
+
+def test_retain_graph_subset_grad_and_dropped_graph() -> None:
+    device = torch.device("cuda", 0)
+    torch.manual_seed(905)
+    base = _tiny(lora=True).to(device).train()
+    latents, contexts = _inputs(device)
+    expected = _run(copy.deepcopy(base), moss_offload.activation_cpu_offload, False, latents, contexts, retain=2)
+    actual = _run(copy.deepcopy(base), moss_offload.activation_cpu_offload, True, latents, contexts, retain=2)
+    _compare(actual, expected, rtol=5e-5, atol=5e-6)
+
+    engine = moss_offload.get_engine(device)
+    # torch.autograd.grad over a subset of the graph
+    model = copy.deepcopy(base)
+    model.activation_offload = True
+    t = torch.tensor([500.0], device=device)
+    out = model(latents[0], t, contexts[0])
+    target = [p for n, p in model.named_parameters() if p.requires_grad and n.startswith("layers.2.")]
+    (sub,) = torch.autograd.grad(out.square().mean(), target[:1])
+    ref_model = copy.deepcopy(base)
+    ref_out = ref_model(latents[0], t, contexts[0])
+    ref_target = [p for n, p in ref_model.named_parameters() if p.requires_grad and n.startswith("layers.2.")]
+    (ref_sub,) = torch.autograd.grad(ref_out.square().mean(), ref_target[:1])
+    torch.testing.assert_close(sub, ref_sub, rtol=5e-5, atol=5e-6)
+    del out, sub
+    # a graph that is never backpropagated
+    out = model(latents[0], t, contexts[0])
+    assert engine.live_groups() > 0
+    del out
+    gc.collect()
+    torch.cuda.synchronize(device)
+    assert engine.live_groups() == 0
+    engine.synchronize()
+    assert engine.stats()["host_bytes_in_use"] == 0
+
+
+def test_several_forwards_one_backward() -> None:
+    """Config-5 unpacked mode: one forward per shape group, one backward over all graphs."""
+
+    device = torch.device("cuda", 0)
+    torch.manual_seed(906)
+    base = _tiny(lora=True, checkpointing=True).to(device).train()
+    latents, contexts = _inputs(device, shapes=((4, 4, 4), (4, 3, 5), (4, 5, 3), (4, 4, 2)), text=(6, 4, 5, 3))
+    expected = _run(copy.deepcopy(base), moss_offload.activation_cpu_offload, False, latents, contexts)
+    _Recording.log, _Recording.checked = {}, 0
+    actual = _run(copy.deepcopy(base), _recording_context, True, latents, contexts)
+    _compare(actual, expected, rtol=5e-5, atol=5e-6)
+
+
+def test_weight_backed_and_staging_buffers_stay_resident() -> None:
+    device = torch.device("cuda", 0)
+    model = _tiny().to(device).train()
+    staging = torch.randn(64, device=device, requires_grad=False)
+
+    class Manager:
+        def owned_cuda_buffers(self):
+            return (staging,)
+
+    model.block_swap_manager = Manager()
+    ctx = moss_offload.activation_cpu_offload(model, True, device)
+    with ctx:
+        weight_view = model.layers[0].proj["q"].weight.t()
+        assert ctx.pack(weight_view) is weight_view
+        assert ctx.pack(staging[8:]) is not None and isinstance(ctx.pack(staging[8:]), torch.Tensor)
+        cpu = torch.randn(3)
+        assert ctx.pack(cpu) is cpu
+        overlapping = torch.randn(16, device=device).as_strided((3, 3), (1, 1))
+        assert ctx.pack(overlapping) is overlapping
+        handle = ctx.pack(torch.randn(4, 0, device=device))
+        assert isinstance(handle, _OffloadedTensor) and ctx.unpack(handle).shape == (4, 0)
