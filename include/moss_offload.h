@@ -43,8 +43,9 @@ extern "C" {
 #define MO_E_STATE 1004     /* call not valid in the engine's current state */
 
 /* Flags for mo_config.flags. */
-#define MO_FLAG_TIMING 0x1       /* time every D2H/H2D copy with HIP events       */
-#define MO_FLAG_KERNEL_COPY 0x2  /* move D2H/H2D with a copy kernel, not the DMA */
+#define MO_FLAG_TIMING 0x1         /* time every D2H/H2D copy with HIP events            */
+#define MO_FLAG_KERNEL_COPY 0x2    /* move D2H/H2D with a copy kernel, not the DMA      */
+#define MO_FLAG_KERNEL_TIMING 0x4  /* time every pack/unpack launch with HIP events     */
 
 /*
  * A strided tensor view on the device. `ptr` is the address of logical element (0,...,0),
@@ -91,6 +92,9 @@ typedef struct mo_stats {
   uint64_t restore_fetches;    /* segments fetched on demand by unpack                 */
   double d2h_ms, h2d_ms;       /* summed copy durations (MO_FLAG_TIMING), completed only */
   uint64_t timed_d2h_bytes, timed_h2d_bytes;
+  double pack_ms, unpack_ms;   /* summed kernel durations (MO_FLAG_KERNEL_TIMING)         */
+  uint64_t timed_pack_bytes, timed_unpack_bytes; /* payload bytes of those launches      */
+  uint64_t timed_pack_launches, timed_unpack_launches;
 } mo_stats;
 
 typedef struct mo_engine mo_engine;

@@ -252,10 +252,12 @@ struct PendingFree {
   hipEvent_t ev[2];
 };
 
+enum TimingKind { kTimeD2H = 0, kTimeH2D = 1, kTimePack = 2, kTimeUnpack = 3 };
+
 struct Timing {
   hipEvent_t start, end;
   uint64_t bytes;
-  bool d2h;
+  int kind;
 };
 
 }  // namespace
@@ -293,9 +295,13 @@ struct Engine {
   void recycle(hipEvent_t ev) {
     if (ev) event_pool.push_back(ev);
   }
+  bool timed(int kind) const {
+    const bool copy = kind == kTimeD2H || kind == kTimeH2D;
+    return (cfg.flags & (copy ? MO_FLAG_TIMING : MO_FLAG_KERNEL_TIMING)) != 0;
+  }
   int timing_begin(hipStream_t s, Timing& t) {
     t.start = t.end = nullptr;
-    if (!(cfg.flags & MO_FLAG_TIMING)) return 0;
+    if (!timed(t.kind)) return 0;
     for (hipEvent_t* e : {&t.start, &t.end}) {
       if (!timing_pool.empty()) {
         *e = timing_pool.back();
@@ -320,12 +326,13 @@ struct Engine {
       else if (hipEventQuery(t.end) != hipSuccess) break;
       float ms = 0.f;
       if (hipEventElapsedTime(&ms, t.start, t.end) == hipSuccess) {
-        if (t.d2h) {
-          st.d2h_ms += ms;
-          st.timed_d2h_bytes += t.bytes;
-        } else {
-          st.h2d_ms += ms;
-          st.timed_h2d_bytes += t.bytes;
+        switch (t.kind) {
+          case kTimeD2H: st.d2h_ms += ms; st.timed_d2h_bytes += t.bytes; break;
+          case kTimeH2D: st.h2d_ms += ms; st.timed_h2d_bytes += t.bytes; break;
+          case kTimePack:
+            st.pack_ms += ms; st.timed_pack_bytes += t.bytes; st.timed_pack_launches++; break;
+          default:
+            st.unpack_ms += ms; st.timed_unpack_bytes += t.bytes; st.timed_unpack_launches++; break;
         }
       }
       timing_pool.push_back(t.start);
@@ -358,7 +365,7 @@ struct Engine {
   int copy(char* dst, const char* src, uint64_t bytes, bool to_host, hipStream_t s) {
     Timing t{};
     t.bytes = bytes;
-    t.d2h = to_host;
+    t.kind = to_host ? kTimeD2H : kTimeH2D;
     if (int rc = timing_begin(s, t)) return rc;
     if (cfg.flags & MO_FLAG_KERNEL_COPY) {
       char* d = to_host ? pool.device_alias(dst) : dst;
@@ -370,6 +377,23 @@ struct Engine {
     }
     return timing_end(s, t);
   }
+
+  // Brackets each pack/unpack launch with timing events (MO_FLAG_KERNEL_TIMING).
+  struct KernelTimer : LaunchTimer {
+    Engine* e;
+    int kind;
+    Timing cur{};
+    KernelTimer(Engine* engine, int k) : e(engine), kind(k) {}
+    int before(hipStream_t s) override {
+      cur = Timing{};
+      cur.kind = kind;
+      return e->timing_begin(s, cur);
+    }
+    int after(hipStream_t s, uint64_t bytes) override {
+      cur.bytes = bytes;
+      return e->timing_end(s, cur);
+    }
+  };
 
   // ---- forward ----
   int close_segment(Launcher& L, hipStream_t stream) {
@@ -421,7 +445,8 @@ struct Engine {
       st.groups_created++;
     }
     Group& g = *open_group;
-    Launcher L(true, stream);
+    KernelTimer timer(this, kTimePack);
+    Launcher L(true, stream, &timer);
     const uint64_t slot_bytes = cfg.stage_slot_bytes;
     for (int i = 0; i < n; ++i) {
       const Canon& c = canons[i];
@@ -472,7 +497,8 @@ struct Engine {
   int commit(hipStream_t stream, uint64_t* gid) {
     *gid = kNone;
     if (!open_group) return 0;
-    Launcher L(true, stream);
+    KernelTimer timer(this, kTimePack);
+    Launcher L(true, stream, &timer);
     if (int rc = close_segment(L, stream)) return rc;
     open_group->open = false;
     *gid = open_group->id;
@@ -597,7 +623,8 @@ struct Engine {
       seg.prefetched = false;
       RestoreSlot& r = restore[k];
       MO_HIP(hipStreamWaitEvent(stream, r.ready, 0));
-      Launcher L(false, stream);
+      KernelTimer timer(this, kTimeUnpack);
+      Launcher L(false, stream, &timer);
       for (const Piece& p : seg.pieces) {
         if (!dst[p.entry]) continue;
         KDesc kd;

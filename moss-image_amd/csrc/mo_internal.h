@@ -51,10 +51,19 @@ static_assert(sizeof(LaunchArgs) <= 4096, "kernel arguments must fit in 4 KiB");
 int make_kdesc(const Canon& c, uint64_t tensor_base, uint64_t first, uint64_t nbytes, uint64_t payload,
                KDesc& kd, std::string& err);
 
+// Optional observer that brackets each kernel launch (e.g. with timing events).
+class LaunchTimer {
+ public:
+  virtual ~LaunchTimer() = default;
+  virtual int before(hipStream_t stream) = 0;
+  virtual int after(hipStream_t stream, uint64_t bytes) = 0;
+};
+
 // Accumulates pieces and launches the pack (or unpack) kernel in batches of kMaxDesc.
 class Launcher {
  public:
-  Launcher(bool pack, hipStream_t stream) : pack_(pack), stream_(stream) {}
+  Launcher(bool pack, hipStream_t stream, LaunchTimer* timer = nullptr)
+      : pack_(pack), stream_(stream), timer_(timer) {}
   void add(const KDesc& kd);
   int flush();
   int status() const { return status_; }
@@ -64,11 +73,13 @@ class Launcher {
  private:
   bool pack_;
   hipStream_t stream_;
+  LaunchTimer* timer_;
   LaunchArgs args_;
   uint32_t tiles_ = 0;
   int status_ = 0;
   uint64_t launches_ = 0;
-  uint64_t bytes_ = 0;
+  uint64_t bytes_ = 0;          // all bytes added
+  uint64_t pending_bytes_ = 0;  // bytes of the batch not launched yet
 };
 
 int launch_link_copy(void* dst, const void* src, uint64_t bytes, uint32_t blocks, hipStream_t stream);

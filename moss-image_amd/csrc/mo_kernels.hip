@@ -262,12 +262,14 @@ void Launcher::add(const KDesc& kd) {
   const uint64_t t = (kd.nbytes + kTileBytes - 1) / kTileBytes;
   tiles_ += (uint32_t)t;
   bytes_ += kd.nbytes;
+  pending_bytes_ += kd.nbytes;
   args_.ndesc++;
   if (tiles_ > kMaxTilesPerLaunch) flush();
 }
 
 int Launcher::flush() {
   if (args_.ndesc == 0) return 0;
+  if (status_ == 0 && timer_) status_ = timer_->before(stream_);
   if (status_ == 0) {
     if (pack_) {
       hipLaunchKernelGGL(copy_kernel<true>, dim3(tiles_), dim3(kThreads), 0, stream_, args_);
@@ -278,8 +280,10 @@ int Launcher::flush() {
     if (e != hipSuccess) status_ = (int)e;
     launches_++;
   }
+  if (status_ == 0 && timer_) status_ = timer_->after(stream_, pending_bytes_);
   args_.ndesc = 0;
   tiles_ = 0;
+  pending_bytes_ = 0;
   return status_;
 }
 

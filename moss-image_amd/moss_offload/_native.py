@@ -25,6 +25,7 @@ MO_E_STATE = 1004
 
 MO_FLAG_TIMING = 0x1
 MO_FLAG_KERNEL_COPY = 0x2
+MO_FLAG_KERNEL_TIMING = 0x4
 
 NO_GROUP = (1 << 64) - 1
 
@@ -84,6 +85,12 @@ class MoStats(ctypes.Structure):
         ("h2d_ms", ctypes.c_double),
         ("timed_d2h_bytes", ctypes.c_uint64),
         ("timed_h2d_bytes", ctypes.c_uint64),
+        ("pack_ms", ctypes.c_double),
+        ("unpack_ms", ctypes.c_double),
+        ("timed_pack_bytes", ctypes.c_uint64),
+        ("timed_unpack_bytes", ctypes.c_uint64),
+        ("timed_pack_launches", ctypes.c_uint64),
+        ("timed_unpack_launches", ctypes.c_uint64),
     ]
 
     def as_dict(self) -> dict:

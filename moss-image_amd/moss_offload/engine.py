@@ -37,6 +37,7 @@ class EngineConfig:
     host_limit_bytes: int = 0
     host_chunk_bytes: int = 1 << 30
     timing: bool = False
+    kernel_timing: bool = False
     kernel_copy: bool = False
     copy_kernel_blocks: int = 64
     prefetch: bool = True
@@ -49,8 +50,10 @@ class EngineConfig:
         cfg.restore_slots = self.restore_slots
         cfg.host_limit_bytes = self.host_limit_bytes
         cfg.host_chunk_bytes = self.host_chunk_bytes
-        cfg.flags = (_native.MO_FLAG_TIMING if self.timing else 0) | (
-            _native.MO_FLAG_KERNEL_COPY if self.kernel_copy else 0
+        cfg.flags = (
+            (_native.MO_FLAG_TIMING if self.timing else 0)
+            | (_native.MO_FLAG_KERNEL_COPY if self.kernel_copy else 0)
+            | (_native.MO_FLAG_KERNEL_TIMING if self.kernel_timing else 0)
         )
         cfg.copy_kernel_blocks = self.copy_kernel_blocks
         return cfg
