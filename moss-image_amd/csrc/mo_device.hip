@@ -1,12 +1,13 @@
-// Pack / unpack kernels for gfx950 (MI355X).
+// Pack / unpack kernels for gfx950 (MI355X), compiled to a standalone code object
+// (hipcc --genco) that the host library embeds and loads with hipModuleLoadData.
 //
 // One launch moves up to kMaxDesc "pieces" (a byte range of one tensor's payload) between
 // strided tensor views and a dense staging payload. The payload is in storage order, so the
 // tensor side is walked in address order too; nothing is transposed. The work is pure data
 // movement and HBM-bound: every path aims at 128-bit coalesced loads and stores.
 //
-//   CONTIG  the piece is one contiguous run and 16-byte aligned: 64-bit-free address math,
-//           kUnroll x 16 B in flight per lane.
+//   CONTIG  the piece is one contiguous run and 16-byte aligned: kUnroll x 16 B in flight
+//           per lane, no index arithmetic.
 //   RUNS    contiguous runs whose length, start and strides are multiples of 16 B: each
 //           16-byte chunk is located with fast division over the canonical dimensions.
 //   ELEM    anything else (misaligned bases, odd run lengths, element-strided innermost
@@ -19,15 +20,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include <string>
-#include <vector>
-
-#include "mo_internal.h"
+#include "mo_kdesc.h"
 
 namespace mo {
-
-// ------------------------------------------------------------------------------------------
-// device helpers
 
 __device__ __forceinline__ uint32_t fdiv(uint32_t n, uint32_t m, uint32_t s) {
   const uint64_t t = __umulhi(m, n);
@@ -35,7 +30,7 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, uint32_t m, uint32_t s) {
 }
 
 // Address offset (bytes, relative to the tensor base) of unit `u` of a piece's tensor side.
-// A unit is a 16-byte chunk (RUNS) or an element (ELEM). inner: units per innermost run.
+// A unit is a 16-byte chunk (RUNS) or an element (ELEM).
 __device__ __forceinline__ uint64_t unit_offset(const KDesc& d, uint32_t u) {
   uint32_t q = fdiv(u, d.inner.m, d.inner.s);
   uint64_t off = (uint64_t)(u - q * d.inner.d) * d.inner_stride;
@@ -65,7 +60,7 @@ __device__ __forceinline__ uint4 ld16(const char* p) { return *(const uint4*)p; 
 __device__ __forceinline__ void st16(char* p, uint4 v) { *(uint4*)p = v; }
 
 template <bool kPack>
-__global__ __launch_bounds__(kThreads) void copy_kernel(const LaunchArgs args) {
+__device__ __forceinline__ void copy_body(const LaunchArgs& args) {
   __shared__ uint4 lds[kTileBytes / 16];
   const uint32_t tile = blockIdx.x;
   uint32_t i = 0;
@@ -142,12 +137,22 @@ __global__ __launch_bounds__(kThreads) void copy_kernel(const LaunchArgs args) {
   }
 }
 
+}  // namespace mo
+
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_pack_kernel(const mo::LaunchArgs args) {
+  mo::copy_body<true>(args);
+}
+
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_unpack_kernel(const mo::LaunchArgs args) {
+  mo::copy_body<false>(args);
+}
+
 // Device <-> pinned-host copy through the shader engines instead of a DMA engine.
 // Each lane keeps kLinkUnroll 16-byte transfers in flight; the grid strides over the buffer.
-constexpr int kLinkUnroll = 8;
-
-__global__ __launch_bounds__(kThreads) void link_copy_kernel(char* __restrict__ dst, const char* __restrict__ src,
-                                                             uint64_t nbytes) {
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_link_copy_kernel(char* __restrict__ dst,
+                                                                                const char* __restrict__ src,
+                                                                                uint64_t nbytes) {
+  using namespace mo;
   const uint64_t nvec = nbytes / 16;
   const uint64_t lanes = (uint64_t)gridDim.x * kThreads;
   const uint64_t step = lanes * kLinkUnroll;
@@ -164,136 +169,3 @@ __global__ __launch_bounds__(kThreads) void link_copy_kernel(char* __restrict__ 
     for (uint64_t b = nvec * 16 + threadIdx.x; b < nbytes; b += kThreads) dst[b] = src[b];
   }
 }
-
-// ------------------------------------------------------------------------------------------
-// host: piece -> kernel descriptor
-
-// Fill `kd` for the byte range [first, first + nbytes) of the payload of tensor `c`, whose
-// tensor side starts at `tensor_base` (a restored tensor has the same strides as the packed
-// one but another base). `payload` is the device address of the piece's payload bytes.
-int make_kdesc(const Canon& c, uint64_t tensor_base, uint64_t first, uint64_t nbytes, uint64_t payload,
-               KDesc& kd, std::string& err) {
-  kd = KDesc();
-  kd.tensor = tensor_base;
-  kd.payload = payload;
-  kd.nbytes = nbytes;
-  kd.eb = (uint8_t)c.eb;
-  if (payload % 16 != 0 || first % 16 != 0) {
-    err = "piece payload and offset must be 16-byte aligned";
-    return MO_E_INVALID;
-  }
-  // Canonical dims, innermost last. Treat a unit-stride innermost dim as a contiguous run.
-  const int nd = c.nd;
-  const bool inner_contig = nd == 0 || (uint64_t)c.stride[nd - 1] == c.eb;
-  const uint64_t run_bytes = nd == 0 ? c.eb : (inner_contig ? (uint64_t)c.size[nd - 1] * c.eb : c.eb);
-  const int nouter = inner_contig ? (nd > 0 ? nd - 1 : 0) : nd;  // dims outside the run
-  if (nouter == 0 && tensor_base % 16 == 0) {
-    kd.path = kPathContig;
-    kd.first = first;
-    return 0;
-  }
-  bool runs16 = run_bytes % 16 == 0 && tensor_base % 16 == 0;
-  for (int k = 0; k < nouter && runs16; ++k) runs16 = c.stride[k] % 16 == 0;
-  if (runs16) {
-    if (nouter > kMaxOuter) {
-      err = "too many canonical dimensions for one descriptor";
-      return MO_E_STATE;
-    }
-    const uint64_t run_chunks = run_bytes / 16;
-    const uint64_t total_chunks = c.nbytes / 16;
-    if (run_chunks >= (1ull << 32) || total_chunks >= (1ull << 32)) {
-      err = "tensor too large for 32-bit chunk indexing";
-      return MO_E_INVALID;
-    }
-    kd.path = kPathRuns;
-    kd.first = first / 16;
-    const FastDiv f = make_fastdiv((uint32_t)run_chunks);
-    kd.inner = KFastDiv{f.d, f.m, f.s};
-    kd.inner_stride = 16;
-    kd.nouter = (uint8_t)nouter;
-    for (int k = 0; k < nouter; ++k) {  // kernel order: innermost outer dim first
-      const int dim = nouter - 1 - k;
-      const FastDiv g = make_fastdiv((uint32_t)c.size[dim]);
-      kd.outer[k] = KFastDiv{g.d, g.m, g.s};
-      kd.ostride[k] = (uint64_t)c.stride[dim];
-    }
-    return 0;
-  }
-  // ELEM path: units are elements. Innermost canonical dim is the "inner" run.
-  if (c.numel >= (1ull << 32)) {
-    err = "tensor too large for 32-bit element indexing";
-    return MO_E_INVALID;
-  }
-  const int eouter = nd > 0 ? nd - 1 : 0;
-  if (eouter > kMaxOuter) {
-    err = "too many canonical dimensions for one descriptor";
-    return MO_E_STATE;
-  }
-  kd.path = kPathElem;
-  kd.first = first / c.eb;
-  if (nd == 0) {
-    kd.inner = KFastDiv{1, 1, 0};
-    kd.inner_stride = c.eb;
-    kd.nouter = 0;
-    return 0;
-  }
-  const FastDiv f = make_fastdiv((uint32_t)c.size[nd - 1]);
-  kd.inner = KFastDiv{f.d, f.m, f.s};
-  kd.inner_stride = (uint64_t)c.stride[nd - 1];
-  kd.nouter = (uint8_t)eouter;
-  for (int k = 0; k < eouter; ++k) {
-    const int dim = eouter - 1 - k;
-    const FastDiv g = make_fastdiv((uint32_t)c.size[dim]);
-    kd.outer[k] = KFastDiv{g.d, g.m, g.s};
-    kd.ostride[k] = (uint64_t)c.stride[dim];
-  }
-  return 0;
-}
-
-// ------------------------------------------------------------------------------------------
-// host: batched launches
-
-void Launcher::add(const KDesc& kd) {
-  if (kd.nbytes == 0) return;
-  if (args_.ndesc == kMaxDesc) flush();
-  KDesc& slot = args_.d[args_.ndesc];
-  slot = kd;
-  slot.tile0 = tiles_;
-  const uint64_t t = (kd.nbytes + kTileBytes - 1) / kTileBytes;
-  tiles_ += (uint32_t)t;
-  bytes_ += kd.nbytes;
-  pending_bytes_ += kd.nbytes;
-  args_.ndesc++;
-  if (tiles_ > kMaxTilesPerLaunch) flush();
-}
-
-int Launcher::flush() {
-  if (args_.ndesc == 0) return 0;
-  if (status_ == 0 && timer_) status_ = timer_->before(stream_);
-  if (status_ == 0) {
-    if (pack_) {
-      hipLaunchKernelGGL(copy_kernel<true>, dim3(tiles_), dim3(kThreads), 0, stream_, args_);
-    } else {
-      hipLaunchKernelGGL(copy_kernel<false>, dim3(tiles_), dim3(kThreads), 0, stream_, args_);
-    }
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) status_ = (int)e;
-    launches_++;
-  }
-  if (status_ == 0 && timer_) status_ = timer_->after(stream_, pending_bytes_);
-  args_.ndesc = 0;
-  tiles_ = 0;
-  pending_bytes_ = 0;
-  return status_;
-}
-
-int launch_link_copy(void* dst, const void* src, uint64_t bytes, uint32_t blocks, hipStream_t stream) {
-  if (bytes == 0) return 0;
-  if (blocks == 0) blocks = 64;
-  const uint64_t max_blocks = (bytes / 16 + kThreads - 1) / kThreads;
-  if (blocks > max_blocks) blocks = (uint32_t)(max_blocks ? max_blocks : 1);
-  hipLaunchKernelGGL(link_copy_kernel, dim3(blocks), dim3(kThreads), 0, stream, (char*)dst, (const char*)src, bytes);
-  return (int)hipGetLastError();
-}
-
-}  // namespace mo

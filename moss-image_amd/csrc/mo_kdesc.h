@@ -1,0 +1,49 @@
+// Kernel-argument structures shared by the device code (mo_device.hip) and the host launchers.
+// Plain data only: no HIP headers, so the host side compiles with any C++17 compiler.
+#pragma once
+
+#include <stdint.h>
+
+#include "../../include/moss_offload.h"
+
+namespace mo {
+
+constexpr int kThreads = 256;                 // lanes per workgroup (4 wave64)
+constexpr int kUnroll = 4;                    // 16-byte transfers in flight per lane
+constexpr uint32_t kTileBytes = kThreads * kUnroll * 16;  // 16 KiB of payload per workgroup
+constexpr int kMaxOuter = MO_MAX_DIMS - 1;    // canonical dims beyond the innermost run
+constexpr int kMaxDesc = 16;                  // pieces per launch (kernel-argument budget)
+constexpr uint32_t kMaxTilesPerLaunch = 1u << 22;
+constexpr int kLinkUnroll = 8;                // 16-byte transfers in flight per lane (link copy)
+
+enum : uint8_t { kPathContig = 0, kPathRuns = 1, kPathElem = 2 };
+
+struct KFastDiv {
+  uint32_t d, m, s;
+};
+
+// One piece: a byte range of one tensor's storage-order payload.
+struct KDesc {
+  uint64_t tensor;        // tensor-side base address (element (0,...,0))
+  uint64_t payload;       // payload-side address of the piece's first byte
+  uint64_t first;         // piece start in path units: bytes | 16-B chunks | elements
+  uint64_t nbytes;        // piece length in bytes
+  uint64_t inner_stride;  // bytes between consecutive units of the innermost run
+  uint32_t tile0;         // first tile of this piece within the launch
+  uint8_t path;
+  uint8_t eb;
+  uint8_t nouter;
+  uint8_t pad;
+  KFastDiv inner;               // units per innermost run
+  KFastDiv outer[kMaxOuter];    // sizes of the outer dims, innermost first
+  uint64_t ostride[kMaxOuter];  // byte strides of the outer dims
+};
+
+struct LaunchArgs {
+  uint32_t ndesc;
+  uint32_t pad;
+  KDesc d[kMaxDesc];
+};
+static_assert(sizeof(LaunchArgs) <= 4096, "kernel arguments must fit in 4 KiB");
+
+}  // namespace mo

@@ -1,0 +1,188 @@
+// Host side of the kernels: piece -> kernel descriptor, batched launches, and the loader of
+// the embedded gfx950 code object (mo_device.hip compiled with hipcc --genco).
+//
+// The device code is loaded with hipModuleLoadData on first use on each device and its
+// kernels are launched with hipModuleLaunchKernel. The library therefore registers no fat
+// binary with the HIP runtime at load time and unregisters none at process exit; the runtime
+// shared with the host application (torch's) owns the module like any other.
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+
+#include "mo_internal.h"
+
+extern "C" const unsigned char mo_device_code[];
+extern "C" const uint64_t mo_device_code_size;
+
+namespace mo {
+
+namespace {
+
+struct DeviceModule {
+  hipModule_t module = nullptr;
+  hipFunction_t pack = nullptr, unpack = nullptr, link = nullptr;
+};
+
+std::mutex g_modules_mu;
+std::map<int, DeviceModule> g_modules;
+
+int load_functions(DeviceModule& m) {
+  hipError_t e = hipModuleLoadData(&m.module, mo_device_code);
+  if (e != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.pack, m.module, "mo_pack_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.unpack, m.module, "mo_unpack_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.link, m.module, "mo_link_copy_kernel")) != hipSuccess) return (int)e;
+  return 0;
+}
+
+}  // namespace
+
+// Kernels of the current device, loading the code object on first use.
+static int kernels(hipFunction_t* pack, hipFunction_t* unpack, hipFunction_t* link) {
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return (int)e;
+  std::lock_guard<std::mutex> lock(g_modules_mu);
+  auto it = g_modules.find(device);
+  if (it == g_modules.end()) {
+    DeviceModule m;
+    if (int rc = load_functions(m)) return rc;
+    it = g_modules.emplace(device, m).first;
+  }
+  if (pack) *pack = it->second.pack;
+  if (unpack) *unpack = it->second.unpack;
+  if (link) *link = it->second.link;
+  return 0;
+}
+
+// ------------------------------------------------------------------------------------------
+// piece -> kernel descriptor
+
+int make_kdesc(const Canon& c, uint64_t tensor_base, uint64_t first, uint64_t nbytes, uint64_t payload,
+               KDesc& kd, std::string& err) {
+  kd = KDesc();
+  kd.tensor = tensor_base;
+  kd.payload = payload;
+  kd.nbytes = nbytes;
+  kd.eb = (uint8_t)c.eb;
+  kd.inner = KFastDiv{1, 1, 0};
+  if (payload % 16 != 0 || first % 16 != 0) {
+    err = "piece payload and offset must be 16-byte aligned";
+    return MO_E_INVALID;
+  }
+  // Canonical dims, innermost last. A unit-stride innermost dim is a contiguous run.
+  const int nd = c.nd;
+  const bool inner_contig = nd == 0 || (uint64_t)c.stride[nd - 1] == c.eb;
+  const uint64_t run_bytes = nd == 0 ? c.eb : (inner_contig ? (uint64_t)c.size[nd - 1] * c.eb : c.eb);
+  const int nouter = inner_contig ? (nd > 0 ? nd - 1 : 0) : nd;  // dims outside the run
+  if (nouter == 0 && tensor_base % 16 == 0) {
+    kd.path = kPathContig;
+    kd.first = first;
+    return 0;
+  }
+  bool runs16 = run_bytes % 16 == 0 && tensor_base % 16 == 0 && nouter <= kMaxOuter;
+  for (int k = 0; k < nouter && runs16; ++k) runs16 = c.stride[k] % 16 == 0;
+  if (runs16) {
+    const uint64_t run_chunks = run_bytes / 16;
+    const uint64_t total_chunks = c.nbytes / 16;
+    if (run_chunks >= (1ull << 32) || total_chunks >= (1ull << 32)) {
+      err = "tensor too large for 32-bit chunk indexing";
+      return MO_E_INVALID;
+    }
+    kd.path = kPathRuns;
+    kd.first = first / 16;
+    const FastDiv f = make_fastdiv((uint32_t)run_chunks);
+    kd.inner = KFastDiv{f.d, f.m, f.s};
+    kd.inner_stride = 16;
+    kd.nouter = (uint8_t)nouter;
+    for (int k = 0; k < nouter; ++k) {  // kernel order: innermost outer dim first
+      const int dim = nouter - 1 - k;
+      const FastDiv g = make_fastdiv((uint32_t)c.size[dim]);
+      kd.outer[k] = KFastDiv{g.d, g.m, g.s};
+      kd.ostride[k] = (uint64_t)c.stride[dim];
+    }
+    return 0;
+  }
+  // ELEM path: units are elements; the innermost canonical dim is the inner run.
+  if (c.numel >= (1ull << 32)) {
+    err = "tensor too large for 32-bit element indexing";
+    return MO_E_INVALID;
+  }
+  const int eouter = nd > 0 ? nd - 1 : 0;
+  kd.path = kPathElem;
+  kd.first = first / c.eb;
+  if (nd == 0) {
+    kd.inner_stride = c.eb;
+    return 0;
+  }
+  const FastDiv f = make_fastdiv((uint32_t)c.size[nd - 1]);
+  kd.inner = KFastDiv{f.d, f.m, f.s};
+  kd.inner_stride = (uint64_t)c.stride[nd - 1];
+  kd.nouter = (uint8_t)eouter;
+  for (int k = 0; k < eouter; ++k) {
+    const int dim = eouter - 1 - k;
+    const FastDiv g = make_fastdiv((uint32_t)c.size[dim]);
+    kd.outer[k] = KFastDiv{g.d, g.m, g.s};
+    kd.ostride[k] = (uint64_t)c.stride[dim];
+  }
+  return 0;
+}
+
+// ------------------------------------------------------------------------------------------
+// batched launches
+
+Launcher::Launcher(bool pack, hipStream_t stream, LaunchTimer* timer) : pack_(pack), stream_(stream), timer_(timer) {
+  args_.ndesc = 0;
+  args_.pad = 0;
+}
+
+void Launcher::add(const KDesc& kd) {
+  if (kd.nbytes == 0) return;
+  if (args_.ndesc == (uint32_t)kMaxDesc) flush();
+  KDesc& slot = args_.d[args_.ndesc];
+  slot = kd;
+  slot.tile0 = tiles_;
+  const uint64_t t = (kd.nbytes + kTileBytes - 1) / kTileBytes;
+  tiles_ += (uint32_t)t;
+  bytes_ += kd.nbytes;
+  pending_bytes_ += kd.nbytes;
+  args_.ndesc++;
+  if (tiles_ > kMaxTilesPerLaunch) flush();
+}
+
+int Launcher::flush() {
+  if (args_.ndesc == 0) return 0;
+  hipFunction_t fn = nullptr;
+  if (status_ == 0) status_ = pack_ ? kernels(&fn, nullptr, nullptr) : kernels(nullptr, &fn, nullptr);
+  if (status_ == 0 && timer_) status_ = timer_->before(stream_);
+  if (status_ == 0) {
+    void* params[] = {&args_};
+    const hipError_t e = hipModuleLaunchKernel(fn, tiles_, 1, 1, kThreads, 1, 1, 0, stream_, params, nullptr);
+    if (e != hipSuccess) status_ = (int)e;
+    launches_++;
+  }
+  if (status_ == 0 && timer_) status_ = timer_->after(stream_, pending_bytes_);
+  args_.ndesc = 0;
+  tiles_ = 0;
+  pending_bytes_ = 0;
+  return status_;
+}
+
+int launch_link_copy(void* dst, const void* src, uint64_t bytes, uint32_t blocks, hipStream_t stream) {
+  if (bytes == 0) return 0;
+  if (blocks == 0) blocks = 64;
+  const uint64_t max_blocks = (bytes / 16 + kThreads - 1) / kThreads;
+  if (blocks > max_blocks) blocks = (uint32_t)(max_blocks ? max_blocks : 1);
+  hipFunction_t fn = nullptr;
+  if (int rc = kernels(nullptr, nullptr, &fn)) return rc;
+  void* d = dst;
+  const void* s = src;
+  uint64_t n = bytes;
+  void* params[] = {&d, &s, &n};
+  return (int)hipModuleLaunchKernel(fn, blocks, 1, 1, kThreads, 1, 1, 0, stream, params, nullptr);
+}
+
+}  // namespace mo

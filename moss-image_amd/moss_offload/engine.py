@@ -17,6 +17,7 @@ copy streams, events and kernels. This layer decides *when* to call it:
 
 from __future__ import annotations
 
+import atexit
 import bisect
 import ctypes
 import threading
@@ -304,4 +305,18 @@ def reset_engines() -> None:
                 raise RuntimeError("cannot reset an engine that still holds offloaded activations")
         for engine in _ENGINES.values():
             engine.close()
+        _ENGINES.clear()
+
+
+@atexit.register
+def _close_engines_at_exit() -> None:
+    # Release streams, events, staging memory and pinned host memory while the HIP runtime is
+    # still fully alive, instead of leaving them to process teardown. Handles that outlive
+    # this (graphs still referenced at exit) find their engine closed and do nothing.
+    with _ENGINES_LOCK:
+        for engine in _ENGINES.values():
+            try:
+                engine.close()
+            except Exception:
+                pass
         _ENGINES.clear()
