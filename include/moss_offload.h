@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 1
+#define MO_ABI_VERSION 2
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -43,9 +43,10 @@ extern "C" {
 #define MO_E_STATE 1004     /* call not valid in the engine's current state */
 
 /* Flags for mo_config.flags. */
-#define MO_FLAG_TIMING 0x1         /* time every D2H/H2D copy with HIP events            */
-#define MO_FLAG_KERNEL_COPY 0x2    /* move D2H/H2D with a copy kernel, not the DMA      */
-#define MO_FLAG_KERNEL_TIMING 0x4  /* time every pack/unpack launch with HIP events     */
+#define MO_FLAG_TIMING 0x1         /* KERNEL_COPY link: time every copy with HIP events   */
+#define MO_FLAG_KERNEL_COPY 0x2    /* move D2H/H2D with a copy kernel on HIP streams instead
+                                      of the SDMA engines (comparison; contends for CUs)   */
+#define MO_FLAG_KERNEL_TIMING 0x4  /* time every pack/unpack launch with HIP events       */
 
 /*
  * A strided tensor view on the device. `ptr` is the address of logical element (0,...,0),
@@ -69,7 +70,9 @@ typedef struct mo_config {
   uint64_t host_limit_bytes;    /* [0 = no limit] cap on pinned host memory             */
   uint64_t host_chunk_bytes;    /* [1 GiB] granularity of hipHostMalloc reservations   */
   uint32_t flags;               /* MO_FLAG_*                                          */
-  uint32_t copy_kernel_blocks;  /* [64] workgroups of the copy kernel (KERNEL_COPY)  */
+  uint32_t copy_kernel_blocks;  /* [16] workgroups of the copy kernel (KERNEL_COPY)  */
+  uint32_t d2h_engine;          /* [0 = first available] SDMA engine bit for D2H      */
+  uint32_t h2d_engine;          /* [0 = first available other than D2H's] for H2D     */
 } mo_config;
 
 /* Where one packed tensor lives: its group (one block's saves) and index in the group. */
@@ -90,8 +93,10 @@ typedef struct mo_stats {
   uint64_t prefetch_issued;    /* segments fetched ahead of their unpack              */
   uint64_t prefetch_hits;      /* segments already resident when unpack asked          */
   uint64_t restore_fetches;    /* segments fetched on demand by unpack                 */
-  double d2h_ms, h2d_ms;       /* summed copy durations (MO_FLAG_TIMING), completed only */
-  uint64_t timed_d2h_bytes, timed_h2d_bytes;
+  double d2h_ms, h2d_ms;       /* copy-engine busy time of completed copies (SDMA: host
+                                  clock at issue/completion; KERNEL_COPY: HIP events)  */
+  uint64_t timed_d2h_bytes, timed_h2d_bytes; /* bytes of those completed copies          */
+  uint64_t copy_failures;      /* copies the runtime reported as failed                 */
   double pack_ms, unpack_ms;   /* summed kernel durations (MO_FLAG_KERNEL_TIMING)         */
   uint64_t timed_pack_bytes, timed_unpack_bytes; /* payload bytes of those launches      */
   uint64_t timed_pack_launches, timed_unpack_launches;
@@ -164,6 +169,9 @@ int mo_reset_stats(mo_engine* engine);
 
 /* Release pinned chunks that hold no live payload. */
 int mo_trim(mo_engine* engine);
+
+/* Name of the host-link transport in use: "sdma" or "kernel". */
+const char* mo_link_name(mo_engine* engine);
 
 #ifdef __cplusplus
 }

@@ -1,31 +1,34 @@
-// Activation-offload engine: staging ring, pinned host pool, copy streams, restore ring and
-// the C ABI declared in include/moss_offload.h.
+// Activation-offload engine: staging ring, pinned host pool, restore ring and the C ABI
+// declared in include/moss_offload.h.
 //
 // Forward (replaces activation_offload.py:116-134, one pinned tensor + copy per save):
 //   mo_pack gathers each saved tensor into the open segment of the device staging ring on the
-//   caller's compute stream. A segment closes when its slot fills or the group (one block's
-//   saves) is committed: the compute stream records an event, the D2H stream waits for it and
-//   copies the whole segment into pinned host memory in one transfer. Before a slot is
-//   refilled, the compute stream waits (on the GPU, never on the host) for the slot's last D2H.
+//   caller's compute stream. A segment closes when its slot fills or its group (one block's
+//   saves) is committed; the link then copies the whole segment to pinned host memory in one
+//   transfer (SDMA engine by default). Before a slot is refilled the compute stream waits, on
+//   the GPU, for that slot's last D2H.
 // Backward (replaces activation_offload.py:136-147, wait_event + _restore_layout):
-//   mo_prefetch copies a group's segments into free restore slots on the H2D stream ahead of
-//   use. mo_unpack fetches whatever is missing, makes the compute stream wait for the H2D, and
-//   scatters each entry into its destination with the unpack kernel.
+//   mo_prefetch copies a group's segments into free restore slots ahead of use. mo_unpack
+//   fetches whatever is missing, makes the compute stream wait for the copy, and scatters each
+//   entry into its destination with the unpack kernel.
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
 #include <string.h>
 
 #include <algorithm>
+#include <chrono>
 #include <deque>
 #include <map>
 #include <memory>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
 #include "../../include/moss_offload.h"
 #include "mo_internal.h"
+#include "mo_link.h"
 
 namespace mo {
 namespace {
@@ -37,15 +40,21 @@ int fail(int code, const std::string& msg) {
   return code;
 }
 
-int hip_fail(hipError_t e, const char* what) {
-  g_error = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
-  return (int)e;
+int hip_fail(int e, const char* what) {
+  g_error = std::string(what) + ": " + hipGetErrorName((hipError_t)e) + " (" + hipGetErrorString((hipError_t)e) + ")";
+  return e;
 }
 
-#define MO_HIP(call)                              \
-  do {                                            \
-    hipError_t _e = (call);                       \
-    if (_e != hipSuccess) return hip_fail(_e, #call); \
+#define MO_HIP(call)                                       \
+  do {                                                     \
+    hipError_t _e = (call);                                \
+    if (_e != hipSuccess) return hip_fail((int)_e, #call); \
+  } while (0)
+
+#define MO_LINK(call)                          \
+  do {                                         \
+    int _rc = (call);                          \
+    if (_rc != 0) return hip_fail(_rc, #call); \
   } while (0)
 
 constexpr uint64_t kNone = UINT64_MAX;
@@ -103,8 +112,8 @@ class HostPool {
     }
     const uint64_t size = align_up(std::max(bytes, chunk_), 2ull << 20);
     if (limit_ && reserved_ + size > limit_) {
-      return fail(MO_E_HOST_OOM, "pinned host pool limit reached: reserved " + std::to_string(reserved_) +
-                                     " B + " + std::to_string(size) + " B > limit " + std::to_string(limit_) +
+      return fail(MO_E_HOST_OOM, "pinned host pool limit reached: reserved " + std::to_string(reserved_) + " B + " +
+                                     std::to_string(size) + " B > limit " + std::to_string(limit_) +
                                      " B (raise host_limit_bytes or offload less)");
     }
     void* p = nullptr;
@@ -192,6 +201,8 @@ class HostPool {
   uint64_t reserved_ = 0, in_use_ = 0, peak_ = 0;
 };
 
+char* host_alias(void* ctx, char* p) { return ((HostPool*)ctx)->device_alias(p); }
+
 // ------------------------------------------------------------------------------------------
 struct Piece {
   uint32_t entry;
@@ -206,10 +217,9 @@ struct Segment {
   uint64_t bytes = 0;
   std::vector<Piece> pieces;
   char* host = nullptr;
-  hipEvent_t d2h_done = nullptr;
-  hipEvent_t h2d_done = nullptr;
+  CopyRef d2h;  // the copy that filled `host`
+  CopyRef h2d;  // the last copy that read `host`
   bool committed = false;
-  bool h2d_issued = false;
   bool prefetched = false;
   int restore_slot = -1;
   uint64_t restore_gen = 0;
@@ -230,8 +240,7 @@ struct Group {
 struct StageSlot {
   char* dev = nullptr;
   uint64_t used = 0;
-  hipEvent_t free_ev = nullptr;
-  bool free_recorded = false;
+  int gate = -1;
 };
 
 struct RestoreSlot {
@@ -241,24 +250,22 @@ struct RestoreSlot {
   uint64_t gen = 0;
   uint64_t tick = 0;
   bool consumed = true;  // scattered at least once since fetched (or empty)
-  hipEvent_t ready = nullptr;
-  hipEvent_t consumed_ev = nullptr;
-  bool consumed_recorded = false;
+  int gate = -1;
 };
 
 struct PendingFree {
   char* host;
   uint64_t bytes;
-  hipEvent_t ev[2];
+  CopyRef copies[2];
 };
-
-enum TimingKind { kTimeD2H = 0, kTimeH2D = 1, kTimePack = 2, kTimeUnpack = 3 };
 
 struct Timing {
   hipEvent_t start, end;
   uint64_t bytes;
-  int kind;
+  bool pack;
 };
+
+bool idle(const CopyRef& c) { return !c || c->done(); }
 
 }  // namespace
 
@@ -266,8 +273,7 @@ struct Engine {
   int device = 0;
   mo_config cfg{};
   std::mutex mu;
-  hipStream_t d2h = nullptr, h2d = nullptr;
-  hipEvent_t ev_tmp = nullptr;
+  std::unique_ptr<Link> link;
   std::vector<StageSlot> stage;
   std::vector<RestoreSlot> restore;
   int stage_cur = 0;
@@ -277,48 +283,41 @@ struct Engine {
   int open_seg = -1;  // index into open_group->segs, or -1
   uint64_t next_group = 0;
   uint64_t gen_counter = 0, tick = 0;
-  std::vector<hipEvent_t> event_pool, timing_pool;
+  std::vector<hipEvent_t> timing_pool;
   std::deque<PendingFree> pending;
   std::deque<Timing> timings;
   mo_stats st{};
 
-  // ---- events ----
-  int new_event(hipEvent_t* ev) {
-    if (!event_pool.empty()) {
-      *ev = event_pool.back();
-      event_pool.pop_back();
+  // ---- pack/unpack kernel timing (MO_FLAG_KERNEL_TIMING) ----
+  struct KernelTimer : LaunchTimer {
+    Engine* e;
+    bool pack;
+    Timing cur{};
+    KernelTimer(Engine* engine, bool p) : e(engine), pack(p) {}
+    int before(hipStream_t s) override {
+      cur = Timing{nullptr, nullptr, 0, pack};
+      if (!(e->cfg.flags & MO_FLAG_KERNEL_TIMING)) return 0;
+      for (hipEvent_t* ev : {&cur.start, &cur.end}) {
+        if (!e->timing_pool.empty()) {
+          *ev = e->timing_pool.back();
+          e->timing_pool.pop_back();
+        } else {
+          hipError_t err = hipEventCreate(ev);
+          if (err != hipSuccess) return (int)err;
+        }
+      }
+      return (int)hipEventRecord(cur.start, s);
+    }
+    int after(hipStream_t s, uint64_t bytes) override {
+      if (!cur.start) return 0;
+      cur.bytes = bytes;
+      hipError_t err = hipEventRecord(cur.end, s);
+      if (err != hipSuccess) return (int)err;
+      e->timings.push_back(cur);
       return 0;
     }
-    MO_HIP(hipEventCreateWithFlags(ev, hipEventDisableTiming));
-    return 0;
-  }
-  void recycle(hipEvent_t ev) {
-    if (ev) event_pool.push_back(ev);
-  }
-  bool timed(int kind) const {
-    const bool copy = kind == kTimeD2H || kind == kTimeH2D;
-    return (cfg.flags & (copy ? MO_FLAG_TIMING : MO_FLAG_KERNEL_TIMING)) != 0;
-  }
-  int timing_begin(hipStream_t s, Timing& t) {
-    t.start = t.end = nullptr;
-    if (!timed(t.kind)) return 0;
-    for (hipEvent_t* e : {&t.start, &t.end}) {
-      if (!timing_pool.empty()) {
-        *e = timing_pool.back();
-        timing_pool.pop_back();
-      } else {
-        MO_HIP(hipEventCreate(e));
-      }
-    }
-    MO_HIP(hipEventRecord(t.start, s));
-    return 0;
-  }
-  int timing_end(hipStream_t s, Timing& t) {
-    if (!t.start) return 0;
-    MO_HIP(hipEventRecord(t.end, s));
-    timings.push_back(t);
-    return 0;
-  }
+  };
+
   void process_timings(bool wait) {
     while (!timings.empty()) {
       Timing& t = timings.front();
@@ -326,13 +325,14 @@ struct Engine {
       else if (hipEventQuery(t.end) != hipSuccess) break;
       float ms = 0.f;
       if (hipEventElapsedTime(&ms, t.start, t.end) == hipSuccess) {
-        switch (t.kind) {
-          case kTimeD2H: st.d2h_ms += ms; st.timed_d2h_bytes += t.bytes; break;
-          case kTimeH2D: st.h2d_ms += ms; st.timed_h2d_bytes += t.bytes; break;
-          case kTimePack:
-            st.pack_ms += ms; st.timed_pack_bytes += t.bytes; st.timed_pack_launches++; break;
-          default:
-            st.unpack_ms += ms; st.timed_unpack_bytes += t.bytes; st.timed_unpack_launches++; break;
+        if (t.pack) {
+          st.pack_ms += ms;
+          st.timed_pack_bytes += t.bytes;
+          st.timed_pack_launches++;
+        } else {
+          st.unpack_ms += ms;
+          st.timed_unpack_bytes += t.bytes;
+          st.timed_unpack_launches++;
         }
       }
       timing_pool.push_back(t.start);
@@ -341,76 +341,48 @@ struct Engine {
     }
   }
 
+  // A failed copy still releases whoever waits on it (no hang); report it at the next call.
+  uint64_t seen_failures = 0;
+  int check_link() {
+    LinkStats ls;
+    link->stats(&ls);
+    if (ls.failures > seen_failures) {
+      seen_failures = ls.failures;
+      return fail(MO_E_STATE, "a host-link copy failed; offloaded data may be lost");
+    }
+    return 0;
+  }
+
   // ---- deferred host frees ----
-  void process_pending(bool wait) {
+  int process_pending(bool wait) {
+    const auto deadline = std::chrono::steady_clock::now() + std::chrono::seconds(300);
     for (auto it = pending.begin(); it != pending.end();) {
-      bool done = true;
-      for (hipEvent_t e : it->ev) {
-        if (!e) continue;
-        if (wait) (void)hipEventSynchronize(e);
-        else if (hipEventQuery(e) != hipSuccess) done = false;
+      bool done = idle(it->copies[0]) && idle(it->copies[1]);
+      while (!done && wait) {
+        if (std::chrono::steady_clock::now() > deadline) return fail(MO_E_STATE, "copies did not finish in 300 s");
+        std::this_thread::sleep_for(std::chrono::microseconds(50));
+        done = idle(it->copies[0]) && idle(it->copies[1]);
       }
       if (done) {
         pool.free(it->host, it->bytes);
-        recycle(it->ev[0]);
-        recycle(it->ev[1]);
         it = pending.erase(it);
       } else {
         ++it;
       }
     }
+    return 0;
   }
-
-  // ---- link copies ----
-  int copy(char* dst, const char* src, uint64_t bytes, bool to_host, hipStream_t s) {
-    Timing t{};
-    t.bytes = bytes;
-    t.kind = to_host ? kTimeD2H : kTimeH2D;
-    if (int rc = timing_begin(s, t)) return rc;
-    if (cfg.flags & MO_FLAG_KERNEL_COPY) {
-      char* d = to_host ? pool.device_alias(dst) : dst;
-      const char* sp = to_host ? src : pool.device_alias((char*)src);
-      int rc = launch_link_copy(d, sp, bytes, cfg.copy_kernel_blocks, s);
-      if (rc) return hip_fail((hipError_t)rc, "link copy kernel launch");
-    } else {
-      MO_HIP(hipMemcpyAsync(dst, src, bytes, to_host ? hipMemcpyDeviceToHost : hipMemcpyHostToDevice, s));
-    }
-    return timing_end(s, t);
-  }
-
-  // Brackets each pack/unpack launch with timing events (MO_FLAG_KERNEL_TIMING).
-  struct KernelTimer : LaunchTimer {
-    Engine* e;
-    int kind;
-    Timing cur{};
-    KernelTimer(Engine* engine, int k) : e(engine), kind(k) {}
-    int before(hipStream_t s) override {
-      cur = Timing{};
-      cur.kind = kind;
-      return e->timing_begin(s, cur);
-    }
-    int after(hipStream_t s, uint64_t bytes) override {
-      cur.bytes = bytes;
-      return e->timing_end(s, cur);
-    }
-  };
 
   // ---- forward ----
   int close_segment(Launcher& L, hipStream_t stream) {
     if (!open_group || open_seg < 0) return 0;
-    if (int rc = L.flush()) return hip_fail((hipError_t)rc, "pack kernel launch");
+    if (int rc = L.flush()) return hip_fail(rc, "pack kernel launch");
     Segment& seg = open_group->segs[open_seg];
     StageSlot& slot = stage[seg.stage_slot];
     seg.bytes = slot.used - seg.stage_off;
     open_seg = -1;
     if (int rc = pool.alloc(seg.bytes, &seg.host)) return rc;
-    MO_HIP(hipEventRecord(ev_tmp, stream));
-    MO_HIP(hipStreamWaitEvent(d2h, ev_tmp, 0));
-    if (int rc = copy(seg.host, slot.dev + seg.stage_off, seg.bytes, true, d2h)) return rc;
-    if (int rc = new_event(&seg.d2h_done)) return rc;
-    MO_HIP(hipEventRecord(seg.d2h_done, d2h));
-    MO_HIP(hipEventRecord(slot.free_ev, d2h));
-    slot.free_recorded = true;
+    MO_LINK(link->d2h(seg.host, slot.dev + seg.stage_off, seg.bytes, stream, slot.gate, &seg.d2h));
     seg.committed = true;
     st.d2h_copies++;
     st.bytes_d2h += seg.bytes;
@@ -420,21 +392,20 @@ struct Engine {
   int advance_slot(hipStream_t stream) {
     stage_cur = (stage_cur + 1) % (int)stage.size();
     StageSlot& s = stage[stage_cur];
-    if (s.free_recorded) {
-      if (hipEventQuery(s.free_ev) != hipSuccess) st.stage_slot_busy++;
-      MO_HIP(hipStreamWaitEvent(stream, s.free_ev, 0));
-      st.stage_slot_waits++;
-    }
+    st.stage_slot_waits++;
+    MO_LINK(link->wait(s.gate, stream));
     s.used = 0;
     return 0;
   }
 
   int pack(const mo_tensor* ts, int n, hipStream_t stream, mo_ref* refs) {
+    if (int rc = check_link()) return rc;
     process_pending(false);
     std::vector<Canon> canons(n);
     std::string err;
     for (int i = 0; i < n; ++i) {
-      if (int rc = canonicalize(ts[i], canons[i], err)) return fail(rc, "mo_pack: tensor " + std::to_string(i) + ": " + err);
+      if (int rc = canonicalize(ts[i], canons[i], err))
+        return fail(rc, "mo_pack: tensor " + std::to_string(i) + ": " + err);
     }
     if (!open_group) {
       auto g = std::make_unique<Group>();
@@ -445,7 +416,7 @@ struct Engine {
       st.groups_created++;
     }
     Group& g = *open_group;
-    KernelTimer timer(this, kTimePack);
+    KernelTimer timer(this, true);
     Launcher L(true, stream, &timer);
     const uint64_t slot_bytes = cfg.stage_slot_bytes;
     for (int i = 0; i < n; ++i) {
@@ -466,10 +437,7 @@ struct Engine {
           if (int rc = advance_slot(stream)) return rc;
           continue;
         }
-        if (open_seg < 0 || g.segs[open_seg].stage_slot != stage_cur) {
-          if (open_seg >= 0) {
-            if (int rc = close_segment(L, stream)) return rc;
-          }
+        if (open_seg < 0) {
           Segment seg;
           seg.stage_slot = stage_cur;
           seg.stage_off = pos;
@@ -480,7 +448,8 @@ struct Engine {
         uint64_t take = std::min(remaining, space);
         if (take < remaining) take = take / kPieceAlign * kPieceAlign;
         KDesc kd;
-        if (int rc = make_kdesc(c, c.base, first, take, (uint64_t)(s.dev + pos), kd, err)) return fail(rc, "mo_pack: " + err);
+        if (int rc = make_kdesc(c, c.base, first, take, (uint64_t)(s.dev + pos), kd, err))
+          return fail(rc, "mo_pack: " + err);
         L.add(kd);
         seg.pieces.push_back(Piece{idx, first, take, pos - seg.stage_off});
         s.used = pos + take;
@@ -489,7 +458,7 @@ struct Engine {
         st.bytes_packed += take;
       }
     }
-    if (int rc = L.flush()) return hip_fail((hipError_t)rc, "pack kernel launch");
+    if (int rc = L.flush()) return hip_fail(rc, "pack kernel launch");
     st.pack_launches += L.launches();
     return 0;
   }
@@ -497,8 +466,7 @@ struct Engine {
   int commit(hipStream_t stream, uint64_t* gid) {
     *gid = kNone;
     if (!open_group) return 0;
-    KernelTimer timer(this, kTimePack);
-    Launcher L(true, stream, &timer);
+    Launcher L(true, stream);
     if (int rc = close_segment(L, stream)) return rc;
     open_group->open = false;
     *gid = open_group->id;
@@ -520,8 +488,8 @@ struct Engine {
     return r.group == g.id && r.seg == si && r.gen == seg.restore_gen;
   }
 
-  // Choose a restore slot to fill with segment `si` of group `g`.
-  // for_prefetch: only take slots that are empty or already consumed (never waste a prefetch).
+  // Choose a restore slot for segment `si` of group `g`. for_prefetch: only slots that are
+  // empty or already consumed (a prefetch never evicts data that is still waiting for use).
   int pick_slot(const Group& g, uint32_t si, bool for_prefetch) {
     int best = -1;
     for (int k = 0; k < (int)restore.size(); ++k) {
@@ -557,15 +525,9 @@ struct Engine {
     if (!seg.committed || !seg.host)
       return fail(MO_E_STATE, "group " + std::to_string(g.id) + " segment " + std::to_string(si) +
                                   " has no host copy (its D2H was never issued)");
-    if (r.consumed_recorded) MO_HIP(hipStreamWaitEvent(h2d, r.consumed_ev, 0));
-    if (seg.d2h_done) MO_HIP(hipStreamWaitEvent(h2d, seg.d2h_done, 0));
-    if (int rc = copy(r.dev, seg.host, seg.bytes, false, h2d)) return rc;
-    MO_HIP(hipEventRecord(r.ready, h2d));
-    if (!seg.h2d_done) {
-      if (int rc = new_event(&seg.h2d_done)) return rc;
-    }
-    MO_HIP(hipEventRecord(seg.h2d_done, h2d));
-    seg.h2d_issued = true;
+    CopyRef copy;
+    MO_LINK(link->h2d(r.dev, seg.host, seg.bytes, seg.d2h, r.gate, &copy));
+    seg.h2d = std::move(copy);
     r.group = g.id;
     r.seg = si;
     r.gen = ++gen_counter;
@@ -595,6 +557,7 @@ struct Engine {
   }
 
   int unpack(uint64_t gid, const uint64_t* dst, uint32_t n, hipStream_t stream) {
+    if (int rc = check_link()) return rc;
     process_pending(false);
     Group* g = find(gid);
     if (!g) return fail(MO_E_INVALID, "mo_unpack: unknown group " + std::to_string(gid));
@@ -622,8 +585,8 @@ struct Engine {
       }
       seg.prefetched = false;
       RestoreSlot& r = restore[k];
-      MO_HIP(hipStreamWaitEvent(stream, r.ready, 0));
-      KernelTimer timer(this, kTimeUnpack);
+      MO_LINK(link->wait(r.gate, stream));
+      KernelTimer timer(this, false);
       Launcher L(false, stream, &timer);
       for (const Piece& p : seg.pieces) {
         if (!dst[p.entry]) continue;
@@ -635,10 +598,9 @@ struct Engine {
         L.add(kd);
         st.bytes_unpacked += p.nbytes;
       }
-      if (int rc = L.flush()) return hip_fail((hipError_t)rc, "unpack kernel launch");
+      if (int rc = L.flush()) return hip_fail(rc, "unpack kernel launch");
       st.unpack_launches += L.launches();
-      MO_HIP(hipEventRecord(r.consumed_ev, stream));
-      r.consumed_recorded = true;
+      MO_LINK(link->consumed(r.gate, stream));
       r.consumed = true;
       r.tick = ++tick;
     }
@@ -654,12 +616,7 @@ struct Engine {
       open_seg = -1;
     }
     for (Segment& seg : g->segs) {
-      if (seg.host) {
-        pending.push_back(PendingFree{seg.host, seg.bytes, {seg.d2h_done, seg.h2d_done}});
-      } else {
-        recycle(seg.d2h_done);
-        recycle(seg.h2d_done);
-      }
+      if (seg.host) pending.push_back(PendingFree{seg.host, seg.bytes, {seg.d2h, seg.h2d}});
       if (seg.restore_slot >= 0) {
         RestoreSlot& r = restore[seg.restore_slot];
         if (r.group == g->id && r.gen == seg.restore_gen) {
@@ -669,20 +626,25 @@ struct Engine {
       }
     }
     groups.erase(gid);
-    process_pending(false);
-    return 0;
+    return process_pending(false);
   }
 
   int synchronize() {
-    MO_HIP(hipStreamSynchronize(d2h));
-    MO_HIP(hipStreamSynchronize(h2d));
-    process_pending(true);
+    MO_LINK(link->synchronize());
+    if (int rc = process_pending(true)) return rc;
     process_timings(true);
     return 0;
   }
 
   void fill_stats(mo_stats* out) {
     process_timings(false);
+    LinkStats ls;
+    link->stats(&ls);
+    st.d2h_ms = ls.d2h_ms;
+    st.h2d_ms = ls.h2d_ms;
+    st.timed_d2h_bytes = ls.d2h_done_bytes;
+    st.timed_h2d_bytes = ls.h2d_done_bytes;
+    st.copy_failures = ls.failures;
     st.groups_live = groups.size();
     uint64_t e = 0;
     for (auto& kv : groups) e += kv.second->entries.size();
@@ -693,6 +655,12 @@ struct Engine {
     *out = st;
   }
 
+  void reset_stats() {
+    process_timings(false);
+    link->reset_stats();
+    st = mo_stats{};
+  }
+
   int init(int dev, const mo_config* c) {
     device = dev;
     if (c) cfg = *c;
@@ -700,66 +668,58 @@ struct Engine {
     if (!cfg.stage_slots) cfg.stage_slots = 4;
     if (!cfg.restore_slots) cfg.restore_slots = 4;
     if (!cfg.host_chunk_bytes) cfg.host_chunk_bytes = 1ull << 30;
-    if (!cfg.copy_kernel_blocks) cfg.copy_kernel_blocks = 64;
+    if (!cfg.copy_kernel_blocks) cfg.copy_kernel_blocks = 16;
     if (cfg.stage_slot_bytes < 2 * kMinPiece || cfg.stage_slot_bytes % kPieceAlign)
       return fail(MO_E_INVALID, "stage_slot_bytes must be a multiple of 4096 and at least 2 MiB");
-    if (cfg.stage_slots < 2 || cfg.restore_slots < 2) return fail(MO_E_INVALID, "need at least 2 stage and 2 restore slots");
+    if (cfg.stage_slots < 2 || cfg.restore_slots < 2 || cfg.stage_slots + cfg.restore_slots > 64)
+      return fail(MO_E_INVALID, "need at least 2 stage and 2 restore slots, 64 in total at most");
     pool.configure(cfg.host_limit_bytes, cfg.host_chunk_bytes);
     DeviceGuard guard(device);
-    MO_HIP(hipStreamCreateWithFlags(&d2h, hipStreamNonBlocking));
-    MO_HIP(hipStreamCreateWithFlags(&h2d, hipStreamNonBlocking));
-    MO_HIP(hipEventCreateWithFlags(&ev_tmp, hipEventDisableTiming));
+    std::string err;
+    int status = 0;
+    if (cfg.flags & MO_FLAG_KERNEL_COPY) {
+      link = make_stream_link(device, cfg.copy_kernel_blocks, (cfg.flags & MO_FLAG_TIMING) != 0, host_alias, &pool,
+                              err, &status);
+    } else {
+      link = make_sdma_link(device, cfg.d2h_engine, cfg.h2d_engine, err, &status);
+    }
+    if (!link) return fail(status ? status : MO_E_STATE, "creating the host link failed: " + err);
     stage.resize(cfg.stage_slots);
     for (auto& s : stage) {
       MO_HIP(hipMalloc(&s.dev, cfg.stage_slot_bytes));
-      MO_HIP(hipEventCreateWithFlags(&s.free_ev, hipEventDisableTiming));
+      MO_LINK(link->new_gate(&s.gate));
     }
     restore.resize(cfg.restore_slots);
     for (auto& r : restore) {
       MO_HIP(hipMalloc(&r.dev, cfg.stage_slot_bytes));
-      MO_HIP(hipEventCreateWithFlags(&r.ready, hipEventDisableTiming));
-      MO_HIP(hipEventCreateWithFlags(&r.consumed_ev, hipEventDisableTiming));
+      MO_LINK(link->new_gate(&r.gate));
     }
     return 0;
   }
 
   void teardown() {
     DeviceGuard guard(device);
+    // Drain the link first: compute streams may wait on copies that are still queued.
+    if (link) (void)link->synchronize();
     (void)hipDeviceSynchronize();
-    for (auto& kv : groups)
-      for (Segment& seg : kv.second->segs) {
-        if (seg.d2h_done) (void)hipEventDestroy(seg.d2h_done);
-        if (seg.h2d_done) (void)hipEventDestroy(seg.h2d_done);
-      }
     groups.clear();
-    for (auto& p : pending)
-      for (hipEvent_t e : p.ev)
-        if (e) (void)hipEventDestroy(e);
+    (void)process_pending(true);
     pending.clear();
+    link.reset();
     for (auto& t : timings) {
       (void)hipEventDestroy(t.start);
       (void)hipEventDestroy(t.end);
     }
     timings.clear();
-    for (hipEvent_t e : event_pool) (void)hipEventDestroy(e);
     for (hipEvent_t e : timing_pool) (void)hipEventDestroy(e);
-    event_pool.clear();
     timing_pool.clear();
-    for (auto& s : stage) {
+    for (auto& s : stage)
       if (s.dev) (void)hipFree(s.dev);
-      if (s.free_ev) (void)hipEventDestroy(s.free_ev);
-    }
-    for (auto& r : restore) {
+    for (auto& r : restore)
       if (r.dev) (void)hipFree(r.dev);
-      if (r.ready) (void)hipEventDestroy(r.ready);
-      if (r.consumed_ev) (void)hipEventDestroy(r.consumed_ev);
-    }
     stage.clear();
     restore.clear();
     pool.release_all();
-    if (ev_tmp) (void)hipEventDestroy(ev_tmp);
-    if (d2h) (void)hipStreamDestroy(d2h);
-    if (h2d) (void)hipStreamDestroy(h2d);
   }
 };
 
@@ -800,7 +760,7 @@ static int run_copy(bool pack, const mo_tensor* ts, int n, uint64_t payload, con
       return fail(rc, "tensor " + std::to_string(i) + ": " + err);
     L.add(kd);
   }
-  if (int rc = L.flush()) return hip_fail((hipError_t)rc, pack ? "pack kernel launch" : "unpack kernel launch");
+  if (int rc = L.flush()) return hip_fail(rc, pack ? "pack kernel launch" : "unpack kernel launch");
   return 0;
 }
 
@@ -814,21 +774,21 @@ struct mo_engine {
 };
 
 #define MO_GUARD_BEGIN try {
-#define MO_GUARD_END                                               \
-  }                                                                \
-  catch (const std::exception& ex) {                               \
+#define MO_GUARD_END                                                          \
+  }                                                                           \
+  catch (const std::exception& ex) {                                          \
     return mo::fail(MO_E_STATE, std::string("internal error: ") + ex.what()); \
-  }                                                                \
-  catch (...) {                                                    \
-    return mo::fail(MO_E_STATE, "internal error");                 \
+  }                                                                           \
+  catch (...) {                                                               \
+    return mo::fail(MO_E_STATE, "internal error");                            \
   }
 
-#define MO_ENGINE_CALL(engine, expr)                         \
-  MO_GUARD_BEGIN                                             \
+#define MO_ENGINE_CALL(engine, expr)                           \
+  MO_GUARD_BEGIN                                               \
   if (!(engine)) return mo::fail(MO_E_INVALID, "null engine"); \
-  std::lock_guard<std::mutex> lock((engine)->e.mu);          \
-  mo::DeviceGuard guard((engine)->e.device);                 \
-  return (expr);                                             \
+  std::lock_guard<std::mutex> lock((engine)->e.mu);            \
+  mo::DeviceGuard guard((engine)->e.device);                   \
+  return (expr);                                               \
   MO_GUARD_END
 
 extern "C" {
@@ -864,7 +824,7 @@ int mo_link_copy(uint64_t dst, uint64_t src, uint64_t bytes, int direction, uint
   MO_GUARD_BEGIN
   (void)direction;
   int rc = mo::launch_link_copy((void*)dst, (const void*)src, bytes, blocks, (hipStream_t)stream);
-  if (rc) return mo::hip_fail((hipError_t)rc, "link copy kernel launch");
+  if (rc) return mo::hip_fail(rc, "link copy kernel launch");
   return 0;
   MO_GUARD_END
 }
@@ -925,7 +885,6 @@ int mo_group_info(mo_engine* engine, uint64_t group, uint32_t* entries, uint64_t
   MO_GUARD_BEGIN
   if (!engine) return mo::fail(MO_E_INVALID, "null engine");
   std::lock_guard<std::mutex> lock(engine->e.mu);
-  mo::DeviceGuard guard(engine->e.device);
   mo::Group* g = engine->e.find(group);
   if (!g) return mo::fail(MO_E_INVALID, "mo_group_info: unknown group " + std::to_string(group));
   if (entries) *entries = (uint32_t)g->entries.size();
@@ -933,7 +892,7 @@ int mo_group_info(mo_engine* engine, uint64_t group, uint32_t* entries, uint64_t
   if (d2h_complete) {
     int done = g->open ? 0 : 1;
     for (auto& seg : g->segs)
-      if (seg.d2h_done && hipEventQuery(seg.d2h_done) != hipSuccess) done = 0;
+      if (!mo::idle(seg.d2h)) done = 0;
     *d2h_complete = done;
   }
   return 0;
@@ -947,12 +906,15 @@ int mo_get_stats(mo_engine* engine, mo_stats* stats) {
   MO_ENGINE_CALL(engine, (engine->e.fill_stats(stats), 0));
 }
 
-int mo_reset_stats(mo_engine* engine) {
-  MO_ENGINE_CALL(engine, (engine->e.process_timings(false), engine->e.st = mo_stats{}, 0));
-}
+int mo_reset_stats(mo_engine* engine) { MO_ENGINE_CALL(engine, (engine->e.reset_stats(), 0)); }
 
 int mo_trim(mo_engine* engine) {
   MO_ENGINE_CALL(engine, (engine->e.process_pending(false), engine->e.pool.trim(), 0));
+}
+
+const char* mo_link_name(mo_engine* engine) {
+  if (!engine || !engine->e.link) return "";
+  return engine->e.link->name();
 }
 
 }  // extern "C"

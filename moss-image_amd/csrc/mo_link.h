@@ -1,0 +1,72 @@
+// Host-link transport of the engine: how a staging segment gets to pinned host memory and
+// back, and how the compute stream is ordered against those copies.
+//
+// Two implementations:
+//   SdmaLink    (default) the MI355X's SDMA copy engines through the HSA runtime
+//               (hsa_amd_memory_async_copy_on_engine). No compute unit is used, so copies
+//               overlap GEMM-heavy compute without slowing it. Ordering with HIP streams:
+//                 compute -> copy : the copy job waits for a HIP event (issuer thread),
+//                 copy -> copy    : HSA completion signal passed as a dependency,
+//                 copy -> compute : the completion handler publishes a generation number in
+//                                   coherent pinned memory; the stream hipStreamWaitValue32s.
+//   StreamLink  a copy kernel on dedicated HIP streams ordered with HIP events. Kept for
+//               comparison: shader copies contend with compute for compute units.
+//
+// A "gate" is the ordering point of one device slot (staging or restore): copies into or out
+// of the slot go through its gate, and the compute stream waits on the gate before it touches
+// the slot again.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#include <memory>
+#include <string>
+
+namespace mo {
+
+// Completion state of one copy, shared between segment bookkeeping and the transport.
+struct CopyState {
+  virtual ~CopyState() = default;
+  // The copy finished (or failed) and the transport holds no more references to it.
+  virtual bool done() const = 0;
+  virtual bool failed() const = 0;
+};
+using CopyRef = std::shared_ptr<CopyState>;
+
+struct LinkStats {
+  uint64_t d2h_bytes = 0, h2d_bytes = 0;        // issued
+  uint64_t d2h_done_bytes = 0, h2d_done_bytes = 0;  // completed and timed
+  double d2h_ms = 0, h2d_ms = 0;                // engine-busy time of completed copies
+  uint64_t failures = 0;
+};
+
+class Link {
+ public:
+  virtual ~Link() = default;
+  virtual int new_gate(int* gate) = 0;
+  // Copy device `src` to pinned host `dst` once the work enqueued so far on `compute` is done.
+  // Completion is published through `gate`.
+  virtual int d2h(void* dst, const void* src, uint64_t bytes, hipStream_t compute, int gate, CopyRef* out) = 0;
+  // Copy pinned host `src` to device `dst` once `after` (the D2H that filled src) finished and
+  // the gate's last consumer (see consumed()) finished. Completion is published through `gate`.
+  virtual int h2d(void* dst, const void* src, uint64_t bytes, const CopyRef& after, int gate, CopyRef* out) = 0;
+  // Make `compute` wait for the last copy published through `gate` (no-op if none).
+  virtual int wait(int gate, hipStream_t compute) = 0;
+  // Record that the slot behind `gate` is free for the next copy once `compute` reaches here.
+  virtual int consumed(int gate, hipStream_t compute) = 0;
+  // Block until every copy issued so far finished.
+  virtual int synchronize() = 0;
+  virtual void stats(LinkStats* out) = 0;
+  virtual void reset_stats() = 0;
+  virtual const char* name() const = 0;
+};
+
+// `status`/`err` receive the failure when a factory returns null.
+std::unique_ptr<Link> make_sdma_link(int device, uint32_t d2h_engine, uint32_t h2d_engine, std::string& err,
+                                     int* status);
+// `alias` maps a pinned host pointer to its device-visible address for the copy kernel.
+std::unique_ptr<Link> make_stream_link(int device, uint32_t copy_blocks, bool timing, char* (*alias)(void*, char*),
+                                       void* alias_ctx, std::string& err, int* status);
+
+}  // namespace mo

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 1
+MO_ABI_VERSION = 2
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -49,6 +49,8 @@ class MoConfig(ctypes.Structure):
         ("host_chunk_bytes", ctypes.c_uint64),
         ("flags", ctypes.c_uint32),
         ("copy_kernel_blocks", ctypes.c_uint32),
+        ("d2h_engine", ctypes.c_uint32),
+        ("h2d_engine", ctypes.c_uint32),
     ]
 
 
@@ -85,6 +87,7 @@ class MoStats(ctypes.Structure):
         ("h2d_ms", ctypes.c_double),
         ("timed_d2h_bytes", ctypes.c_uint64),
         ("timed_h2d_bytes", ctypes.c_uint64),
+        ("copy_failures", ctypes.c_uint64),
         ("pack_ms", ctypes.c_double),
         ("unpack_ms", ctypes.c_double),
         ("timed_pack_bytes", ctypes.c_uint64),
@@ -131,6 +134,7 @@ SIGNATURES: dict[str, tuple] = {
     "mo_get_stats": (ctypes.c_int, [ctypes.c_void_p, _P(MoStats)]),
     "mo_reset_stats": (ctypes.c_int, [ctypes.c_void_p]),
     "mo_trim": (ctypes.c_int, [ctypes.c_void_p]),
+    "mo_link_name": (ctypes.c_char_p, [ctypes.c_void_p]),
 }
 
 _lock = threading.Lock()
