@@ -356,7 +356,15 @@ def run(args) -> dict:
             configure_mode(model, mode, regime)
             engine = get_engine(device)
             engine.reset_stats()
-            seconds, peak = time_steps(model, opt, inputs, steps, warmup, f"{regime}/{mode}")
+            try:
+                seconds, peak = time_steps(model, opt, inputs, steps, warmup, f"{regime}/{mode}")
+            except RuntimeError as exc:  # e.g. the reference hooks exhausting pinned host memory
+                log(f"{regime}/{mode} failed: {exc}")
+                entry[mode] = {"error": str(exc).splitlines()[0]}
+                opt.zero_grad(set_to_none=True)
+                torch.cuda.synchronize()
+                torch._C._host_emptyCache()
+                continue
             record = {"s_per_it": seconds, "peak_device_bytes": peak}
             if mode == "engine":
                 engine.synchronize()
@@ -386,13 +394,13 @@ def run(args) -> dict:
             entry[mode] = record
         none = entry.get("none", {}).get("s_per_it")
         eng = entry.get("engine")
-        if none is not None and eng is not None:
+        if none is not None and eng is not None and "s_per_it" in eng:
             copy_s = eng["d2h_s_per_step"] + eng["h2d_s_per_step"]
             exposed = eng["s_per_it"] - none
             eng["hidden_fraction"] = min(1.0, max(0.0, 1.0 - exposed / copy_s)) if copy_s > 0 else None
             eng["exposed_s"] = exposed
         ref = entry.get("reference")
-        if none is not None and ref is not None:
+        if none is not None and ref is not None and "s_per_it" in ref:
             ref["exposed_s"] = ref["s_per_it"] - none
         result["regimes"][regime] = entry
     return result
