@@ -321,7 +321,15 @@ def run(args) -> dict:
     device = torch.device("cuda", 0)
     props = torch.cuda.get_device_properties(device)
     log(f"device {props.name}, {props.total_memory / 2**30:.0f} GiB, host cores {os.cpu_count()}")
-    configure(timing=True, kernel_timing=True)
+    configure(
+        timing=True,
+        kernel_timing=True,
+        stage_slots=args.stage_slots,
+        restore_slots=args.restore_slots,
+        stage_slot_bytes=args.slot_mib << 20,
+        staged_restore=not args.no_staged_restore,
+        kernel_copy=args.kernel_copy,
+    )
     model = build_model(device, args.layers)
     inputs = make_inputs(device)
     params = [p for p in model.parameters() if p.requires_grad]
@@ -417,6 +425,11 @@ def main() -> int:
     parser.add_argument("--modes", default="none,engine,reference")
     parser.add_argument("--layers", type=int, default=CONFIG3["num_layers"])
     parser.add_argument("--no-parity", action="store_true")
+    parser.add_argument("--stage-slots", type=int, default=4)
+    parser.add_argument("--restore-slots", type=int, default=4)
+    parser.add_argument("--slot-mib", type=int, default=64)
+    parser.add_argument("--no-staged-restore", action="store_true")
+    parser.add_argument("--kernel-copy", action="store_true", help="copy kernel on HIP streams instead of SDMA")
     parser.add_argument("--cpu-threads", type=int, default=16)
     parser.add_argument("--cpu-budget", type=float, default=15.0)
     args = parser.parse_args()

@@ -47,6 +47,8 @@ extern "C" {
 #define MO_FLAG_KERNEL_COPY 0x2    /* move D2H/H2D with a copy kernel on HIP streams instead
                                       of the SDMA engines (comparison; contends for CUs)   */
 #define MO_FLAG_KERNEL_TIMING 0x4  /* time every pack/unpack launch with HIP events       */
+#define MO_FLAG_NO_STAGED_RESTORE 0x8 /* always restore through H2D, even when a segment is
+                                         still intact in its staging slot                  */
 
 /*
  * A strided tensor view on the device. `ptr` is the address of logical element (0,...,0),
@@ -93,6 +95,8 @@ typedef struct mo_stats {
   uint64_t prefetch_issued;    /* segments fetched ahead of their unpack              */
   uint64_t prefetch_hits;      /* segments already resident when unpack asked          */
   uint64_t restore_fetches;    /* segments fetched on demand by unpack                 */
+  uint64_t staged_hits;        /* segments unpacked from their staging slot (no H2D)   */
+  uint64_t bytes_staged;       /* bytes of those segments                              */
   double d2h_ms, h2d_ms;       /* copy-engine busy time of completed copies (SDMA: host
                                   clock at issue/completion; KERNEL_COPY: HIP events)  */
   uint64_t timed_d2h_bytes, timed_h2d_bytes; /* bytes of those completed copies          */
@@ -144,7 +148,8 @@ int mo_pack(mo_engine* engine, const mo_tensor* tensors, int n, uint64_t stream,
 int mo_commit(mo_engine* engine, uint64_t stream, uint64_t* group);
 
 /* Enqueue H2D copies of a committed group into free restore slots (as many segments as fit),
- * so a later mo_unpack finds them resident. Never blocks the host. */
+ * so a later mo_unpack on `stream` finds them resident. Segments still intact in their staging
+ * slot (and packed on `stream`) are skipped: unpack reads them there. Never blocks the host. */
 int mo_prefetch(mo_engine* engine, uint64_t group, uint64_t stream);
 
 /* Restore entries of a group: dst[i] is the device address for entry i (0 = skip it), laid out

@@ -214,6 +214,9 @@ struct Piece {
 struct Segment {
   int stage_slot = -1;
   uint64_t stage_off = 0;
+  uint64_t stage_gen = 0;          // fill generation of the staging slot when packed
+  hipStream_t pack_stream = nullptr;
+  bool one_stream = true;          // every piece was packed on pack_stream
   uint64_t bytes = 0;
   std::vector<Piece> pieces;
   char* host = nullptr;
@@ -240,6 +243,7 @@ struct Group {
 struct StageSlot {
   char* dev = nullptr;
   uint64_t used = 0;
+  uint64_t fill_gen = 0;  // bumped every time the slot is reset for refilling
   int gate = -1;
 };
 
@@ -395,7 +399,16 @@ struct Engine {
     st.stage_slot_waits++;
     MO_LINK(link->wait(s.gate, stream));
     s.used = 0;
+    s.fill_gen++;
     return 0;
+  }
+
+  // A committed segment whose staging bytes have not been overwritten since it was packed on
+  // `stream` can be unpacked from the staging slot itself: no H2D needed. (Its D2H still ran,
+  // so the host copy remains the reference once the slot is refilled.)
+  bool staged(const Segment& seg, hipStream_t stream) const {
+    return (cfg.flags & MO_FLAG_NO_STAGED_RESTORE) == 0 && seg.committed && seg.stage_slot >= 0 &&
+           stage[seg.stage_slot].fill_gen == seg.stage_gen && seg.one_stream && seg.pack_stream == stream;
   }
 
   int pack(const mo_tensor* ts, int n, hipStream_t stream, mo_ref* refs) {
@@ -441,10 +454,13 @@ struct Engine {
           Segment seg;
           seg.stage_slot = stage_cur;
           seg.stage_off = pos;
+          seg.stage_gen = s.fill_gen;
+          seg.pack_stream = stream;
           g.segs.push_back(std::move(seg));
           open_seg = (int)g.segs.size() - 1;
         }
         Segment& seg = g.segs[open_seg];
+        if (seg.pack_stream != stream) seg.one_stream = false;
         uint64_t take = std::min(remaining, space);
         if (take < remaining) take = take / kPieceAlign * kPieceAlign;
         KDesc kd;
@@ -540,13 +556,13 @@ struct Engine {
     return 0;
   }
 
-  int prefetch(uint64_t gid) {
+  int prefetch(uint64_t gid, hipStream_t stream) {
     process_pending(false);
     Group* g = find(gid);
     if (!g) return fail(MO_E_INVALID, "mo_prefetch: unknown group " + std::to_string(gid));
     if (g->open) return 0;
     for (uint32_t si = 0; si < g->segs.size(); ++si) {
-      if (resident(*g, si)) continue;
+      if (resident(*g, si) || staged(g->segs[si], stream)) continue;
       const int k = pick_slot(*g, si, true);
       if (k < 0) break;
       if (int rc = fetch(*g, si, k)) return rc;
@@ -574,18 +590,28 @@ struct Engine {
       bool any = false;
       for (const Piece& p : seg.pieces) any = any || dst[p.entry] != 0;
       if (!any) continue;
-      int k = seg.restore_slot;
+      RestoreSlot* r = nullptr;
+      const char* src = nullptr;
       if (resident(*g, si)) {
         if (seg.prefetched) st.prefetch_hits++;
+        r = &restore[seg.restore_slot];
+      } else if (staged(seg, stream)) {
+        // Still in the staging slot, stream-ordered after its pack kernels: no H2D.
+        src = stage[seg.stage_slot].dev + seg.stage_off;
+        st.staged_hits++;
+        st.bytes_staged += seg.bytes;
       } else {
-        k = pick_slot(*g, si, false);
+        const int k = pick_slot(*g, si, false);
         if (k < 0) return fail(MO_E_STATE, "mo_unpack: no restore slot available");
         if (int rc = fetch(*g, si, k)) return rc;
         st.restore_fetches++;
+        r = &restore[k];
       }
       seg.prefetched = false;
-      RestoreSlot& r = restore[k];
-      MO_LINK(link->wait(r.gate, stream));
+      if (r) {
+        MO_LINK(link->wait(r->gate, stream));
+        src = r->dev;
+      }
       KernelTimer timer(this, false);
       Launcher L(false, stream, &timer);
       for (const Piece& p : seg.pieces) {
@@ -593,16 +619,18 @@ struct Engine {
         KDesc kd;
         const Canon& c = g->entries[p.entry].canon;
         if (dst[p.entry] % c.eb != 0) return fail(MO_E_INVALID, "mo_unpack: misaligned destination");
-        if (int rc = make_kdesc(c, dst[p.entry], p.first, p.nbytes, (uint64_t)(r.dev + p.seg_off), kd, err))
+        if (int rc = make_kdesc(c, dst[p.entry], p.first, p.nbytes, (uint64_t)(src + p.seg_off), kd, err))
           return fail(rc, "mo_unpack: " + err);
         L.add(kd);
         st.bytes_unpacked += p.nbytes;
       }
       if (int rc = L.flush()) return hip_fail(rc, "unpack kernel launch");
       st.unpack_launches += L.launches();
-      MO_LINK(link->consumed(r.gate, stream));
-      r.consumed = true;
-      r.tick = ++tick;
+      if (r) {
+        MO_LINK(link->consumed(r->gate, stream));
+        r->consumed = true;
+        r->tick = ++tick;
+      }
     }
     return 0;
   }
@@ -870,8 +898,7 @@ int mo_commit(mo_engine* engine, uint64_t stream, uint64_t* group) {
 }
 
 int mo_prefetch(mo_engine* engine, uint64_t group, uint64_t stream) {
-  (void)stream;
-  MO_ENGINE_CALL(engine, engine->e.prefetch(group));
+  MO_ENGINE_CALL(engine, engine->e.prefetch(group, (hipStream_t)stream));
 }
 
 int mo_unpack(mo_engine* engine, uint64_t group, const uint64_t* dst, uint32_t n, uint64_t stream) {

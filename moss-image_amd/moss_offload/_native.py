@@ -26,6 +26,7 @@ MO_E_STATE = 1004
 MO_FLAG_TIMING = 0x1
 MO_FLAG_KERNEL_COPY = 0x2
 MO_FLAG_KERNEL_TIMING = 0x4
+MO_FLAG_NO_STAGED_RESTORE = 0x8
 
 NO_GROUP = (1 << 64) - 1
 
@@ -81,6 +82,8 @@ class MoStats(ctypes.Structure):
             "prefetch_issued",
             "prefetch_hits",
             "restore_fetches",
+            "staged_hits",
+            "bytes_staged",
         )
     ] + [
         ("d2h_ms", ctypes.c_double),

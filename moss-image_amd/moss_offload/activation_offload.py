@@ -145,6 +145,7 @@ class _ActivationOffload:
         }
         self.dedupe = self.engine.config.dedupe and StorageWeakRef is not None
         self._seen: dict[tuple, tuple] = {}
+        self._shared: set[int] = set()  # groups holding saves made more than once
         self._hooks = torch.autograd.graph.saved_tensors_hooks(self.pack, self.unpack)
         self._block_handles: list = []
 
@@ -168,9 +169,13 @@ class _ActivationOffload:
             self._seen.clear()
         stream = torch.cuda.current_stream(self.device).cuda_stream
         last = self.engine.commit(stream)
-        if last is not None and self.engine.config.prefetch and exc[0] is None:
-            # Backward starts with the last group: start bringing it back now.
-            self.engine.prefetch(last, stream)
+        if self.engine.config.prefetch and exc[0] is None:
+            # Backward starts with the last group, and with every group holding a save the
+            # forward made repeatedly (e.g. one RoPE table checkpointed with every block): start
+            # bringing them back now. Segments still in the staging ring are skipped.
+            for gid in ([last] if last is not None else []) + sorted(self._shared - {last}, reverse=True):
+                self.engine.prefetch(gid, stream)
+        self._shared.clear()
         return False
 
     def _boundary(self, module, args):
@@ -210,6 +215,7 @@ class _ActivationOffload:
             if hit is not None:
                 ref, version, gid, idx = hit
                 if not ref.expired() and version == tensor._version and self.engine.acquire(gid, idx):
+                    self._shared.add(gid)
                     return _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
         stream = torch.cuda.current_stream(device).cuda_stream
         gid, idx = self.engine.pack(source, stream)

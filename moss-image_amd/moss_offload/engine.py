@@ -40,7 +40,10 @@ class EngineConfig:
     timing: bool = False
     kernel_timing: bool = False
     kernel_copy: bool = False
-    copy_kernel_blocks: int = 64
+    copy_kernel_blocks: int = 16
+    d2h_engine: int = 0
+    h2d_engine: int = 0
+    staged_restore: bool = True
     prefetch: bool = True
     dedupe: bool = True
 
@@ -55,8 +58,11 @@ class EngineConfig:
             (_native.MO_FLAG_TIMING if self.timing else 0)
             | (_native.MO_FLAG_KERNEL_COPY if self.kernel_copy else 0)
             | (_native.MO_FLAG_KERNEL_TIMING if self.kernel_timing else 0)
+            | (0 if self.staged_restore else _native.MO_FLAG_NO_STAGED_RESTORE)
         )
         cfg.copy_kernel_blocks = self.copy_kernel_blocks
+        cfg.d2h_engine = self.d2h_engine
+        cfg.h2d_engine = self.h2d_engine
         return cfg
 
 
@@ -252,6 +258,10 @@ class OffloadEngine:
     def live_groups(self) -> int:
         with self._lock:
             return len(self._groups)
+
+    def link_name(self) -> str:
+        with self._lock:
+            return self._lib.mo_link_name(self._handle).decode()
 
     def close(self) -> None:
         with self._lock:

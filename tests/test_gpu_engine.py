@@ -54,11 +54,13 @@ def _restore_and_check(engine, handles, device, order):
         assert_bitwise(restored, original)
 
 
+@pytest.mark.parametrize("staged", [False, True])
 @pytest.mark.parametrize("kernel_copy", [False, True])
 @pytest.mark.parametrize("seed", [0, 1])
-def test_groups_round_trip_lifo(seed, kernel_copy) -> None:
+def test_groups_round_trip_lifo(seed, kernel_copy, staged) -> None:
     device = torch.device("cuda", 0)
-    engine = _engine(kernel_copy=kernel_copy, timing=True)
+    engine = _engine(kernel_copy=kernel_copy, timing=True, staged_restore=staged)
+    assert engine.link_name() == ("kernel" if kernel_copy else "sdma")
     rng = random.Random(seed)
     stream = torch.cuda.current_stream(device).cuda_stream
     handles = []
@@ -80,6 +82,9 @@ def test_groups_round_trip_lifo(seed, kernel_copy) -> None:
     assert stats["bytes_unpacked"] == stats["bytes_packed"]
     assert stats["stage_slot_waits"] > 0  # the ring wrapped
     assert stats["prefetch_hits"] > 0
+    assert stats["copy_failures"] == 0
+    # the newest segments are still in the staging ring at backward start
+    assert (stats["staged_hits"] > 0) == staged
     for _, gid, idx in handles:
         engine.drop(gid, idx)
     engine.synchronize()
