@@ -391,7 +391,10 @@ def run(args) -> dict:
                     unpack_avg_launch_us=st["unpack_ms"] * 1e3 / max(st["timed_unpack_launches"], 1),
                     pack_bytes_per_launch=st["timed_pack_bytes"] / max(st["timed_pack_launches"], 1),
                     unpack_bytes_per_launch=st["timed_unpack_bytes"] / max(st["timed_unpack_launches"], 1),
-                    stage_slot_busy=st["stage_slot_busy"],
+                    host_blocks=st["host_blocks"],
+                    host_block_ms=st["host_block_ms"],
+                    staged_hits=st["staged_hits"],
+                    bytes_staged=st["bytes_staged"],
                     prefetch_hits=st["prefetch_hits"],
                     restore_fetches=st["restore_fetches"],
                     host_pinned_peak_bytes=st["host_bytes_peak"],

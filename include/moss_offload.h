@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 2
+#define MO_ABI_VERSION 3
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -90,8 +90,9 @@ typedef struct mo_stats {
   uint64_t bytes_d2h, bytes_h2d;          /* bytes over the host link                  */
   uint64_t pack_launches, unpack_launches, d2h_copies, h2d_copies;
   uint64_t host_bytes_in_use, host_bytes_peak, host_bytes_reserved;
-  uint64_t stage_slot_waits;   /* compute stream told to wait for a staging slot's D2H */
-  uint64_t stage_slot_busy;    /* ... while that D2H was still running (a likely stall) */
+  uint64_t stage_slot_waits;   /* staging slots reused (each ordered after its last D2H) */
+  uint64_t host_blocks;        /* engine calls that blocked the host for a copy          */
+  double host_block_ms;        /* time spent blocked in them                             */
   uint64_t prefetch_issued;    /* segments fetched ahead of their unpack              */
   uint64_t prefetch_hits;      /* segments already resident when unpack asked          */
   uint64_t restore_fetches;    /* segments fetched on demand by unpack                 */

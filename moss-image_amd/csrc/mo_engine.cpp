@@ -5,12 +5,12 @@
 //   mo_pack gathers each saved tensor into the open segment of the device staging ring on the
 //   caller's compute stream. A segment closes when its slot fills or its group (one block's
 //   saves) is committed; the link then copies the whole segment to pinned host memory in one
-//   transfer (SDMA engine by default). Before a slot is refilled the compute stream waits, on
-//   the GPU, for that slot's last D2H.
+//   transfer (SDMA engine by default). Pack kernels that refill a slot are enqueued only once
+//   that slot's last D2H finished.
 // Backward (replaces activation_offload.py:136-147, wait_event + _restore_layout):
 //   mo_prefetch copies a group's segments into free restore slots ahead of use. mo_unpack
-//   fetches whatever is missing, makes the compute stream wait for the copy, and scatters each
-//   entry into its destination with the unpack kernel.
+//   fetches whatever is missing, orders the unpack kernel after that copy, and scatters each
+//   entry into its destination. Segments still intact in their staging slot skip the H2D.
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
 #include <string.h>
@@ -673,6 +673,8 @@ struct Engine {
     st.timed_d2h_bytes = ls.d2h_done_bytes;
     st.timed_h2d_bytes = ls.h2d_done_bytes;
     st.copy_failures = ls.failures;
+    st.host_blocks = ls.host_blocks;
+    st.host_block_ms = ls.host_block_ms;
     st.groups_live = groups.size();
     uint64_t e = 0;
     for (auto& kv : groups) e += kv.second->entries.size();

@@ -7,6 +7,8 @@
 #include <hsa/hsa_ext_amd.h>
 #include <stdint.h>
 
+#include <sys/prctl.h>
+
 #include <atomic>
 #include <chrono>
 #include <condition_variable>
@@ -26,18 +28,25 @@ int64_t now_ns() {
       .count();
 }
 
-constexpr int kMaxGates = 64;
-constexpr int kFlagStride = 16;  // uint32 per gate: one 64-byte line each
+constexpr int64_t kWaitLimitNs = 300ll * 1000000000ll;  // a copy that takes longer is reported as failed
 
-// Atomically raise *flag to at least `value` (flags only move forward).
-void publish(uint32_t* flag, uint32_t value) {
-  uint32_t cur = __atomic_load_n(flag, __ATOMIC_RELAXED);
-  while (cur < value && !__atomic_compare_exchange_n(flag, &cur, value, true, __ATOMIC_RELEASE, __ATOMIC_RELAXED)) {
+// Short polling sleep. The default 50 us timer slack of a Linux thread would dominate a 5 us
+// sleep, so each polling thread lowers its own slack once.
+void short_sleep() {
+  thread_local bool tuned = false;
+  if (!tuned) {
+    prctl(PR_SET_TIMERSLACK, 1000UL, 0, 0, 0);
+    tuned = true;
   }
+  std::this_thread::sleep_for(std::chrono::microseconds(5));
 }
 
 // ==========================================================================================
 // SDMA link
+//
+// Ordering uses only host-visible completion: HIP events (queried) for GPU work, HSA signal
+// values (loaded) for SDMA copies. No GPU queue ever waits on memory the host writes, so a
+// missed wake-up can only delay the host, never stall the GPU; every host wait is bounded.
 
 class SdmaLink;
 
@@ -51,38 +60,33 @@ struct EventHold {
 using EventRef = std::shared_ptr<EventHold>;
 
 struct SdmaCopy : CopyState {
-  hsa_signal_t sig{0};
-  std::atomic<bool> handled{false};
+  std::atomic<bool> finished{false};
   std::atomic<bool> fail{false};
   bool to_host = true;
   uint64_t bytes = 0;
   int64_t issue_ns = 0;
-  uint32_t* flag = nullptr;
-  uint32_t value = 0;
-  SdmaLink* link = nullptr;
-  std::shared_ptr<SdmaCopy> self;  // keeps the copy alive until its completion handler ran
-  int64_t retired_ns = 0;
-  ~SdmaCopy() override {
-    if (sig.handle) hsa_signal_destroy(sig);
-  }
-  bool done() const override { return handled.load(std::memory_order_acquire); }
+  bool done() const override { return finished.load(std::memory_order_acquire); }
   bool failed() const override { return fail.load(std::memory_order_acquire); }
 };
+using SdmaRef = std::shared_ptr<SdmaCopy>;
 
 struct Job {
-  std::shared_ptr<SdmaCopy> copy;
+  SdmaRef copy;
   void* dst = nullptr;
   const void* src = nullptr;
-  EventRef wait;                    // issue after this HIP event completed
-  std::shared_ptr<SdmaCopy> after;  // and after this copy completed
+  EventRef wait;  // issue after this HIP event completed
+  SdmaRef after;  // and after this copy completed
+};
+
+struct InFlight {
+  SdmaRef copy;
+  hsa_signal_t sig;
 };
 
 struct GateState {
-  uint32_t gen = 0;
-  EventRef consumed;
+  SdmaRef last;      // the last copy through the gate
+  EventRef consumed;  // the slot's last consumer on a compute stream
 };
-
-hsa_status_t find_agents(hsa_agent_t agent, void* data);
 
 struct AgentSearch {
   uint32_t bus = 0, dev = 0, domain = 0;
@@ -123,8 +127,8 @@ class SdmaLink : public Link {
       return MO_E_STATE;
     }
     hsa_inited_ = true;
-    AgentSearch s;
     // Match the HIP device to its HSA agent by PCI location (falls back to the ordinal).
+    AgentSearch s;
     int v = 0;
     if (hipDeviceGetAttribute(&v, hipDeviceAttributePciBusId, device) == hipSuccess) s.bus = (uint32_t)v;
     if (hipDeviceGetAttribute(&v, hipDeviceAttributePciDeviceId, device) == hipSuccess) s.dev = (uint32_t)v;
@@ -149,22 +153,11 @@ class SdmaLink : public Link {
     }
     e_d2h_ = pick(d2h_mask, d2h_engine, 0);
     e_h2d_ = pick(h2d_mask, h2d_engine, e_d2h_);
-    void* p = nullptr;
-    if (hipHostMalloc(&p, sizeof(uint32_t) * kFlagStride * kMaxGates, hipHostMallocCoherent) != hipSuccess) {
-      err = "hipHostMalloc of gate flags failed";
-      return MO_E_STATE;
-    }
-    flags_ = (uint32_t*)p;
-    for (int i = 0; i < kFlagStride * kMaxGates; ++i) flags_[i] = 0;
     worker_ = std::thread([this] { run(); });
     return 0;
   }
 
-  uint32_t d2h_engine() const { return e_d2h_; }
-  uint32_t h2d_engine() const { return e_h2d_; }
-
   int new_gate(int* gate) override {
-    if ((int)gates_.size() >= kMaxGates) return MO_E_INVALID;
     gates_.emplace_back();
     *gate = (int)gates_.size() - 1;
     return 0;
@@ -175,22 +168,21 @@ class SdmaLink : public Link {
     if (int rc = take_event(&ev)) return rc;
     hipError_t e = hipEventRecord(ev->ev, compute);
     if (e != hipSuccess) return (int)e;
-    auto copy = make_copy(true, bytes, gate);
-    if (!copy) return MO_E_STATE;
+    auto copy = make_copy(true, bytes);
     Job job;
     job.copy = copy;
     job.dst = dst;
     job.src = src;
     job.wait = std::move(ev);
     enqueue(std::move(job));
+    gates_[gate].last = copy;
     d2h_bytes_ += bytes;
     *out = copy;
     return 0;
   }
 
   int h2d(void* dst, const void* src, uint64_t bytes, const CopyRef& after, int gate, CopyRef* out) override {
-    auto copy = make_copy(false, bytes, gate);
-    if (!copy) return MO_E_STATE;
+    auto copy = make_copy(false, bytes);
     Job job;
     job.copy = copy;
     job.dst = dst;
@@ -198,15 +190,26 @@ class SdmaLink : public Link {
     job.wait = gates_[gate].consumed;
     job.after = std::dynamic_pointer_cast<SdmaCopy>(after);
     enqueue(std::move(job));
+    gates_[gate].last = copy;
     h2d_bytes_ += bytes;
     *out = copy;
     return 0;
   }
 
+  // Host-side: return once the gate's last copy finished. The caller enqueues the dependent
+  // GPU work afterwards, so stream order does the rest.
   int wait(int gate, hipStream_t compute) override {
-    const uint32_t gen = gates_[gate].gen;
-    if (gen == 0) return 0;
-    return (int)hipStreamWaitValue32(compute, flag(gate), gen, hipStreamWaitValueGte, 0xFFFFFFFFu);
+    (void)compute;
+    const SdmaRef& c = gates_[gate].last;
+    if (!c || c->done()) return 0;
+    const int64_t t0 = now_ns();
+    while (!c->done()) {
+      if (now_ns() - t0 > kWaitLimitNs) return MO_E_STATE;
+      short_sleep();
+    }
+    host_blocks_++;
+    host_block_ns_ += (uint64_t)(now_ns() - t0);
+    return c->failed() ? MO_E_STATE : 0;
   }
 
   int consumed(int gate, hipStream_t compute) override {
@@ -219,16 +222,15 @@ class SdmaLink : public Link {
   }
 
   int synchronize() override {
-    const int64_t deadline = now_ns() + 300ll * 1000000000ll;
+    const int64_t t0 = now_ns();
     for (;;) {
       {
         std::lock_guard<std::mutex> lock(mu_);
-        if (queue_.empty() && busy_ == 0 && completed_.load() == issued_.load()) break;
+        if (queue_.empty() && holding_ == 0 && inflight_count_.load() == 0) break;
       }
-      if (now_ns() > deadline) return MO_E_STATE;
-      std::this_thread::sleep_for(std::chrono::microseconds(50));
+      if (now_ns() - t0 > kWaitLimitNs) return MO_E_STATE;
+      short_sleep();
     }
-    sweep();
     return 0;
   }
 
@@ -240,10 +242,13 @@ class SdmaLink : public Link {
     out->d2h_ms = busy_ns_[0].load() / 1e6;
     out->h2d_ms = busy_ns_[1].load() / 1e6;
     out->failures = failures_.load();
+    out->host_blocks = host_blocks_;
+    out->host_block_ms = host_block_ns_ / 1e6;
   }
 
   void reset_stats() override {
     d2h_bytes_ = h2d_bytes_ = 0;
+    host_blocks_ = host_block_ns_ = 0;
     for (int i = 0; i < 2; ++i) {
       done_bytes_[i] = 0;
       busy_ns_[i] = 0;
@@ -257,31 +262,6 @@ class SdmaLink : public Link {
     ev_pool_.push_back(ev);
   }
 
-  // Completion handler (HSA async-event thread): publish, account, retire. No HIP calls.
-  static bool on_done(hsa_signal_value_t value, void* arg) {
-    auto* c = (SdmaCopy*)arg;
-    SdmaLink* link = c->link;
-    if (value < 0) {
-      c->fail.store(true, std::memory_order_release);
-      link->failures_++;
-    }
-    const int dir = c->to_host ? 0 : 1;
-    const int64_t t = now_ns();
-    const int64_t prev = link->last_done_ns_[dir].exchange(t);
-    const int64_t start = c->issue_ns > prev ? c->issue_ns : prev;
-    link->busy_ns_[dir] += t > start ? (uint64_t)(t - start) : 0;
-    link->done_bytes_[dir] += c->bytes;
-    if (c->flag) publish(c->flag, c->value);
-    c->handled.store(true, std::memory_order_release);
-    {
-      std::lock_guard<std::mutex> lock(link->retire_mu_);
-      c->retired_ns = t;
-      link->retired_.push_back(std::move(c->self));
-    }
-    link->completed_++;
-    return false;  // one-shot
-  }
-
  private:
   static uint32_t pick(uint32_t mask, uint32_t want, uint32_t avoid) {
     if (want && (mask & want)) return want & (~want + 1);
@@ -290,16 +270,10 @@ class SdmaLink : public Link {
     return mask & (~mask + 1);
   }
 
-  uint32_t* flag(int gate) { return flags_ + gate * kFlagStride; }
-
-  std::shared_ptr<SdmaCopy> make_copy(bool to_host, uint64_t bytes, int gate) {
+  SdmaRef make_copy(bool to_host, uint64_t bytes) {
     auto c = std::make_shared<SdmaCopy>();
-    if (hsa_signal_create(1, 0, nullptr, &c->sig) != HSA_STATUS_SUCCESS) return nullptr;
     c->to_host = to_host;
     c->bytes = bytes;
-    c->link = this;
-    c->flag = flag(gate);
-    c->value = ++gates_[gate].gen;
     return c;
   }
 
@@ -313,7 +287,7 @@ class SdmaLink : public Link {
       }
     }
     if (!ev) {
-      hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming | hipEventBlockingSync);
+      hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
       if (e != hipSuccess) return (int)e;
     }
     auto hold = std::make_shared<EventHold>();
@@ -331,84 +305,129 @@ class SdmaLink : public Link {
     cv_.notify_one();
   }
 
-  // Issuer thread: jobs in FIFO order. Every event a job waits for was recorded before the job
-  // was enqueued, and every stream wait on a job's gate is enqueued after the job, so waiting
-  // here can never depend on a job behind this one.
-  void run() {
-    if (hipSetDevice(device_) != hipSuccess) {
-      // Still drain the queue below so no stream waits forever.
+  // Worker-owned signal pool: a signal goes back to the pool as soon as its copy finished.
+  bool take_signal(hsa_signal_t* sig) {
+    if (!sig_pool_.empty()) {
+      *sig = sig_pool_.back();
+      sig_pool_.pop_back();
+      hsa_signal_store_screlease(*sig, 1);
+      return true;
     }
+    return hsa_signal_create(1, 0, nullptr, sig) == HSA_STATUS_SUCCESS;
+  }
+
+  void finish(const SdmaRef& c, bool failed) {
+    const int dir = c->to_host ? 0 : 1;
+    const int64_t t = now_ns();
+    if (failed) {
+      c->fail.store(true, std::memory_order_release);
+      failures_++;
+    } else {
+      // Engine-busy time: copies on one engine run back to back, so a copy starts at the later
+      // of its issue and the previous completion in its direction.
+      const int64_t start = c->issue_ns > last_done_ns_[dir] ? c->issue_ns : last_done_ns_[dir];
+      busy_ns_[dir] += t > start ? (uint64_t)(t - start) : 0;
+      done_bytes_[dir] += c->bytes;
+      last_done_ns_[dir] = t;
+    }
+    c->finished.store(true, std::memory_order_release);
+  }
+
+  // Issue `job` if its dependencies are met. Returns true if the job left the queue.
+  bool try_issue(Job& job) {
+    if (job.wait) {
+      const hipError_t q = hipEventQuery(job.wait->ev);
+      if (q == hipErrorNotReady) return false;
+      job.wait.reset();
+      if (q != hipSuccess) {
+        finish(job.copy, true);
+        return true;
+      }
+    }
+    if (job.after) {
+      if (!job.after->done()) return false;
+      const bool bad = job.after->failed();
+      job.after.reset();
+      if (bad) {
+        finish(job.copy, true);
+        return true;
+      }
+    }
+    hsa_signal_t sig{0};
+    if (!take_signal(&sig)) {
+      finish(job.copy, true);
+      return true;
+    }
+    SdmaCopy& c = *job.copy;
+    c.issue_ns = now_ns();
+    const hsa_status_t st = hsa_amd_memory_async_copy_on_engine(
+        job.dst, c.to_host ? cpu_ : gpu_, job.src, c.to_host ? gpu_ : cpu_, c.bytes, 0, nullptr, sig,
+        (hsa_amd_sdma_engine_id_t)(c.to_host ? e_d2h_ : e_h2d_), true);
+    if (st != HSA_STATUS_SUCCESS) {
+      sig_pool_.push_back(sig);
+      finish(job.copy, true);
+      return true;
+    }
+    inflight_.push_back(InFlight{job.copy, sig});
+    inflight_count_++;
+    return true;
+  }
+
+  // Completed copies leave the in-flight list (in issue order per engine, but checked all).
+  bool poll_inflight() {
+    bool progress = false;
+    for (auto it = inflight_.begin(); it != inflight_.end();) {
+      const hsa_signal_value_t v = hsa_signal_load_scacquire(it->sig);
+      if (v < 1) {
+        finish(it->copy, v < 0);
+        sig_pool_.push_back(it->sig);
+        it = inflight_.erase(it);
+        inflight_count_--;
+        progress = true;
+      } else if (now_ns() - it->copy->issue_ns > kWaitLimitNs) {
+        // Give up on a copy the engine never completed: report it, keep the signal alive.
+        finish(it->copy, true);
+        it = inflight_.erase(it);
+        inflight_count_--;
+        progress = true;
+      } else {
+        ++it;
+      }
+    }
+    return progress;
+  }
+
+  // Issuer thread. Jobs issue in FIFO order. Every event a job waits for was recorded on a
+  // compute stream before the job was enqueued, and no GPU queue waits on the host, so every
+  // dependency eventually completes.
+  void run() {
+    (void)hipSetDevice(device_);
     for (;;) {
+      bool progress = poll_inflight();
       Job job;
+      bool have = false;
       {
         std::unique_lock<std::mutex> lock(mu_);
-        cv_.wait_for(lock, std::chrono::milliseconds(5), [this] { return stop_ || !queue_.empty(); });
-        if (queue_.empty()) {
+        if (queue_.empty() && inflight_.empty()) {
           if (stop_) return;
-          lock.unlock();
-          sweep();
+          cv_.wait_for(lock, std::chrono::milliseconds(2), [this] { return stop_ || !queue_.empty(); });
           continue;
         }
-        job = std::move(queue_.front());
-        queue_.pop_front();
-        busy_++;
+        if (!queue_.empty()) {
+          job = std::move(queue_.front());
+          queue_.pop_front();
+          holding_++;
+          have = true;
+        }
       }
-      issue(job);
-      {
+      if (have) {
+        const bool issued = try_issue(job);
         std::lock_guard<std::mutex> lock(mu_);
-        busy_--;
+        if (issued) progress = true;
+        else queue_.push_front(std::move(job));
+        holding_--;
       }
-      sweep();
-    }
-  }
-
-  void issue(Job& job) {
-    if (job.wait) {
-      (void)hipEventSynchronize(job.wait->ev);
-      job.wait.reset();
-    }
-    auto& c = job.copy;
-    bool ok = true;
-    if (job.after) {
-      // The host bytes must have arrived before they leave again.
-      const int64_t deadline = now_ns() + 120ll * 1000000000ll;
-      while (!job.after->done() && now_ns() < deadline) std::this_thread::sleep_for(std::chrono::microseconds(20));
-      ok = job.after->done() && !job.after->failed();
-      job.after.reset();
-    }
-    c->issue_ns = now_ns();
-    c->self = c;
-    issued_++;
-    hsa_status_t st = HSA_STATUS_ERROR;
-    if (ok) {
-      st = hsa_amd_memory_async_copy_on_engine(job.dst, c->to_host ? cpu_ : gpu_, job.src, c->to_host ? gpu_ : cpu_,
-                                               c->bytes, 0, nullptr, c->sig,
-                                               (hsa_amd_sdma_engine_id_t)(c->to_host ? e_d2h_ : e_h2d_), true);
-    }
-    if (st == HSA_STATUS_SUCCESS) {
-      st = hsa_amd_signal_async_handler(c->sig, HSA_SIGNAL_CONDITION_LT, 1, on_done, c.get());
-      if (st == HSA_STATUS_SUCCESS) return;
-      // No handler: wait here and complete inline.
-      hsa_signal_value_t v = 1;
-      while ((v = hsa_signal_wait_scacquire(c->sig, HSA_SIGNAL_CONDITION_LT, 1, 1000000, HSA_WAIT_STATE_BLOCKED)) >= 1) {
-      }
-      on_done(v, c.get());
-      return;
-    }
-    // Never leave a stream waiting on a copy that will not happen: complete it as failed.
-    on_done(-1, c.get());
-  }
-
-  // Destroy retired copies a while after their handler ran (their signals are then idle).
-  void sweep() {
-    std::vector<std::shared_ptr<SdmaCopy>> drop;
-    {
-      std::lock_guard<std::mutex> lock(retire_mu_);
-      const int64_t limit = now_ns() - 5000000;  // 5 ms
-      while (!retired_.empty() && retired_.front()->retired_ns < limit) {
-        drop.push_back(std::move(retired_.front()));
-        retired_.pop_front();
-      }
+      if (!progress) short_sleep();
     }
   }
 
@@ -419,23 +438,15 @@ class SdmaLink : public Link {
         stop_ = true;
       }
       cv_.notify_all();
-      worker_.join();  // drains the queue first
-      (void)synchronize();
-      std::this_thread::sleep_for(std::chrono::milliseconds(10));
+      worker_.join();  // returns once the queue is drained and nothing is in flight
     }
     gates_.clear();
-    {
-      std::lock_guard<std::mutex> lock(retire_mu_);
-      retired_.clear();
-    }
+    for (hsa_signal_t s : sig_pool_) hsa_signal_destroy(s);
+    sig_pool_.clear();
     {
       std::lock_guard<std::mutex> lock(ev_mu_);
       for (hipEvent_t e : ev_pool_) (void)hipEventDestroy(e);
       ev_pool_.clear();
-    }
-    if (flags_) {
-      (void)hipHostFree(flags_);
-      flags_ = nullptr;
     }
     if (hsa_inited_) {
       hsa_shut_down();
@@ -447,8 +458,8 @@ class SdmaLink : public Link {
   bool hsa_inited_ = false;
   hsa_agent_t gpu_{0}, cpu_{0};
   uint32_t e_d2h_ = 0, e_h2d_ = 0;
-  uint32_t* flags_ = nullptr;
-  std::vector<GateState> gates_;  // touched by API threads only (engine mutex)
+  std::vector<GateState> gates_;  // API threads only (engine mutex)
+  uint64_t d2h_bytes_ = 0, h2d_bytes_ = 0, host_blocks_ = 0, host_block_ns_ = 0;  // API threads only
 
   std::mutex ev_mu_;
   std::vector<hipEvent_t> ev_pool_;
@@ -456,18 +467,19 @@ class SdmaLink : public Link {
   std::mutex mu_;
   std::condition_variable cv_;
   std::deque<Job> queue_;
-  int busy_ = 0;
   bool stop_ = false;
+  int holding_ = 0;  // jobs popped by the worker and not yet issued or put back
   std::thread worker_;
 
-  std::mutex retire_mu_;
-  std::deque<std::shared_ptr<SdmaCopy>> retired_;
+  // worker thread only
+  std::vector<InFlight> inflight_;
+  std::vector<hsa_signal_t> sig_pool_;
+  int64_t last_done_ns_[2] = {0, 0};
 
-  std::atomic<uint64_t> issued_{0}, completed_{0}, failures_{0};
-  std::atomic<int64_t> last_done_ns_[2]{{0}, {0}};
+  std::atomic<int> inflight_count_{0};
+  std::atomic<uint64_t> failures_{0};
   std::atomic<uint64_t> busy_ns_[2]{{0}, {0}};
   std::atomic<uint64_t> done_bytes_[2]{{0}, {0}};
-  uint64_t d2h_bytes_ = 0, h2d_bytes_ = 0;
 };
 
 EventHold::~EventHold() {

@@ -5,10 +5,12 @@
 //   SdmaLink    (default) the MI355X's SDMA copy engines through the HSA runtime
 //               (hsa_amd_memory_async_copy_on_engine). No compute unit is used, so copies
 //               overlap GEMM-heavy compute without slowing it. Ordering with HIP streams:
-//                 compute -> copy : the copy job waits for a HIP event (issuer thread),
-//                 copy -> copy    : HSA completion signal passed as a dependency,
-//                 copy -> compute : the completion handler publishes a generation number in
-//                                   coherent pinned memory; the stream hipStreamWaitValue32s.
+//                 compute -> copy : an issuer thread queries the HIP event recorded after the
+//                                   producing kernels, then issues the copy,
+//                 copy -> copy    : the issuer holds a copy until the one it depends on finished,
+//                 copy -> compute : the host waits for the copy's HSA signal before it enqueues
+//                                   the dependent kernels (wait()).
+//               No GPU queue ever waits on host-written memory, and every wait is bounded.
 //   StreamLink  a copy kernel on dedicated HIP streams ordered with HIP events. Kept for
 //               comparison: shader copies contend with compute for compute units.
 //
@@ -39,6 +41,8 @@ struct LinkStats {
   uint64_t d2h_done_bytes = 0, h2d_done_bytes = 0;  // completed and timed
   double d2h_ms = 0, h2d_ms = 0;                // engine-busy time of completed copies
   uint64_t failures = 0;
+  uint64_t host_blocks = 0;                     // wait() calls that had to block the host
+  double host_block_ms = 0;                     // time spent blocked in them
 };
 
 class Link {
@@ -51,7 +55,8 @@ class Link {
   // Copy pinned host `src` to device `dst` once `after` (the D2H that filled src) finished and
   // the gate's last consumer (see consumed()) finished. Completion is published through `gate`.
   virtual int h2d(void* dst, const void* src, uint64_t bytes, const CopyRef& after, int gate, CopyRef* out) = 0;
-  // Make `compute` wait for the last copy published through `gate` (no-op if none).
+  // Order work enqueued on `compute` after this call behind the gate's last copy (no-op if
+  // none): SdmaLink blocks the host until the copy finished; StreamLink makes the stream wait.
   virtual int wait(int gate, hipStream_t compute) = 0;
   // Record that the slot behind `gate` is free for the next copy once `compute` reaches here.
   virtual int consumed(int gate, hipStream_t compute) = 0;

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 2
+MO_ABI_VERSION = 3
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -78,7 +78,11 @@ class MoStats(ctypes.Structure):
             "host_bytes_peak",
             "host_bytes_reserved",
             "stage_slot_waits",
-            "stage_slot_busy",
+            "host_blocks",
+        )
+    ] + [("host_block_ms", ctypes.c_double)] + [
+        (name, ctypes.c_uint64)
+        for name in (
             "prefetch_issued",
             "prefetch_hits",
             "restore_fetches",
