@@ -16,7 +16,7 @@ sees each block's inputs. Regime B: no checkpointing, so the hook sees every act
 
 Prints ONE JSON line (stdout). Progress goes to stderr.
 
-  python bench.py [--steps K] [--warmup W] [--regimes A,B] [--micro ITERS]
+  python bench.py [--steps K] [--warmup W] [--regimes M,A,B] [--micro-iters N]
 """
 
 from __future__ import annotations
@@ -275,6 +275,165 @@ def record_manifest(model, inputs, regime: str):
     return recorder
 
 
+def capture_block_saves(model, inputs):
+    """The offloadable saved tensors of one joint block in regime B, in the order the hook sees them.
+
+    One forward of the whole model without checkpointing; a pack hook keeps the tensors saved
+    between the middle block's forward pre- and post-hooks, minus parameter/buffer-backed saves
+    and layouts the reference keeps resident (training/activation_offload.py:101-121). Repeated
+    saves of the same view are kept once (the engine deduplicates them).
+    """
+
+    import torch
+    from moss_offload import dit
+    from moss_offload.activation_offload import _offload_view, _storage_key
+
+    configure_mode(model, "none", "B")
+    resident = {_storage_key(t) for t in (*model.parameters(), *model.buffers())}
+    layer = model.layers[len(model.layers) // 2]
+    state = {"on": False}
+    saved, seen = [], set()
+
+    def pack(t):
+        if state["on"] and t.device.type == "cuda" and _storage_key(t) not in resident and _offload_view(t) is not None:
+            key = (t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype)
+            if key not in seen:
+                seen.add(key)
+                saved.append(t)
+        return t
+
+    handles = [
+        layer.register_forward_pre_hook(lambda m, a: state.__setitem__("on", True)),
+        layer.register_forward_hook(lambda m, a, o: state.__setitem__("on", False)),
+    ]
+    clean, noise, sigma, context = inputs
+    try:
+        with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t), torch.autocast("cuda", dtype=torch.bfloat16):
+            error, _ = dit.squared_error(model, clean, noise, sigma, context)
+    finally:
+        for h in handles:
+            h.remove()
+    del error
+    return saved
+
+
+def _same_bits(a, b) -> bool:
+    import torch
+
+    ints = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}
+    if a.shape != b.shape or a.stride() != b.stride() or a.dtype != b.dtype:
+        return False
+    dt = ints[a.element_size()]
+    return bool(torch.equal(a.view(dt), b.view(dt)))
+
+
+CAL_BYTES = 256 << 20
+CAL_BLOCKS = 1024
+
+
+def calibration_copy(device, stream: int, repeats: int = 3) -> None:
+    """A plain device-to-device copy of CAL_BYTES with the engine's link-copy kernel.
+
+    Under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` its dispatches (grid CAL_BLOCKS x 256)
+    read and write exactly CAL_BYTES each, which scales the counters to bytes.
+    """
+
+    import torch
+    from moss_offload import _native
+
+    lib = _native.load()
+    buf = torch.empty(2, CAL_BYTES, dtype=torch.uint8, device=device)
+    for _ in range(repeats):
+        _native.check("mo_link_copy", lib.mo_link_copy(buf[1].data_ptr(), buf[0].data_ptr(), CAL_BYTES, 0,
+                                                       CAL_BLOCKS, stream))
+    torch.cuda.synchronize()
+    del buf
+
+
+def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: int, restore_slots: int):
+    """one regime-B block's saved set through pack -> D2H -> H2D -> unpack.
+
+    Every iteration packs the block's tensors into one group (staging ring + SDMA D2H), commits
+    it, restores every entry (SDMA H2D + unpack kernel, staged restore off so each byte crosses
+    the link both ways) and releases the group. The sources are refilled with fresh random bits
+    before the first and the last iteration, and those iterations' restored tensors are checked
+    bitwise against them (shape, strides, dtype, bits).
+    """
+
+    import torch
+    from moss_offload.engine import EngineConfig, OffloadEngine
+
+    engine = OffloadEngine(device, EngineConfig(
+        stage_slot_bytes=slot_mib << 20, stage_slots=stage_slots, restore_slots=restore_slots,
+        timing=True, kernel_timing=True, staged_restore=False, prefetch=False))
+    stream = torch.cuda.current_stream(device).cuda_stream
+    payload = sum(t.numel() * t.element_size() for t in tensors)
+    storages = {}
+    for t in tensors:
+        storages.setdefault(t.untyped_storage().data_ptr(), t)
+
+    def refill():
+        for t in storages.values():
+            torch.empty(0, dtype=torch.uint8, device=device).set_(t.untyped_storage()).random_(0, 256)
+
+    def one(keep: bool):
+        refs = [engine.pack(t, stream) for t in tensors]
+        engine.commit(stream)
+        outs = [engine.restore(g, i, stream) for g, i in refs]
+        for g, i in refs:
+            engine.drop(g, i)
+        return outs if keep else None
+
+    def check(outs) -> bool:
+        torch.cuda.synchronize()
+        return all(_same_bits(o.as_strided(t.shape, t.stride()), t) for o, t in zip(outs, tensors))
+
+    try:
+        refill()
+        first_ok = check(one(keep=True))
+        for _ in range(max(0, warmup - 1)):
+            one(keep=False)
+        torch.cuda.synchronize()
+        engine.synchronize()
+        engine.reset_stats()
+        start = time.perf_counter()
+        for _ in range(iters):
+            one(keep=False)
+        torch.cuda.synchronize()
+        engine.synchronize()
+        seconds = (time.perf_counter() - start) / iters
+        st = engine.stats()
+        # after the timed region: fresh bits, one more iteration, checked
+        refill()
+        last_ok = check(one(keep=True))
+        calibration_copy(device, stream)
+    finally:
+        engine.close()
+    out = {
+        "tensors": len(tensors),
+        "payload_bytes": payload,
+        "iters": iters,
+        "s_per_iter": seconds,
+        "bitwise_first": first_ok,
+        "bitwise_last": last_ok,
+        "d2h_gbps": st["timed_d2h_bytes"] / max(st["d2h_ms"], 1e-9) / 1e6,
+        "h2d_gbps": st["timed_h2d_bytes"] / max(st["h2d_ms"], 1e-9) / 1e6,
+        "pipeline_gbps": 2 * payload / seconds / 1e9,
+        "pack_hbm_gbps": 2 * st["timed_pack_bytes"] / max(st["pack_ms"], 1e-9) / 1e6,
+        "unpack_hbm_gbps": 2 * st["timed_unpack_bytes"] / max(st["unpack_ms"], 1e-9) / 1e6,
+        "pack_avg_launch_us": st["pack_ms"] * 1e3 / max(st["timed_pack_launches"], 1),
+        "unpack_avg_launch_us": st["unpack_ms"] * 1e3 / max(st["timed_unpack_launches"], 1),
+        "pack_bytes_per_launch": st["timed_pack_bytes"] / max(st["timed_pack_launches"], 1),
+        "unpack_bytes_per_launch": st["timed_unpack_bytes"] / max(st["timed_unpack_launches"], 1),
+        "pack_launches_per_iter": st["timed_pack_launches"] / iters,
+        "unpack_launches_per_iter": st["timed_unpack_launches"] / iters,
+        "host_blocks_per_iter": st["host_blocks"] / iters,
+        "host_block_ms_per_iter": st["host_block_ms"] / iters,
+        "copy_failures": st["copy_failures"],
+    }
+    return out
+
+
 def cpu_baseline(recorder, threads: int, budget_s: float = 15.0):
     """The oracle's restatement of the reference hooks with CPU payloads, on the host cores.
 
@@ -344,7 +503,20 @@ def run(args) -> dict:
         result["parity"] = parity(model, inputs)
         log(f"parity: {result['parity']}")
 
-    for regime in args.regimes:
+    if "M" in args.regimes:
+        tensors = capture_block_saves(model, inputs)
+        torch.cuda.synchronize()
+        payload = sum(t.numel() * t.element_size() for t in tensors)
+        log(f"micro: one regime-B block, {len(tensors)} unique saves, {payload / 1e6:.1f} MB")
+        result["micro"] = micro(device, tensors, args.micro_iters, args.micro_warmup, args.slot_mib,
+                                args.stage_slots, args.restore_slots)
+        m = result["micro"]
+        log(f"micro: {m['s_per_iter'] * 1e3:.2f} ms/iter, D2H {m['d2h_gbps']:.1f} GB/s, H2D {m['h2d_gbps']:.1f} GB/s, "
+            f"pack {m['pack_hbm_gbps']:.0f} GB/s ({m['pack_avg_launch_us']:.1f} us/launch), unpack "
+            f"{m['unpack_hbm_gbps']:.0f} GB/s, bitwise {m['bitwise_first'] and m['bitwise_last']}")
+        del tensors
+
+    for regime in (r for r in args.regimes if r != "M"):
         manifest = record_manifest(model, inputs, regime)
         payload_unique = manifest.payload_bytes(unique=True)
         payload_copied = manifest.payload_bytes(unique=False)
@@ -424,7 +596,9 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--steps-b", type=int, default=2)
     parser.add_argument("--warmup-b", type=int, default=1)
-    parser.add_argument("--regimes", default="A,B")
+    parser.add_argument("--regimes", default="M,A,B", help="M = config-2 block microbench, A/B = config-3 steps")
+    parser.add_argument("--micro-iters", type=int, default=200)
+    parser.add_argument("--micro-warmup", type=int, default=3)
     parser.add_argument("--modes", default="none,engine,reference")
     parser.add_argument("--layers", type=int, default=CONFIG3["num_layers"])
     parser.add_argument("--no-parity", action="store_true")
@@ -454,7 +628,7 @@ def main() -> int:
         return 2
     result = run(args)
     regimes = result["regimes"]
-    headline = regimes.get("A") or next(iter(regimes.values()))
+    headline = regimes.get("A") or next(iter(regimes.values()), {})
     eng = headline.get("engine", {})
     # cpu baseline: oracle restatement, bounded sample (one regime-B block's saves if recorded)
     sample = None
@@ -480,16 +654,22 @@ def main() -> int:
     for r in regimes.values():
         r.pop("cpu_sample", None)
     # dominant engine kernel of the headline regime
+    # Dominant engine kernel: the pack kernel (mo_pack_kernel). Measured on the config-2 block
+    # microbench when it ran (one regime-B block's saves, the bulk of all offload traffic),
+    # else on the headline regime's steps. achieved = 2 x payload bytes per launch (read the
+    # source, write the staging slot) / average dispatch duration (HIP events of the launch).
+    src = result.get("micro") or eng
     pack_bound = {
         "bound": "hbm",
-        "kernel": "mo::copy_kernel<true> (pack)",
-        "achieved": round(eng.get("pack_hbm_gbps", 0.0), 1),
+        "kernel": "mo_pack_kernel",
+        "workload": "config-2 block microbench" if "micro" in result else "headline regime steps",
+        "achieved": round(src.get("pack_hbm_gbps", 0.0), 1),
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
-        "frac": round(eng.get("pack_hbm_gbps", 0.0) / HBM_PEAK_GBPS, 4),
+        "frac": round(src.get("pack_hbm_gbps", 0.0) / HBM_PEAK_GBPS, 4),
         "traffic": None,
-        "bytes_per_launch": eng.get("pack_bytes_per_launch"),
-        "avg_launch_us": eng.get("pack_avg_launch_us"),
+        "algorithmic_bytes_per_launch": 2 * src.get("pack_bytes_per_launch", 0.0),
+        "avg_launch_us": src.get("pack_avg_launch_us"),
     }
     line = {
         "metric": "DiT step s/it @1024² w/ act-offload; D2H/H2D GB/s; % copy hidden",

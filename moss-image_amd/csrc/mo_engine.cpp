@@ -298,7 +298,7 @@ struct Engine {
     bool pack;
     Timing cur{};
     KernelTimer(Engine* engine, bool p) : e(engine), pack(p) {}
-    int before(hipStream_t s) override {
+    int events(hipEvent_t* start, hipEvent_t* stop) override {
       cur = Timing{nullptr, nullptr, 0, pack};
       if (!(e->cfg.flags & MO_FLAG_KERNEL_TIMING)) return 0;
       for (hipEvent_t* ev : {&cur.start, &cur.end}) {
@@ -310,15 +310,14 @@ struct Engine {
           if (err != hipSuccess) return (int)err;
         }
       }
-      return (int)hipEventRecord(cur.start, s);
-    }
-    int after(hipStream_t s, uint64_t bytes) override {
-      if (!cur.start) return 0;
-      cur.bytes = bytes;
-      hipError_t err = hipEventRecord(cur.end, s);
-      if (err != hipSuccess) return (int)err;
-      e->timings.push_back(cur);
+      *start = cur.start;
+      *stop = cur.end;
       return 0;
+    }
+    void launched(uint64_t bytes) override {
+      cur.bytes = bytes;
+      e->timings.push_back(cur);
+      cur = Timing{nullptr, nullptr, 0, pack};
     }
   };
 
@@ -784,11 +783,16 @@ static int run_copy(bool pack, const mo_tensor* ts, int n, uint64_t payload, con
   Launcher L(pack, (hipStream_t)stream);
   std::string err;
   for (int i = 0; i < n; ++i) {
-    if (cs[i].nbytes == 0) continue;
-    KDesc kd;
-    if (int rc = make_kdesc(cs[i], cs[i].base, 0, cs[i].nbytes, payload + offs[i], kd, err))
-      return fail(rc, "tensor " + std::to_string(i) + ": " + err);
-    L.add(kd);
+    // Pieces of at most one launch's worth of tiles, so a launch grid never exceeds
+    // kMaxTilesPerLaunch + kMaxDesc workgroups.
+    const uint64_t chunk = (uint64_t)kMaxTilesPerLaunch * kTileBytes;
+    for (uint64_t first = 0; first < cs[i].nbytes; first += chunk) {
+      const uint64_t take = std::min(chunk, cs[i].nbytes - first);
+      KDesc kd;
+      if (int rc = make_kdesc(cs[i], cs[i].base, first, take, payload + offs[i] + first, kd, err))
+        return fail(rc, "tensor " + std::to_string(i) + ": " + err);
+      L.add(kd);
+    }
   }
   if (int rc = L.flush()) return hip_fail(rc, pack ? "pack kernel launch" : "unpack kernel launch");
   return 0;

@@ -14,12 +14,15 @@ namespace mo {
 int make_kdesc(const Canon& c, uint64_t tensor_base, uint64_t first, uint64_t nbytes, uint64_t payload,
                KDesc& kd, std::string& err);
 
-// Optional observer that brackets each kernel launch (e.g. with timing events).
+// Optional observer of kernel launches: supplies the HIP events a launch records its own
+// start and end into (the timestamps of the dispatch itself, the same interval a kernel trace
+// reports), and is told the payload bytes of each timed launch.
 class LaunchTimer {
  public:
   virtual ~LaunchTimer() = default;
-  virtual int before(hipStream_t stream) = 0;
-  virtual int after(hipStream_t stream, uint64_t bytes) = 0;
+  // *start/*stop stay null when the next launch is not timed.
+  virtual int events(hipEvent_t* start, hipEvent_t* stop) = 0;
+  virtual void launched(uint64_t bytes) = 0;
 };
 
 // Accumulates pieces and launches the pack (or unpack) kernel in batches of kMaxDesc.

@@ -17,6 +17,16 @@
 extern "C" const unsigned char mo_device_code[];
 extern "C" const uint64_t mo_device_code_size;
 
+// Exported by libamdhip64 (declared in hip/hip_ext.h, which only hipcc can parse): a module
+// launch that records its own dispatch start and end into two HIP events. Grid sizes are in
+// work-items.
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX, uint32_t globalWorkSizeY,
+                                               uint32_t globalWorkSizeZ, uint32_t localWorkSizeX,
+                                               uint32_t localWorkSizeY, uint32_t localWorkSizeZ,
+                                               size_t sharedMemBytes, hipStream_t hStream, void** kernelParams,
+                                               void** extra, hipEvent_t startEvent, hipEvent_t stopEvent,
+                                               uint32_t flags);
+
 namespace mo {
 
 namespace {
@@ -157,14 +167,19 @@ int Launcher::flush() {
   if (args_.ndesc == 0) return 0;
   hipFunction_t fn = nullptr;
   if (status_ == 0) status_ = pack_ ? kernels(&fn, nullptr, nullptr) : kernels(nullptr, &fn, nullptr);
-  if (status_ == 0 && timer_) status_ = timer_->before(stream_);
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  if (status_ == 0 && timer_) status_ = timer_->events(&t0, &t1);
   if (status_ == 0) {
     void* params[] = {&args_};
-    const hipError_t e = hipModuleLaunchKernel(fn, tiles_, 1, 1, kThreads, 1, 1, 0, stream_, params, nullptr);
+    // The extended launch takes the grid in work-items (tiles_ <= kMaxTilesPerLaunch + kMaxDesc,
+    // so tiles_ * kThreads stays far below 2^32).
+    const hipError_t e = t0 ? hipExtModuleLaunchKernel(fn, tiles_ * kThreads, 1, 1, kThreads, 1, 1, 0, stream_,
+                                                       params, nullptr, t0, t1, 0)
+                            : hipModuleLaunchKernel(fn, tiles_, 1, 1, kThreads, 1, 1, 0, stream_, params, nullptr);
     if (e != hipSuccess) status_ = (int)e;
     launches_++;
+    if (e == hipSuccess && t0) timer_->launched(pending_bytes_);
   }
-  if (status_ == 0 && timer_) status_ = timer_->after(stream_, pending_bytes_);
   args_.ndesc = 0;
   tiles_ = 0;
   pending_bytes_ = 0;
