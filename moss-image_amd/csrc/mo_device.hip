@@ -46,18 +46,73 @@ __device__ __forceinline__ uint64_t unit_offset(const KDesc& d, uint32_t u) {
   return off;
 }
 
+// Every device pointer reaches the kernels as an integer inside a descriptor, so the compiler
+// cannot infer its address space and would emit flat (generic) memory instructions. The
+// accessors below name the space: global (HBM or pinned host memory) or LDS.
+#define MO_GLOBAL __attribute__((address_space(1)))
+#define MO_LDS __attribute__((address_space(3)))
+
+enum Space { kG, kL };
+
+// 16-byte values move as a native vector: uint4 is a class whose copy constructor takes a
+// generic reference, which would turn the access back into a flat one.
+typedef unsigned int mo_u32x4 __attribute__((ext_vector_type(4)));
+
+template <Space S, typename T>
+__device__ __forceinline__ T ld(const char* p) {
+  if (S == kG) return *(const MO_GLOBAL T*)p;
+  return *(const MO_LDS T*)p;
+}
+template <Space S, typename T>
+__device__ __forceinline__ void st(char* p, T v) {
+  if (S == kG) *(MO_GLOBAL T*)p = v;
+  else *(MO_LDS T*)p = v;
+}
+template <>
+__device__ __forceinline__ uint4 ld<kG, uint4>(const char* p) {
+  const mo_u32x4 x = *(const MO_GLOBAL mo_u32x4*)p;
+  return make_uint4(x.x, x.y, x.z, x.w);
+}
+template <>
+__device__ __forceinline__ uint4 ld<kL, uint4>(const char* p) {
+  const mo_u32x4 x = *(const MO_LDS mo_u32x4*)p;
+  return make_uint4(x.x, x.y, x.z, x.w);
+}
+template <>
+__device__ __forceinline__ void st<kG, uint4>(char* p, uint4 v) {
+  *(MO_GLOBAL mo_u32x4*)p = mo_u32x4{v.x, v.y, v.z, v.w};
+}
+template <>
+__device__ __forceinline__ void st<kL, uint4>(char* p, uint4 v) {
+  *(MO_LDS mo_u32x4*)p = mo_u32x4{v.x, v.y, v.z, v.w};
+}
+
+template <Space D, Space S>
 __device__ __forceinline__ void copy_elem(char* dst, const char* src, uint32_t eb) {
   switch (eb) {
-    case 1: *(uint8_t*)dst = *(const uint8_t*)src; break;
-    case 2: *(uint16_t*)dst = *(const uint16_t*)src; break;
-    case 4: *(uint32_t*)dst = *(const uint32_t*)src; break;
-    case 8: *(uint64_t*)dst = *(const uint64_t*)src; break;
-    default: *(uint4*)dst = *(const uint4*)src; break;
+    case 1: st<D>(dst, ld<S, uint8_t>(src)); break;
+    case 2: st<D>(dst, ld<S, uint16_t>(src)); break;
+    case 4: st<D>(dst, ld<S, uint32_t>(src)); break;
+    case 8: st<D>(dst, ld<S, uint64_t>(src)); break;
+    default: st<D>(dst, ld<S, uint4>(src)); break;
   }
 }
 
-__device__ __forceinline__ uint4 ld16(const char* p) { return *(const uint4*)p; }
-__device__ __forceinline__ void st16(char* p, uint4 v) { *(uint4*)p = v; }
+__device__ __forceinline__ uint4 ld16(const char* p) { return ld<kG, uint4>(p); }
+__device__ __forceinline__ void st16(char* p, uint4 v) { st<kG>(p, v); }
+
+// Streaming store for the staging payload: it is written once and next read by a DMA engine,
+// so the write is marked non-temporal (no reuse expected in the GPU caches).
+__device__ __forceinline__ void st16_stream(char* p, uint4 v) {
+  const mo_u32x4 x = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(x, (MO_GLOBAL mo_u32x4*)p);
+}
+// Payload-side store: streaming when packing (the payload is the staging buffer).
+template <bool kPack>
+__device__ __forceinline__ void st16_out(char* p, uint4 v) {
+  if (kPack) st16_stream(p, v);
+  else st16(p, v);
+}
 
 template <bool kPack>
 __device__ __forceinline__ void copy_body(const LaunchArgs& args) {
@@ -83,11 +138,11 @@ __device__ __forceinline__ void copy_body(const LaunchArgs& args) {
 #pragma unroll
       for (int k = 0; k < kUnroll; ++k) v[k] = ld16(src + (size_t)(k * kThreads + tid) * 16);
 #pragma unroll
-      for (int k = 0; k < kUnroll; ++k) st16(dst + (size_t)(k * kThreads + tid) * 16, v[k]);
+      for (int k = 0; k < kUnroll; ++k) st16_out<kPack>(dst + (size_t)(k * kThreads + tid) * 16, v[k]);
     } else {
       const uint32_t nvec = tile_bytes / 16;
-      for (uint32_t c = tid; c < nvec; c += kThreads) st16(dst + (size_t)c * 16, ld16(src + (size_t)c * 16));
-      for (uint32_t b = nvec * 16 + tid * eb; b < tile_bytes; b += kThreads * eb) copy_elem(dst + b, src + b, eb);
+      for (uint32_t c = tid; c < nvec; c += kThreads) st16_out<kPack>(dst + (size_t)c * 16, ld16(src + (size_t)c * 16));
+      for (uint32_t b = nvec * 16 + tid * eb; b < tile_bytes; b += kThreads * eb) copy_elem<kG, kG>(dst + b, src + b, eb);
     }
     return;
   }
@@ -110,7 +165,7 @@ __device__ __forceinline__ void copy_body(const LaunchArgs& args) {
     for (int k = 0; k < kUnroll; ++k) {
       const uint32_t c = k * kThreads + tid;
       if (c < nchunk) {
-        if (kPack) st16(payload + (size_t)c * 16, v[k]);
+        if (kPack) st16_stream(payload + (size_t)c * 16, v[k]);
         else st16(tensor + toff[k], v[k]);
       }
     }
@@ -124,16 +179,16 @@ __device__ __forceinline__ void copy_body(const LaunchArgs& args) {
   const uint32_t nvec = tile_bytes / 16;
   if (kPack) {
     for (uint32_t j = tid; j < nelem; j += kThreads)
-      copy_elem(sbuf + (size_t)j * eb, tensor + unit_offset(d, e0 + j), eb);
+      copy_elem<kL, kG>(sbuf + (size_t)j * eb, tensor + unit_offset(d, e0 + j), eb);
     __syncthreads();
-    for (uint32_t c = tid; c < nvec; c += kThreads) st16(payload + (size_t)c * 16, lds[c]);
-    for (uint32_t b = nvec * 16 + tid * eb; b < tile_bytes; b += kThreads * eb) copy_elem(payload + b, sbuf + b, eb);
+    for (uint32_t c = tid; c < nvec; c += kThreads) st16_stream(payload + (size_t)c * 16, ld<kL, uint4>(sbuf + (size_t)c * 16));
+    for (uint32_t b = nvec * 16 + tid * eb; b < tile_bytes; b += kThreads * eb) copy_elem<kG, kL>(payload + b, sbuf + b, eb);
   } else {
-    for (uint32_t c = tid; c < nvec; c += kThreads) lds[c] = ld16(payload + (size_t)c * 16);
-    for (uint32_t b = nvec * 16 + tid * eb; b < tile_bytes; b += kThreads * eb) copy_elem(sbuf + b, payload + b, eb);
+    for (uint32_t c = tid; c < nvec; c += kThreads) st<kL>(sbuf + (size_t)c * 16, ld16(payload + (size_t)c * 16));
+    for (uint32_t b = nvec * 16 + tid * eb; b < tile_bytes; b += kThreads * eb) copy_elem<kL, kG>(sbuf + b, payload + b, eb);
     __syncthreads();
     for (uint32_t j = tid; j < nelem; j += kThreads)
-      copy_elem(tensor + unit_offset(d, e0 + j), sbuf + (size_t)j * eb, eb);
+      copy_elem<kG, kL>(tensor + unit_offset(d, e0 + j), sbuf + (size_t)j * eb, eb);
   }
 }
 
@@ -166,6 +221,6 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_link_copy_kernel(c
   }
   for (; base < nvec; base += lanes) st16(dst + base * 16, ld16(src + base * 16));
   if (blockIdx.x == 0) {
-    for (uint64_t b = nvec * 16 + threadIdx.x; b < nbytes; b += kThreads) dst[b] = src[b];
+    for (uint64_t b = nvec * 16 + threadIdx.x; b < nbytes; b += kThreads) st<kG>(dst + b, ld<kG, uint8_t>(src + b));
   }
 }

@@ -9,6 +9,7 @@
 
 #include <sys/prctl.h>
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <condition_variable>
@@ -76,7 +77,14 @@ struct Job {
   const void* src = nullptr;
   EventRef wait;  // issue after this HIP event completed
   SdmaRef after;  // and after this copy completed
+  // Polling of `wait` backs off while the compute stream is far behind (hipEventQuery is a
+  // runtime call that competes with the application's own launches).
+  int64_t next_query_ns = 0;
+  int64_t query_gap_ns = 0;
 };
+
+constexpr int64_t kQueryGapMinNs = 5000;
+constexpr int64_t kQueryGapMaxNs = 100000;
 
 struct InFlight {
   SdmaRef copy;
@@ -336,8 +344,14 @@ class SdmaLink : public Link {
   // Issue `job` if its dependencies are met. Returns true if the job left the queue.
   bool try_issue(Job& job) {
     if (job.wait) {
+      const int64_t now = now_ns();
+      if (now < job.next_query_ns) return false;
       const hipError_t q = hipEventQuery(job.wait->ev);
-      if (q == hipErrorNotReady) return false;
+      if (q == hipErrorNotReady) {
+        job.query_gap_ns = job.query_gap_ns ? std::min(2 * job.query_gap_ns, kQueryGapMaxNs) : kQueryGapMinNs;
+        job.next_query_ns = now + job.query_gap_ns;
+        return false;
+      }
       job.wait.reset();
       if (q != hipSuccess) {
         finish(job.copy, true);
