@@ -22,6 +22,7 @@ Prints ONE JSON line (stdout). Progress goes to stderr.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -166,6 +167,7 @@ def time_steps(model, opt, inputs, steps: int, warmup: int, label: str):
         torch.cuda.synchronize()
         log(f"{label}: warmup {i + 1}/{warmup} {time.perf_counter() - t0:.3f} s")
     torch.cuda.synchronize()
+    gc.collect()
     torch.cuda.reset_peak_memory_stats()
     start = time.perf_counter()
     for i in range(steps):
@@ -299,8 +301,12 @@ def capture_block_saves(model, inputs):
             key = (t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype)
             if key not in seen:
                 seen.add(key)
-                saved.append(t)
-        return t
+                # detached: a saved tensor's grad_fn would keep the whole graph (and every
+                # activation up to this block) alive after the forward is dropped
+                saved.append(t.detach())
+        # detached alias: returning `t` itself would tie outputs saved by their own node into
+        # a reference cycle through the graph that the collector cannot break
+        return t.detach()
 
     handles = [
         layer.register_forward_pre_hook(lambda m, a: state.__setitem__("on", True)),
@@ -325,6 +331,24 @@ def _same_bits(a, b) -> bool:
         return False
     dt = ints[a.element_size()]
     return bool(torch.equal(a.view(dt), b.view(dt)))
+
+
+PACK_PROFILE = ROOT / "profiles" / "mo_pack_kernel_block_microbench.md"
+
+
+def profiled_traffic():
+    """HBM bytes per mo_pack_kernel launch on the microbench workload, from the committed
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary (counters scaled by a calibration copy).
+    None when the summary is not there."""
+
+    import re
+
+    try:
+        text = PACK_PROFILE.read_text()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)\s*$", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 CAL_BYTES = 256 << 20
@@ -494,6 +518,11 @@ def run(args) -> dict:
     params = [p for p in model.parameters() if p.requires_grad]
     opt = torch.optim.AdamW(params, lr=1e-4, foreach=True)
     log(f"model built: {sum(p.numel() for p in model.parameters()) / 1e9:.2f} B params, {len(params)} adapter tensors")
+    # Long-lived objects (model, optimizer, modules) leave the cyclic collector's scope, as in a
+    # production training loop: a full collection over them stalls the host for ~100 ms at
+    # random steps, in every mode alike, which would otherwise dominate the step-time noise.
+    gc.collect()
+    gc.freeze()
 
     peaks = link_peaks(device)
     log(f"host link: {peaks}")
@@ -667,7 +696,8 @@ def main() -> int:
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
         "frac": round(src.get("pack_hbm_gbps", 0.0) / HBM_PEAK_GBPS, 4),
-        "traffic": None,
+        "traffic": profiled_traffic() if "micro" in result else None,
+        "traffic_source": PACK_PROFILE.name if "micro" in result else None,
         "algorithmic_bytes_per_launch": 2 * src.get("pack_bytes_per_launch", 0.0),
         "avg_launch_us": src.get("pack_avg_launch_us"),
     }

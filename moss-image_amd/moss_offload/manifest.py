@@ -102,7 +102,10 @@ class ManifestRecorder:
                 dup_of,
             )
         )
-        return tensor
+        # A detached alias, not the tensor itself: a node that saves its own output would
+        # otherwise hold that output, whose grad_fn holds the node, a cycle through C++ that
+        # the collector cannot break (the whole graph would outlive the forward).
+        return tensor.detach()
 
     # summaries -------------------------------------------------------------------------------
     def offloaded(self) -> list[SavedRecord]:

@@ -1,0 +1,159 @@
+"""CPU tests of the drop-in's host logic: the gate, the config-1 plumbing and the manifest probe.
+
+- The gate of ``activation_cpu_offload`` (reference training/activation_offload.py:92-93): on
+  the CPU, when disabled and under ``no_grad``, the drop-in is an exact no-op and never touches
+  the native library. ``test_activation_offload_is_cpu_noop`` restates the reference's own test
+  (training/tests/test_packed_features.py:188-198, seed 33, same tiny model sizes).
+- BASELINE config 1 on the CPU: one reference-topology block (hidden 512, 8x64 heads, MLP 2048,
+  fp32, 16x16 image + 64 text tokens) through the oracle's emulation of the reference hooks
+  with CPU payloads. Every restored tensor is bitwise equal to its save, and the loss and
+  every gradient are bitwise equal to the run without hooks. The manifest probe records the
+  same offloaded set the hooks packed.
+- The manifest probe lets the graph go when the forward is dropped (regression: a pack hook
+  that returns its argument ties outputs saved by their own node into an uncollectable cycle).
+"""
+
+from __future__ import annotations
+
+import copy
+import gc
+from contextlib import nullcontext
+
+import torch
+
+import moss_offload
+from moss_offload import dit, engine
+from moss_offload.manifest import ManifestRecorder
+from oracle import reference_hooks
+
+
+def _tiny(layers=2, checkpointing=False):
+    # sizes of the reference's _tiny (training/tests/test_packed_features.py:31-41)
+    return dit.MOSSImageTransformer(
+        dim=32, ffn_dim=64, num_heads=4, num_layers=layers, text_dim=16, freq_dim=8, latent_channels=4,
+        gradient_checkpointing=checkpointing,
+    )
+
+
+def test_activation_offload_is_cpu_noop() -> None:
+    torch.manual_seed(33)
+    base = _tiny().train()
+    offloaded = copy.deepcopy(base).train()
+    offloaded.activation_offload = True
+    target = torch.randn(1, 4, 2, 2)
+    context = torch.randn(1, 2, 16)
+    expected = base(target, torch.tensor([250.0]), context)
+    actual = offloaded(target, torch.tensor([250.0]), context)
+    torch.testing.assert_close(actual, expected)
+    actual.sum().backward()
+    assert not engine._ENGINES  # the CPU path never created a device engine
+
+
+def test_gate_returns_nullcontext_without_touching_the_engine() -> None:
+    model = _tiny()
+    cuda = torch.device("cuda", 0)
+    assert isinstance(moss_offload.activation_cpu_offload(model, True, torch.device("cpu")), nullcontext)
+    assert isinstance(moss_offload.activation_cpu_offload(model, False, cuda), nullcontext)
+    with torch.no_grad():
+        assert isinstance(moss_offload.activation_cpu_offload(model, True, cuda), nullcontext)
+    with torch.inference_mode():
+        assert isinstance(moss_offload.activation_cpu_offload(model, True, cuda), nullcontext)
+    assert not engine._ENGINES
+
+
+def _config1():
+    torch.manual_seed(0)
+    model = dit.MOSSImageTransformer(
+        dim=512, ffn_dim=2048, num_heads=8, num_layers=1, text_dim=64, freq_dim=32, latent_channels=16,
+    )
+    dit.init_weights(model)
+    dit.inject_lora(model, rank=8, alpha=8.0, b_std=0.03)
+    g = torch.Generator(device="cpu").manual_seed(0)
+    latent = torch.randn(1, 16, 16, 16, generator=g)
+    context = torch.randn(1, 64, 64, generator=g)
+    return model.train(), latent, context
+
+
+def _step(model, latent, context, hooks):
+    model.zero_grad(set_to_none=True)
+    with hooks:
+        out = model(latent, torch.tensor([500.0]), context)
+        loss = out.square().mean()
+    loss.backward()
+    grads = {n: p.grad.detach().clone() for n, p in model.named_parameters() if p.grad is not None}
+    return out.detach(), loss.detach(), grads
+
+
+def test_config1_block_through_emulated_reference_hooks_is_bitwise_identity() -> None:
+    model, latent, context = _config1()
+    expected = _step(copy.deepcopy(model), latent, context, nullcontext())
+    recorder = reference_hooks.Recorder()
+    hooked = copy.deepcopy(model)
+    actual = _step(hooked, latent, context, reference_hooks.emulated_offload(hooked, recorder))
+    assert reference_hooks.bitwise_equal(actual[0], expected[0])
+    assert reference_hooks.bitwise_equal(actual[1], expected[1])
+    assert actual[2].keys() == expected[2].keys() and len(actual[2]) > 0
+    for name in expected[2]:
+        assert reference_hooks.bitwise_equal(actual[2][name], expected[2][name]), name
+    # every offloaded save came back with its layout and bits
+    assert len(recorder.packed) > 30 and len(recorder.restored) == len(recorder.packed)
+    originals = {id(p): t for t, p in recorder.packed}
+    assert len(originals) == len(recorder.packed)
+    for original, payload in recorder.packed:
+        assert payload.is_contiguous()
+    by_bits = {}
+    for original, _ in recorder.packed:
+        by_bits.setdefault((tuple(original.shape), tuple(original.stride()), original.dtype), []).append(original)
+    for restored in recorder.restored:
+        candidates = by_bits[(tuple(restored.shape), tuple(restored.stride()), restored.dtype)]
+        assert any(reference_hooks.bitwise_equal(restored, c) for c in candidates)
+
+
+def test_manifest_matches_the_hooks_offloaded_set() -> None:
+    model, latent, context = _config1()
+    recorder = reference_hooks.Recorder()
+    hooked = copy.deepcopy(model)
+    with reference_hooks.emulated_offload(hooked, recorder):
+        hooked(latent, torch.tensor([500.0]), context).square().mean()
+    probe = ManifestRecorder(model, device_type="cpu")
+    with probe:
+        model(latent, torch.tensor([500.0]), context).square().mean()
+    offloaded = probe.offloaded()
+    assert len(offloaded) == len(recorder.packed)
+    assert sum(r.resident != "" for r in probe.records) == recorder.resident
+    assert probe.payload_bytes(unique=False) == recorder.payload_bytes
+    assert [tuple(r.shape) for r in offloaded] == [tuple(t.shape) for t, _ in recorder.packed]
+    # dup structure: fp32 RMSNorm saves its rsqrt statistic twice (square and mul)
+    assert any(r.dup_of is not None for r in offloaded)
+    assert probe.payload_bytes(unique=True) < probe.payload_bytes(unique=False)
+
+
+def _live_tensor_ids():
+    gc.collect()
+    return {id(o) for o in gc.get_objects() if type(o) is torch.Tensor}
+
+
+def test_manifest_probe_releases_the_graph() -> None:
+    torch.manual_seed(1)
+    model = _tiny(layers=2).train()
+    latent, context = torch.randn(1, 4, 4, 4), torch.randn(1, 3, 16)
+    model(latent, torch.tensor([300.0]), context).sum().backward()  # warm caches
+    before = _live_tensor_ids()
+    probe = ManifestRecorder(model, device_type="cpu")
+    with probe:
+        out = model(latent, torch.tensor([300.0]), context).sum()
+    assert len(probe.records) > 10
+    del out
+    assert _live_tensor_ids() - before == set()
+
+
+def test_manifest_probe_leaves_gradients_unchanged() -> None:
+    torch.manual_seed(2)
+    model = _tiny(layers=2).train()
+    dit.inject_lora(model, rank=2, alpha=4.0, b_std=0.03)
+    latent, context = torch.randn(1, 4, 4, 4), torch.randn(1, 3, 16)
+    expected = _step(copy.deepcopy(model), latent, context, nullcontext())
+    probed = copy.deepcopy(model)
+    actual = _step(probed, latent, context, ManifestRecorder(probed, device_type="cpu"))
+    for name in expected[2]:
+        assert reference_hooks.bitwise_equal(actual[2][name], expected[2][name]), name
