@@ -568,7 +568,9 @@ def run(args) -> dict:
             try:
                 seconds, peak = time_steps(model, opt, inputs, steps, warmup, f"{regime}/{mode}")
             except RuntimeError as exc:  # e.g. the reference hooks exhausting pinned host memory
-                log(f"{regime}/{mode} failed: {exc}")
+                import traceback
+
+                log(f"{regime}/{mode} failed: {exc}\n{traceback.format_exc(limit=-4)}")
                 entry[mode] = {"error": str(exc).splitlines()[0]}
                 opt.zero_grad(set_to_none=True)
                 torch.cuda.synchronize()
