@@ -41,6 +41,14 @@ CONFIG3 = dict(dim=3072, ffn_dim=12288, num_heads=24, num_layers=40, text_dim=40
 GRID = (64, 64)
 TEXT_TOKENS = 512
 LORA_RANK = 32
+# 2048^2 (128 x 128 latent grid) + 4096 text tokens
+C4_GRID = (128, 128)
+C4_TEXT = 4096
+# int8 weight-only bases, LoRA r16, batch of 4 aspect buckets (1024^2,
+# 768x1344, 1344x768, 896x1152 -> latent grids /16) with fixed text lengths
+C5_BUCKETS = ((64, 64), (48, 84), (84, 48), (56, 72))
+C5_TEXT = (512, 384, 448, 256)
+C5_RANK = 16
 
 
 def log(msg: str) -> None:
@@ -124,24 +132,81 @@ def build_model(device, layers: int):
     return model.train()
 
 
-def make_inputs(device):
+def make_inputs(device, grid=GRID, text=TEXT_TOKENS, seed=0):
     import torch
 
-    g = torch.Generator(device="cpu").manual_seed(0)
-    clean = torch.randn(1, CONFIG3["latent_channels"], *GRID, generator=g).to(device)
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    clean = torch.randn(1, CONFIG3["latent_channels"], *grid, generator=g).to(device)
     noise = torch.randn(clean.shape, generator=g).to(device)
-    context = torch.randn(1, TEXT_TOKENS, CONFIG3["text_dim"], generator=g).to(device)
+    context = torch.randn(1, text, CONFIG3["text_dim"], generator=g).to(device)
     sigma = torch.rand(1, generator=g).to(device)
     return clean, noise, sigma, context
 
 
-def loss_and_backward(model, inputs):
+def build_c5_model(device, layers: int):
+    """Config 5: config-3 dims with int8 weight-only joint-block bases and LoRA r16."""
+
     import torch
     from moss_offload import dit
 
+    torch.manual_seed(0)
+    cfg = dict(CONFIG3, num_layers=layers)
+    with torch.device(device):
+        model = dit.MOSSImageTransformer(**cfg)
+    model = model.to(torch.bfloat16)
+    dit.init_weights(model, std=0.02)
+    dit.quantize_joint_linears(model, torch.Generator(device=device).manual_seed(5))
+    dit.inject_lora(model, rank=C5_RANK, alpha=float(C5_RANK), b_std=0.03)
+    return model.train()
+
+
+def make_c5_batch(device):
+    return [make_inputs(device, grid, text, seed=50 + i) for i, (grid, text) in enumerate(zip(C5_BUCKETS, C5_TEXT))]
+
+
+def config3_forward(model, inputs):
+    """One shape group: the squared velocity error and its element count (train.py:102-157)."""
+
+    from moss_offload import dit
+
     clean, noise, sigma, context = inputs
+    return dit.squared_error(model, clean, noise, sigma, context)
+
+
+def grouped_forward(model, batch):
+    """Config 5 unpacked: one forward per shape group, so four live graphs before one backward."""
+
+    error, count = None, 0
+    for inputs in batch:
+        e, c = config3_forward(model, inputs)
+        error = e if error is None else error + e
+        count += c
+    return error, count
+
+
+def packed_forward(model, batch):
+    """Config 5 packed: one varlen traversal over the four samples (model.py:502-626)."""
+
+    import torch
+    from moss_offload import dit
+
+    noisy, velocity, contexts, sigmas = [], [], [], []
+    for clean, noise, sigma, context in batch:
+        n, v = dit.noisy_latent(clean, sigma, noise)
+        noisy.append(n[0].to(model.compute_dtype))
+        velocity.append(v[0])
+        contexts.append(context[0].to(model.compute_dtype))
+        sigmas.append(sigma)
+    outputs = model.forward_packed(noisy, torch.cat(sigmas).float() * 1000.0, contexts)
+    error = sum((o.float() - v.float()).square().sum() for o, v in zip(outputs, velocity))
+    return error, sum(v.numel() for v in velocity)
+
+
+def loss_and_backward(model, inputs, forward=config3_forward):
+    import torch
+
     with torch.autocast("cuda", dtype=torch.bfloat16):
-        error, count = dit.squared_error(model, clean, noise, sigma, context)
+        error, count = forward(model, inputs)
     loss = error / count
     loss.backward()
     return loss.detach()
@@ -156,13 +221,13 @@ def configure_mode(model, mode: str, regime: str):
     model.offload_context = reference_offload_context if mode == "reference" else moss_offload.activation_cpu_offload
 
 
-def time_steps(model, opt, inputs, steps: int, warmup: int, label: str):
+def time_steps(model, opt, inputs, steps: int, warmup: int, label: str, forward=config3_forward):
     import torch
 
     for i in range(warmup):
         t0 = time.perf_counter()
         opt.zero_grad(set_to_none=True)
-        loss_and_backward(model, inputs)
+        loss_and_backward(model, inputs, forward)
         opt.step()
         torch.cuda.synchronize()
         log(f"{label}: warmup {i + 1}/{warmup} {time.perf_counter() - t0:.3f} s")
@@ -172,7 +237,7 @@ def time_steps(model, opt, inputs, steps: int, warmup: int, label: str):
     start = time.perf_counter()
     for i in range(steps):
         opt.zero_grad(set_to_none=True)
-        loss_and_backward(model, inputs)
+        loss_and_backward(model, inputs, forward)
         opt.step()
     torch.cuda.synchronize()
     elapsed = (time.perf_counter() - start) / steps
@@ -247,7 +312,7 @@ def link_peaks(device, nbytes: int = 256 << 20, iters: int = 10):
     return {k: round(v, 2) for k, v in out.items()}
 
 
-def record_manifest(model, inputs, regime: str):
+def record_manifest(model, inputs, regime: str, forward=config3_forward):
     """Saved-tensor manifest of one step's forward in the given regime (bytes the hooks see)."""
 
     import torch
@@ -261,12 +326,9 @@ def record_manifest(model, inputs, regime: str):
         layer.register_forward_pre_hook(lambda m, a: marks.append(len(recorder.records))),
         layer.register_forward_hook(lambda m, a, o: marks.append(len(recorder.records))),
     ]
-    clean, noise, sigma, context = inputs
     try:
         with recorder, torch.autocast("cuda", dtype=torch.bfloat16):
-            from moss_offload import dit
-
-            error, _ = dit.squared_error(model, clean, noise, sigma, context)
+            error, _ = forward(model, inputs)
     finally:
         for h in handles:
             h.remove()
@@ -545,34 +607,56 @@ def run(args) -> dict:
             f"{m['unpack_hbm_gbps']:.0f} GB/s, bitwise {m['bitwise_first'] and m['bitwise_last']}")
         del tensors
 
-    for regime in (r for r in args.regimes if r != "M"):
-        manifest = record_manifest(model, inputs, regime)
+    c5 = {}
+
+    def workload(name):
+        """(model, optimizer, inputs, forward, checkpoint regime) of a bench leg."""
+
+        if name in ("A", "B"):
+            return model, opt, inputs, config3_forward, name
+        if name == "A4":
+            return model, opt, make_inputs(device, C4_GRID, C4_TEXT, seed=4), config3_forward, "A"
+        if name in ("C5U", "C5P"):
+            if not c5:
+                c5["model"] = build_c5_model(device, args.layers)
+                c5["opt"] = torch.optim.AdamW([p for p in c5["model"].parameters() if p.requires_grad], lr=1e-4,
+                                              foreach=True)
+                c5["batch"] = make_c5_batch(device)
+                gc.collect()
+                gc.freeze()
+            forward = grouped_forward if name == "C5U" else packed_forward
+            return c5["model"], c5["opt"], c5["batch"], forward, "A"
+        raise ValueError(f"unknown regime {name}")
+
+    for regime_name in (r for r in args.regimes if r != "M"):
+        wl_model, wl_opt, wl_inputs, forward, regime = workload(regime_name)
+        manifest = record_manifest(wl_model, wl_inputs, regime, forward)
         payload_unique = manifest.payload_bytes(unique=True)
         payload_copied = manifest.payload_bytes(unique=False)
         torch.cuda.synchronize()
-        log(f"regime {regime}: hooks see {len(manifest.records)} saves, payload {payload_unique / 1e9:.2f} GB unique "
-            f"({payload_copied / 1e9:.2f} GB as the reference copies it)")
-        steps = args.steps if regime == "A" else max(1, args.steps_b)
-        warmup = args.warmup if regime == "A" else max(1, args.warmup_b)
+        log(f"regime {regime_name}: hooks see {len(manifest.records)} saves, payload {payload_unique / 1e9:.2f} GB "
+            f"unique ({payload_copied / 1e9:.2f} GB as the reference copies it)")
+        steps = args.steps if regime_name == "A" else max(1, args.steps_b)
+        warmup = args.warmup if regime_name == "A" else max(1, args.warmup_b)
         block = [r for r in manifest.block if not r.resident]
         entry = {"payload_unique_bytes": payload_unique, "payload_copied_bytes": payload_copied,
                  "saves": len(manifest.records),
                  "block_payload_unique_bytes": sum(r.payload_bytes for r in block if r.dup_of is None),
                  "block_payload_copied_bytes": sum(r.payload_bytes for r in block)}
-        if regime == "B":
+        if regime_name == "B":
             entry["cpu_sample"] = manifest
         for mode in args.modes:
-            configure_mode(model, mode, regime)
+            configure_mode(wl_model, mode, regime)
             engine = get_engine(device)
             engine.reset_stats()
             try:
-                seconds, peak = time_steps(model, opt, inputs, steps, warmup, f"{regime}/{mode}")
+                seconds, peak = time_steps(wl_model, wl_opt, wl_inputs, steps, warmup, f"{regime_name}/{mode}", forward)
             except RuntimeError as exc:  # e.g. the reference hooks exhausting pinned host memory
                 import traceback
 
-                log(f"{regime}/{mode} failed: {exc}\n{traceback.format_exc(limit=-4)}")
+                log(f"{regime_name}/{mode} failed: {exc}\n{traceback.format_exc(limit=-4)}")
                 entry[mode] = {"error": str(exc).splitlines()[0]}
-                opt.zero_grad(set_to_none=True)
+                wl_opt.zero_grad(set_to_none=True)
                 torch.cuda.synchronize()
                 torch._C._host_emptyCache()
                 continue
@@ -616,7 +700,7 @@ def run(args) -> dict:
         ref = entry.get("reference")
         if none is not None and ref is not None and "s_per_it" in ref:
             ref["exposed_s"] = ref["s_per_it"] - none
-        result["regimes"][regime] = entry
+        result["regimes"][regime_name] = entry
     return result
 
 
@@ -627,7 +711,9 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--steps-b", type=int, default=2)
     parser.add_argument("--warmup-b", type=int, default=1)
-    parser.add_argument("--regimes", default="M,A,B", help="M = config-2 block microbench, A/B = config-3 steps")
+    parser.add_argument("--regimes", default="M,A,B",
+                        help="M = config-2 block microbench, A/B = config-3 steps (checkpointed / not), "
+                        "A4 = config 4 (2048^2, regime A), C5U/C5P = config 5 unpacked / packed (regime A)")
     parser.add_argument("--micro-iters", type=int, default=200)
     parser.add_argument("--micro-warmup", type=int, default=3)
     parser.add_argument("--modes", default="none,engine,reference")

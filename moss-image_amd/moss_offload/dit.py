@@ -452,7 +452,17 @@ class FrozenInt8Linear(nn.Module):
 def joint_linear_names(model: MOSSImageTransformer) -> list[str]:
     """Linear modules of the joint blocks, the ``joint`` LoRA target set (lora.py:117-148)."""
 
-    return [name for name, module in model.named_modules() if isinstance(module, nn.Linear) and name.startswith("layers.")]
+    return [
+        name
+        for name, module in model.named_modules()
+        if isinstance(module, (nn.Linear, FrozenInt8Linear)) and name.startswith("layers.")
+    ]
+
+
+def _module_device(module: nn.Module) -> torch.device:
+    for tensor in (*module.parameters(), *module.buffers()):
+        return tensor.device
+    return torch.device("cpu")
 
 
 def _replace(root: nn.Module, qualified: str, module: nn.Module) -> None:
@@ -478,7 +488,7 @@ def inject_lora(model: MOSSImageTransformer, rank: int, alpha: float, b_std: flo
     names = joint_linear_names(model)
     for name in names:
         base = model.get_submodule(name)
-        wrapped = LoRALinear(base, rank, alpha).to(device=base.weight.device)
+        wrapped = LoRALinear(base, rank, alpha).to(device=_module_device(base))
         if b_std is not None:
             with torch.no_grad():
                 wrapped.lora_B.normal_(0.0, b_std)
@@ -493,7 +503,7 @@ def quantize_joint_linears(model: MOSSImageTransformer, generator: torch.Generat
     and stored fp32 (quantization.py:86-91, :116-121 keep scales fp32).
     """
 
-    names = joint_linear_names(model)
+    names = [name for name in joint_linear_names(model) if isinstance(model.get_submodule(name), nn.Linear)]
     for name in names:
         base = model.get_submodule(name)
         device, dtype = base.weight.device, base.weight.dtype

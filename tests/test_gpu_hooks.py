@@ -201,6 +201,47 @@ def test_several_forwards_one_backward() -> None:
     _compare(actual, expected, rtol=5e-5, atol=5e-6)
 
 
+def _config5_tiny(device):
+    torch.manual_seed(907)
+    model = _tiny(layers=3, checkpointing=True, dim=64, ffn=128, heads=4)
+    model = model.to(device).to(torch.bfloat16)
+    dit.quantize_joint_linears(model, torch.Generator(device=device).manual_seed(5))
+    dit.inject_lora(model, rank=4, alpha=4.0)
+    return model.train()
+
+
+def _packed_run(model, context_factory, enabled, latents, contexts):
+    model.activation_offload = enabled
+    model.offload_context = context_factory
+    model.zero_grad(set_to_none=True)
+    t = torch.linspace(200.0, 800.0, len(latents), device=latents[0].device)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        outputs = model.forward_packed([x[0] for x in latents], t, [c[0] for c in contexts])
+        loss = sum(o.float().square().mean() for o in outputs)
+    loss.backward()
+    grads = {n: p.grad.detach().clone() for n, p in model.named_parameters() if p.grad is not None}
+    return [o.detach() for o in outputs], loss.detach(), grads
+
+
+def test_config5_int8_lora_grouped_and_packed_match_no_offload() -> None:
+    """Config-5 shape: int8 weight-only bases (their int8 weights and fp32 scales are buffers and
+    stay resident), LoRA, checkpointed blocks, four aspect buckets, both batching modes."""
+
+    device = torch.device("cuda", 0)
+    base = _config5_tiny(device)
+    latents, contexts = _inputs(device, shapes=((4, 4, 4), (4, 3, 5), (4, 5, 3), (4, 4, 6)), text=(6, 4, 5, 3))
+    for runner in (_run, _packed_run):
+        kwargs = {"autocast": True} if runner is _run else {}
+        expected = runner(copy.deepcopy(base), moss_offload.activation_cpu_offload, False, latents, contexts, **kwargs)
+        _Recording.log, _Recording.checked = {}, 0
+        actual = runner(copy.deepcopy(base), _recording_context, True, latents, contexts, **kwargs)
+        assert _Recording.checked > 0
+        assert len(expected[2]) > 0
+        # every restored tensor was checked bitwise above; outputs and gradients within the
+        # north_star bf16 tolerance (backward reductions may order differently run to run)
+        _compare(actual, expected, rtol=1e-3, atol=1e-5)
+
+
 def test_weight_backed_and_staging_buffers_stay_resident() -> None:
     device = torch.device("cuda", 0)
     model = _tiny().to(device).train()
