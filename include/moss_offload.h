@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 3
+#define MO_ABI_VERSION 4
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -178,6 +178,48 @@ int mo_trim(mo_engine* engine);
 
 /* Name of the host-link transport in use: "sdma" or "kernel". */
 const char* mo_link_name(mo_engine* engine);
+
+/* ---- frozen-block streaming (AsyncBlockStreamer, training/memory.py:93-361) -------------- */
+
+/* Pinned host memory of `bytes` rounded up to a page, for the block masters of a streamed
+ * model (replaces torch.empty(..., pin_memory=True) at memory.py:461, which rounds each pin up to
+ * a power of two). Independent of any engine; free with mo_pinned_free. */
+int mo_pinned_alloc(uint64_t bytes, uint64_t* host);
+int mo_pinned_free(uint64_t host);
+
+typedef struct mo_streamer mo_streamer;
+
+typedef struct mo_streamer_stats {
+  uint64_t fills, bytes;        /* slot fills issued and their bytes                        */
+  uint64_t timed_bytes;         /* bytes of completed fills                                 */
+  double busy_ms;               /* SDMA busy time of completed fills (host clock)           */
+  uint64_t host_blocks;         /* acquires that had to block the host for a fill           */
+  double host_block_ms;
+  uint64_t copy_failures;
+} mo_streamer_stats;
+
+/* A streamer with `slots` device staging slots (the buffers themselves belong to the caller)
+ * and its own SDMA H2D queue (h2d_engine: SDMA engine bit, 0 = first available). Replaces the
+ * copy stream and slot events of AsyncBlockStreamer (memory.py:109-119). */
+int mo_streamer_create(int device, uint32_t slots, uint32_t h2d_engine, mo_streamer** out);
+int mo_streamer_destroy(mo_streamer* streamer);
+
+/* Copy `bytes` from pinned host `src` to device `dst` (the slot's buffer) once the GPU has
+ * passed the slot's last mo_streamer_release point. Never blocks the host. Replaces
+ * target.copy_(block.cpu_buffer, non_blocking=True) on the copy stream, memory.py:163-174. */
+int mo_streamer_fill(mo_streamer* streamer, uint32_t slot, uint64_t dst, uint64_t src, uint64_t bytes);
+
+/* Work enqueued on `stream` after this call sees the slot's last fill complete: the host waits
+ * for the copy (bounded). Replaces compute_stream.wait_event(slot.ready), memory.py:246-247. */
+int mo_streamer_acquire(mo_streamer* streamer, uint32_t slot, uint64_t stream);
+
+/* The slot may be refilled once `stream` reaches this point. Replaces the slot.reusable events
+ * of memory.py:193-225. */
+int mo_streamer_release(mo_streamer* streamer, uint32_t slot, uint64_t stream);
+
+int mo_streamer_synchronize(mo_streamer* streamer);
+int mo_streamer_get_stats(mo_streamer* streamer, mo_streamer_stats* stats);
+int mo_streamer_reset_stats(mo_streamer* streamer);
 
 #ifdef __cplusplus
 }

@@ -45,6 +45,14 @@ int hip_fail(int e, const char* what) {
   return e;
 }
 
+}  // namespace
+
+// Error setters shared with the other C-ABI translation units (mo_streamer.cpp).
+int set_error(int code, const std::string& msg) { return fail(code, msg); }
+int set_hip_error(int e, const char* what) { return hip_fail(e, what); }
+
+namespace {
+
 #define MO_HIP(call)                                       \
   do {                                                     \
     hipError_t _e = (call);                                \

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 3
+MO_ABI_VERSION = 4
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -107,6 +107,21 @@ class MoStats(ctypes.Structure):
         return {name: getattr(self, name) for name, _ in self._fields_}
 
 
+class MoStreamerStats(ctypes.Structure):
+    _fields_ = [
+        ("fills", ctypes.c_uint64),
+        ("bytes", ctypes.c_uint64),
+        ("timed_bytes", ctypes.c_uint64),
+        ("busy_ms", ctypes.c_double),
+        ("host_blocks", ctypes.c_uint64),
+        ("host_block_ms", ctypes.c_double),
+        ("copy_failures", ctypes.c_uint64),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
 class EngineError(RuntimeError):
     """A non-zero status from the engine library, with its message."""
 
@@ -142,6 +157,16 @@ SIGNATURES: dict[str, tuple] = {
     "mo_reset_stats": (ctypes.c_int, [ctypes.c_void_p]),
     "mo_trim": (ctypes.c_int, [ctypes.c_void_p]),
     "mo_link_name": (ctypes.c_char_p, [ctypes.c_void_p]),
+    "mo_pinned_alloc": (ctypes.c_int, [_u64, _P(_u64)]),
+    "mo_pinned_free": (ctypes.c_int, [_u64]),
+    "mo_streamer_create": (ctypes.c_int, [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, _P(ctypes.c_void_p)]),
+    "mo_streamer_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "mo_streamer_fill": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64, _u64, _u64]),
+    "mo_streamer_acquire": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64]),
+    "mo_streamer_release": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64]),
+    "mo_streamer_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
+    "mo_streamer_get_stats": (ctypes.c_int, [ctypes.c_void_p, _P(MoStreamerStats)]),
+    "mo_streamer_reset_stats": (ctypes.c_int, [ctypes.c_void_p]),
 }
 
 _lock = threading.Lock()

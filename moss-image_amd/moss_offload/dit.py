@@ -291,8 +291,9 @@ class MOSSImageTransformer(nn.Module):
         head = self.video_head_modulation(time.to(_linear_dtype(self.video_head_modulation)))
         return modulation.view(batch, 6, -1), head.view(batch, 2, -1)
 
-    def forward(self, hidden_states, timestep, encoder_hidden_states, encoder_attention_mask=None):
+    def forward(self, hidden_states, timestep, encoder_hidden_states, encoder_attention_mask=None, skip_layers=None):
         batch = hidden_states.shape[0]
+        skipped = frozenset(skip_layers or ())
         mask = encoder_attention_mask
         if mask is None:
             mask = torch.ones(encoder_hidden_states.shape[:2], dtype=torch.bool, device=hidden_states.device)
@@ -303,7 +304,8 @@ class MOSSImageTransformer(nn.Module):
                 context = encoder_hidden_states[index : index + 1, mask[index].bool()]
                 outputs.append(
                     self._forward_sample(
-                        hidden_states[index : index + 1], context, modulation[index : index + 1], head[index : index + 1]
+                        hidden_states[index : index + 1], context, modulation[index : index + 1],
+                        head[index : index + 1], skipped,
                     )
                 )
         return torch.cat(outputs)
@@ -312,7 +314,7 @@ class MOSSImageTransformer(nn.Module):
         tokens = latents.flatten(2).transpose(1, 2)
         return self.video_embedder(tokens.to(_linear_dtype(self.video_embedder)).contiguous())
 
-    def _forward_sample(self, hidden_states, context, modulation, head):
+    def _forward_sample(self, hidden_states, context, modulation, head, skipped=frozenset()):
         _, _, height, width = hidden_states.shape
         video = self._project_video(hidden_states)
         rope = self.rope([(0, height, width)], context.shape[1], hidden_states.device).to(video.dtype)
@@ -320,7 +322,7 @@ class MOSSImageTransformer(nn.Module):
         tokens = torch.cat((video, text), 1)
         if self.training and not tokens.requires_grad:
             tokens.requires_grad_(True)
-        tokens = self._run_layers(tokens, rope, modulation)
+        tokens = self._run_layers(tokens, rope, modulation, skipped=skipped)
         predicted = self.final_norm_video(tokens[:, : height * width].to(self.final_norm_video.weight.dtype))
         predicted = predicted * (1 + head[:, 1, None]) + head[:, 0, None]
         predicted = self.final_linear_video(predicted.to(_linear_dtype(self.final_linear_video)))
@@ -363,11 +365,38 @@ class MOSSImageTransformer(nn.Module):
                 offset += joint
             return outputs
 
-    def _run_layers(self, tokens, rope, modulation, cu_seqlens=None):
+    def _run_layers(self, tokens, rope, modulation, cu_seqlens=None, skipped=frozenset()):
+        """Joint blocks with swapping and selective checkpointing (reference model.py:672-710).
+
+        Blocks from ``len(layers) - blocks_to_swap`` on are swapped (``moss_offload.memory``):
+        streamed through ``block_swap_manager`` with the next block in traversal order
+        prefetched (forward: the following block; recomputation in backward: the preceding
+        one), or run from the CPU with ``offloaded_block`` in synchronous mode.
+        """
+
+        boundary = len(self.layers) - getattr(self, "blocks_to_swap", 0)
+        manager = getattr(self, "block_swap_manager", None)
+        streamed = [index for index in range(boundary, len(self.layers)) if index not in skipped]
+        position = {index: p for p, index in enumerate(streamed)}
         checkpointed = checkpointed_layer_indices(len(self.layers), self.checkpoint_fraction)
         for index, layer in enumerate(self.layers):
+            if index in skipped:
+                continue
             inputs = (tokens, rope, modulation) if cu_seqlens is None else (tokens, rope, modulation, cu_seqlens)
-            if self.gradient_checkpointing and self.training and index in checkpointed:
+            if manager is not None and index >= boundary:
+                p = position[index]
+                tokens = manager.block(
+                    index,
+                    *inputs,
+                    forward_prefetch=streamed[p + 1] if p + 1 < len(streamed) else None,
+                    backward_prefetch=streamed[p - 1] if p else None,
+                    checkpoint_block=torch.is_grad_enabled(),
+                )
+            elif index >= boundary:
+                from .memory import offloaded_block
+
+                tokens = offloaded_block(layer, *inputs)
+            elif self.gradient_checkpointing and self.training and index in checkpointed:
                 tokens = checkpoint(layer, *inputs, use_reentrant=False)
             else:
                 tokens = layer(*inputs)
