@@ -22,6 +22,7 @@ Prints ONE JSON line (stdout). Progress goes to stderr.
 from __future__ import annotations
 
 import argparse
+import copy
 import gc
 import json
 import os
@@ -626,6 +627,50 @@ def run(args) -> dict:
                 gc.freeze()
             forward = grouped_forward if name == "C5U" else packed_forward
             return c5["model"], c5["opt"], c5["batch"], forward, "A"
+        if name == "S5":
+            # config 5's low-VRAM path: every joint block streamed from pinned host masters
+            # (frozen int8 bases; adapters stay on the device), packed batch
+            if "streamed" not in c5:
+                workload("C5P")
+                from moss_offload.memory import place_model
+
+                streamed = copy.deepcopy(c5["model"])
+                place_model(streamed, device, len(streamed.layers), block_swap_mode="async")
+                c5["streamed"] = streamed
+                c5["streamed_opt"] = torch.optim.AdamW([p for p in streamed.parameters() if p.requires_grad],
+                                                       lr=1e-4, foreach=True)
+
+                def loss_and_grads(m):
+                    configure_mode(m, "none", "A")
+                    m.zero_grad(set_to_none=True)
+                    loss = loss_and_backward(m, c5["batch"], packed_forward)
+                    grads = [p.grad.detach().float().clone() for p in m.parameters() if p.grad is not None]
+                    m.zero_grad(set_to_none=True)
+                    return loss.float(), grads
+
+                base_loss, base_grads = loss_and_grads(c5["model"])
+                loss, grads = loss_and_grads(streamed)
+                num = sum(float((g - b).norm() ** 2) for g, b in zip(grads, base_grads)) ** 0.5
+                den = sum(float(b.norm() ** 2) for b in base_grads) ** 0.5
+                def device_bytes(m):
+                    tensors = {t.untyped_storage().data_ptr(): t.untyped_storage().nbytes()
+                               for t in (*m.parameters(), *m.buffers()) if t.is_cuda}
+                    manager = getattr(m, "block_swap_manager", None)
+                    if manager is not None:
+                        tensors.update({b.data_ptr(): b.numel() for b in manager.owned_cuda_buffers()})
+                    return sum(tensors.values())
+
+                result["stream_parity"] = {"loss_bitwise": bool(torch.equal(loss, base_loss)),
+                                           "loss_rel": abs(float((loss - base_loss) / base_loss)),
+                                           "grad_rel": num / den, "grads": len(grads),
+                                           "resident_model_device_bytes": device_bytes(c5["model"]),
+                                           "streamed_model_device_bytes": device_bytes(streamed)}
+                log(f"stream parity: {result['stream_parity']}")
+                del base_grads, grads
+                torch.cuda.empty_cache()
+                gc.collect()
+                gc.freeze()
+            return c5["streamed"], c5["streamed_opt"], c5["batch"], packed_forward, "A"
         raise ValueError(f"unknown regime {name}")
 
     for regime_name in (r for r in args.regimes if r != "M"):
@@ -645,10 +690,13 @@ def run(args) -> dict:
                  "block_payload_copied_bytes": sum(r.payload_bytes for r in block)}
         if regime_name == "B":
             entry["cpu_sample"] = manifest
+        streamer = getattr(wl_model, "block_swap_manager", None)
         for mode in args.modes:
             configure_mode(wl_model, mode, regime)
             engine = get_engine(device)
             engine.reset_stats()
+            if streamer is not None:
+                streamer.reset_stats()
             try:
                 seconds, peak = time_steps(wl_model, wl_opt, wl_inputs, steps, warmup, f"{regime_name}/{mode}", forward)
             except RuntimeError as exc:  # e.g. the reference hooks exhausting pinned host memory
@@ -661,6 +709,18 @@ def run(args) -> dict:
                 torch._C._host_emptyCache()
                 continue
             record = {"s_per_it": seconds, "peak_device_bytes": peak}
+            if streamer is not None:
+                torch.cuda.synchronize()
+                ss = streamer.stats()
+                n = steps + warmup
+                record["stream"] = {
+                    "fills_per_step": ss["fills"] / n,
+                    "bytes_per_step": ss["bytes"] / n,
+                    "busy_s_per_step": ss["busy_ms"] / 1e3 / n,
+                    "h2d_gbps": ss["timed_bytes"] / max(ss["busy_ms"], 1e-9) / 1e6,
+                    "host_block_ms_per_step": ss["host_block_ms"] / n,
+                    "copy_failures": ss["copy_failures"],
+                }
             if mode == "engine":
                 engine.synchronize()
                 st = engine.stats()
@@ -713,7 +773,8 @@ def main() -> int:
     parser.add_argument("--warmup-b", type=int, default=1)
     parser.add_argument("--regimes", default="M,A,B",
                         help="M = config-2 block microbench, A/B = config-3 steps (checkpointed / not), "
-                        "A4 = config 4 (2048^2, regime A), C5U/C5P = config 5 unpacked / packed (regime A)")
+                        "A4 = config 4 (2048^2, regime A), C5U/C5P = config 5 unpacked / packed (regime A), "
+                        "S5 = config 5 packed with every block streamed from pinned host masters")
     parser.add_argument("--micro-iters", type=int, default=200)
     parser.add_argument("--micro-warmup", type=int, default=3)
     parser.add_argument("--modes", default="none,engine,reference")
