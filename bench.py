@@ -161,6 +161,50 @@ def build_c5_model(device, layers: int):
     return model.train()
 
 
+class InBackwardSGD:
+    """Full-parameter SGD applied inside backward by post-accumulate-grad hooks: the shape of a
+    fused optimizer such as the reference's FusedAdafactor (fused_adafactor.py:478-515), which the
+    trainable block ring requires. Each hook updates its parameter in place and reports it."""
+
+    def __init__(self, model, lr: float, streamer=None) -> None:
+        self.lr = lr
+        self.streamer = streamer
+        for p in model.parameters():
+            if p.requires_grad:
+                p.register_post_accumulate_grad_hook(self._hook)
+
+    def _hook(self, p) -> None:
+        import torch
+
+        grad = p.grad
+        p.grad = None
+        with torch.no_grad():
+            p.add_(grad, alpha=-self.lr)
+        if self.streamer is not None:
+            self.streamer.mark_updated(p)
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        pass
+
+    def step(self) -> None:
+        if self.streamer is not None:
+            self.streamer.finish_backward()
+
+
+def build_full_model(device, layers: int):
+    """Config-3 dims, bf16, every parameter trainable (full fine-tuning)."""
+
+    import torch
+    from moss_offload import dit
+
+    torch.manual_seed(0)
+    with torch.device(device):
+        model = dit.MOSSImageTransformer(**dict(CONFIG3, num_layers=layers))
+    model = model.to(torch.bfloat16)
+    dit.init_weights(model, std=0.02)
+    return model.train()
+
+
 def make_c5_batch(device):
     return [make_inputs(device, grid, text, seed=50 + i) for i, (grid, text) in enumerate(zip(C5_BUCKETS, C5_TEXT))]
 
@@ -609,6 +653,7 @@ def run(args) -> dict:
         del tensors
 
     c5 = {}
+    full = {}
 
     def workload(name):
         """(model, optimizer, inputs, forward, checkpoint regime) of a bench leg."""
@@ -671,6 +716,24 @@ def run(args) -> dict:
                 gc.collect()
                 gc.freeze()
             return c5["streamed"], c5["streamed_opt"], c5["batch"], packed_forward, "A"
+        if name in ("F3", "F3S"):
+            # full-parameter training with an in-backward optimizer; F3S streams every block
+            # through the trainable two-slot ring (async_full)
+            if name not in full:
+                if "F3" not in full:
+                    resident = build_full_model(device, args.layers)
+                    full["F3"] = (resident, InBackwardSGD(resident, 1e-6))
+                if name == "F3S":
+                    from moss_offload.memory import place_model
+
+                    streamed = build_full_model(device, args.layers)
+                    place_model(streamed, device, len(streamed.layers), block_swap_mode="async_full")
+                    full["F3S"] = (streamed, InBackwardSGD(streamed, 1e-6, streamed.block_swap_manager))
+                torch.cuda.empty_cache()
+                gc.collect()
+                gc.freeze()
+            model_f, opt_f = full[name]
+            return model_f, opt_f, inputs, config3_forward, "A"
         raise ValueError(f"unknown regime {name}")
 
     for regime_name in (r for r in args.regimes if r != "M"):
@@ -720,6 +783,10 @@ def run(args) -> dict:
                     "h2d_gbps": ss["timed_bytes"] / max(ss["busy_ms"], 1e-9) / 1e6,
                     "host_block_ms_per_step": ss["host_block_ms"] / n,
                     "copy_failures": ss["copy_failures"],
+                    "writebacks_per_step": ss["writebacks"] / n,
+                    "writeback_bytes_per_step": ss["writeback_bytes"] / n,
+                    "writeback_busy_s_per_step": ss["writeback_busy_ms"] / 1e3 / n,
+                    "writeback_gbps": ss["timed_writeback_bytes"] / max(ss["writeback_busy_ms"], 1e-9) / 1e6,
                 }
             if mode == "engine":
                 engine.synchronize()
@@ -774,7 +841,8 @@ def main() -> int:
     parser.add_argument("--regimes", default="M,A,B",
                         help="M = config-2 block microbench, A/B = config-3 steps (checkpointed / not), "
                         "A4 = config 4 (2048^2, regime A), C5U/C5P = config 5 unpacked / packed (regime A), "
-                        "S5 = config 5 packed with every block streamed from pinned host masters")
+                        "S5 = config 5 packed with every block streamed from pinned host masters, "
+                        "F3/F3S = full-parameter training at config-3 dims, resident / every block on the trainable ring")
     parser.add_argument("--micro-iters", type=int, default=200)
     parser.add_argument("--micro-warmup", type=int, default=3)
     parser.add_argument("--modes", default="none,engine,reference")

@@ -1,5 +1,5 @@
 /*
- * moss_offload.h - C ABI of the MI355X activation-offload engine.
+ * moss_offload.h - C ABI of the MI355X activation-offload engine and block streamer.
  *
  * The engine replaces the per-tensor work that MOSS-Image's saved-tensor hooks do in
  * training/activation_offload.py (reference repository RyukoMatoiFan/MOSS-Image):
@@ -179,7 +179,8 @@ int mo_trim(mo_engine* engine);
 /* Name of the host-link transport in use: "sdma" or "kernel". */
 const char* mo_link_name(mo_engine* engine);
 
-/* ---- frozen-block streaming (AsyncBlockStreamer, training/memory.py:93-361) -------------- */
+/* ---- block streaming (AsyncBlockStreamer, training/memory.py:93-361; TrainableBlockStreamer,
+ * training/trainable_offload.py:89-477) --------------------------------------------------- */
 
 /* Pinned host memory of `bytes` rounded up to a page, for the block masters of a streamed
  * model (replaces torch.empty(..., pin_memory=True) at memory.py:461, which rounds each pin up to
@@ -196,11 +197,15 @@ typedef struct mo_streamer_stats {
   uint64_t host_blocks;         /* acquires that had to block the host for a fill           */
   double host_block_ms;
   uint64_t copy_failures;
+  uint64_t writebacks, writeback_bytes;  /* slot write-backs issued and their bytes          */
+  uint64_t timed_writeback_bytes;        /* bytes of completed write-backs                  */
+  double writeback_busy_ms;              /* SDMA busy time of completed write-backs         */
 } mo_streamer_stats;
 
 /* A streamer with `slots` device staging slots (the buffers themselves belong to the caller)
- * and its own SDMA H2D queue (h2d_engine: SDMA engine bit, 0 = first available). Replaces the
- * copy stream and slot events of AsyncBlockStreamer (memory.py:109-119). */
+ * and its own SDMA queues (h2d_engine: SDMA engine bit for fills, 0 = first available other than
+ * the write-back engine). Replaces the copy stream and slot events of AsyncBlockStreamer
+ * (memory.py:109-119) and TrainableBlockStreamer (trainable_offload.py:128-179). */
 int mo_streamer_create(int device, uint32_t slots, uint32_t h2d_engine, mo_streamer** out);
 int mo_streamer_destroy(mo_streamer* streamer);
 
@@ -208,6 +213,12 @@ int mo_streamer_destroy(mo_streamer* streamer);
  * passed the slot's last mo_streamer_release point. Never blocks the host. Replaces
  * target.copy_(block.cpu_buffer, non_blocking=True) on the copy stream, memory.py:163-174. */
 int mo_streamer_fill(mo_streamer* streamer, uint32_t slot, uint64_t dst, uint64_t src, uint64_t bytes);
+
+/* Copy the slot's device contents `src` back to its pinned master `dst` once the GPU has passed
+ * the slot's last mo_streamer_release point; the slot's next fill waits for this copy. Never
+ * blocks the host. Replaces the dirty-slot eviction of TrainableBlockStreamer
+ * (training/trainable_offload.py:245-260). */
+int mo_streamer_writeback(mo_streamer* streamer, uint32_t slot, uint64_t dst, uint64_t src, uint64_t bytes);
 
 /* Work enqueued on `stream` after this call sees the slot's last fill complete: the host waits
  * for the copy (bounded). Replaces compute_stream.wait_event(slot.ready), memory.py:246-247. */

@@ -204,6 +204,20 @@ class SdmaLink : public Link {
     return 0;
   }
 
+  int writeback(void* dst, const void* src, uint64_t bytes, int gate, CopyRef* out) override {
+    auto copy = make_copy(true, bytes);
+    Job job;
+    job.copy = copy;
+    job.dst = dst;
+    job.src = src;
+    job.wait = gates_[gate].consumed;
+    enqueue(std::move(job));
+    gates_[gate].last = copy;
+    d2h_bytes_ += bytes;
+    *out = copy;
+    return 0;
+  }
+
   // Host-side: return once the gate's last copy finished. The caller enqueues the dependent
   // GPU work afterwards, so stream order does the rest.
   int wait(int gate, hipStream_t compute) override {
@@ -571,6 +585,13 @@ class StreamLink : public Link {
     auto prev = std::dynamic_pointer_cast<StreamCopy>(after);
     if (prev && (e = hipStreamWaitEvent(h2d_, prev->ev, 0)) != hipSuccess) return (int)e;
     return copy(h2d_, dst, alias_(alias_ctx_, (char*)src), bytes, false, gate, out);
+  }
+
+  int writeback(void* dst, const void* src, uint64_t bytes, int gate, CopyRef* out) override {
+    hipError_t e;
+    Gate& g = gates_[gate];
+    if (g.consumed_recorded && (e = hipStreamWaitEvent(d2h_, g.consumed, 0)) != hipSuccess) return (int)e;
+    return copy(d2h_, alias_(alias_ctx_, (char*)dst), src, bytes, true, gate, out);
   }
 
   int wait(int gate, hipStream_t compute) override {

@@ -55,6 +55,10 @@ class Link {
   // Copy pinned host `src` to device `dst` once `after` (the D2H that filled src) finished and
   // the gate's last consumer (see consumed()) finished. Completion is published through `gate`.
   virtual int h2d(void* dst, const void* src, uint64_t bytes, const CopyRef& after, int gate, CopyRef* out) = 0;
+  // Copy the slot behind `gate` (device `src`) to pinned host `dst` once the gate's last
+  // consumer (see consumed()) finished. The gate's next h2d (given this copy as `after`) and
+  // wait() are ordered behind it.
+  virtual int writeback(void* dst, const void* src, uint64_t bytes, int gate, CopyRef* out) = 0;
   // Order work enqueued on `compute` after this call behind the gate's last copy (no-op if
   // none): SdmaLink blocks the host until the copy finished; StreamLink makes the stream wait.
   virtual int wait(int gate, hipStream_t compute) = 0;

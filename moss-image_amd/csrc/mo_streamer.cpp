@@ -9,7 +9,11 @@
 //                     slot's last release has completed (the slot's previous contents are no
 //                     longer read by the GPU);
 //   fill -> acquire : the host waits for the fill's completion before it enqueues the
-//                     kernels that read the slot.
+//                     kernels that read the slot;
+//   release -> write-back -> fill : a slot whose contents were updated on the device (the
+//                     trainable ring, training/trainable_offload.py:245-260) is copied back to its
+//                     master after the release point, and the slot's next fill waits for that
+//                     copy.
 // No GPU queue waits on host memory, and every wait is bounded.
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
@@ -34,8 +38,8 @@ struct mo_streamer {
   int device = 0;
   std::unique_ptr<mo::Link> link;
   std::vector<int> gates;        // one per slot
-  std::vector<mo::CopyRef> last; // last fill per slot
-  uint64_t fills = 0, bytes = 0;
+  std::vector<mo::CopyRef> pending_writeback;  // per slot: the next fill waits for it
+  uint64_t fills = 0, bytes = 0, writebacks = 0, writeback_bytes = 0;
 };
 
 namespace {
@@ -115,7 +119,7 @@ int mo_streamer_create(int device, uint32_t slots, uint32_t h2d_engine, mo_strea
       if (int rc = s->link->new_gate(&g)) return mo::set_hip_error(rc, "slot gate");
       s->gates.push_back(g);
     }
-    s->last.resize(slots);
+    s->pending_writeback.resize(slots);
     *out = s.release();
     return 0;
   } catch (const std::exception& ex) {
@@ -142,11 +146,26 @@ int mo_streamer_fill(mo_streamer* s, uint32_t slot, uint64_t dst, uint64_t src, 
     if (!dst || !src) return mo::set_error(MO_E_INVALID, "null fill address");
     if (bytes == 0) return 0;
     mo::CopyRef copy;
-    if (int rc = s->link->h2d((void*)dst, (const void*)src, bytes, mo::CopyRef(), s->gates[slot], &copy))
+    if (int rc = s->link->h2d((void*)dst, (const void*)src, bytes, s->pending_writeback[slot], s->gates[slot], &copy))
       return mo::set_hip_error(rc, "slot fill (SDMA H2D)");
-    s->last[slot] = std::move(copy);
+    s->pending_writeback[slot].reset();
     s->fills++;
     s->bytes += bytes;
+    return 0;
+  });
+}
+
+int mo_streamer_writeback(mo_streamer* s, uint32_t slot, uint64_t dst, uint64_t src, uint64_t bytes) {
+  MO_STREAMER_CALL(s, {
+    if (int rc = check_slot(s, slot)) return rc;
+    if (!dst || !src) return mo::set_error(MO_E_INVALID, "null write-back address");
+    if (bytes == 0) return 0;
+    mo::CopyRef copy;
+    if (int rc = s->link->writeback((void*)dst, (const void*)src, bytes, s->gates[slot], &copy))
+      return mo::set_hip_error(rc, "slot write-back (SDMA D2H)");
+    s->pending_writeback[slot] = std::move(copy);
+    s->writebacks++;
+    s->writeback_bytes += bytes;
     return 0;
   });
 }
@@ -185,6 +204,10 @@ int mo_streamer_get_stats(mo_streamer* s, mo_streamer_stats* out) {
     out->bytes = s->bytes;
     out->timed_bytes = ls.h2d_done_bytes;
     out->busy_ms = ls.h2d_ms;
+    out->writebacks = s->writebacks;
+    out->writeback_bytes = s->writeback_bytes;
+    out->timed_writeback_bytes = ls.d2h_done_bytes;
+    out->writeback_busy_ms = ls.d2h_ms;
     out->host_blocks = ls.host_blocks;
     out->host_block_ms = ls.host_block_ms;
     out->copy_failures = ls.failures;
@@ -195,7 +218,7 @@ int mo_streamer_get_stats(mo_streamer* s, mo_streamer_stats* out) {
 int mo_streamer_reset_stats(mo_streamer* s) {
   MO_STREAMER_CALL(s, {
     s->link->reset_stats();
-    s->fills = s->bytes = 0;
+    s->fills = s->bytes = s->writebacks = s->writeback_bytes = 0;
     return 0;
   });
 }

@@ -116,6 +116,10 @@ class MoStreamerStats(ctypes.Structure):
         ("host_blocks", ctypes.c_uint64),
         ("host_block_ms", ctypes.c_double),
         ("copy_failures", ctypes.c_uint64),
+        ("writebacks", ctypes.c_uint64),
+        ("writeback_bytes", ctypes.c_uint64),
+        ("timed_writeback_bytes", ctypes.c_uint64),
+        ("writeback_busy_ms", ctypes.c_double),
     ]
 
     def as_dict(self) -> dict:
@@ -162,6 +166,7 @@ SIGNATURES: dict[str, tuple] = {
     "mo_streamer_create": (ctypes.c_int, [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, _P(ctypes.c_void_p)]),
     "mo_streamer_destroy": (ctypes.c_int, [ctypes.c_void_p]),
     "mo_streamer_fill": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64, _u64, _u64]),
+    "mo_streamer_writeback": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64, _u64, _u64]),
     "mo_streamer_acquire": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64]),
     "mo_streamer_release": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64]),
     "mo_streamer_synchronize": (ctypes.c_int, [ctypes.c_void_p]),

@@ -9,8 +9,9 @@ rest:
 - ``"async"``: the frozen parameters and buffers of each swapped block are packed into one
   pinned host *master*; LoRA adapters move to the device. An :class:`AsyncBlockStreamer` copies
   masters into two reusable device staging slots ahead of use (reference :93-361).
-- ``"async_full"`` (``TrainableBlockStreamer``, reference trainable_offload.py) is validated like
-  the reference but not provided by this build.
+- ``"async_full"``: every parameter and buffer of the swapped blocks streams through a
+  two-slot ring with write-back of updated blocks (``moss_offload.trainable_offload``, reference
+  trainable_offload.py:89-477).
 
 What is MI355X-specific: the masters of all swapped blocks live in one pinned host arena of
 exactly the packed size (``mo_pinned_alloc``; the reference pins each block through torch's
@@ -442,6 +443,19 @@ def _validate(model: nn.Module, device: torch.device, blocks_to_swap: int, mode:
         dtypes = {p.dtype for p in trainable}
         if len(dtypes) != 1 or not dtypes <= {torch.float32, torch.bfloat16}:
             raise ValueError("async_full requires homogeneous FP32 or BF16 trainable model parameters.")
+        seen: dict[int, str] = {}
+        for index, layer in enumerate(model.layers):
+            if index < boundary:
+                continue
+            for name, parameter in layer.named_parameters():
+                qualified = f"layers.{index}.{name}"
+                if not parameter.is_floating_point():
+                    raise TypeError(f"async_full cannot stream non-floating parameter {qualified}.")
+                first = seen.setdefault(id(parameter), qualified)
+                if first != qualified:
+                    raise ValueError(
+                        f"async_full does not support parameters shared across streamed blocks ({first} and {qualified})."
+                    )
         return
     invalid = [
         f"layers.{index}.{name}"
@@ -463,8 +477,6 @@ def place_model(model: nn.Module, device: torch.device, blocks_to_swap: int, *, 
 
     device = torch.device(device)
     _validate(model, device, blocks_to_swap, block_swap_mode)
-    if block_swap_mode == "async_full" and blocks_to_swap:
-        raise NotImplementedError("block_swap_mode='async_full' (trainable block streaming) is not provided by this build.")
     previous = getattr(model, "block_swap_manager", None)
     if previous is not None:
         previous.close()
@@ -475,9 +487,18 @@ def place_model(model: nn.Module, device: torch.device, blocks_to_swap: int, *, 
         if name != "layers":
             child.to(device)
     boundary = len(model.layers) - blocks_to_swap
-    if block_swap_mode in ("sync", "async_full"):
+    if block_swap_mode == "sync":
         for index, layer in enumerate(model.layers):
             layer.to("cpu" if index >= boundary else device)
+        return
+    if block_swap_mode == "async_full":
+        from .trainable_offload import TrainableBlockStreamer
+
+        for layer in model.layers[:boundary]:
+            layer.to(device)
+        if blocks_to_swap:
+            model.block_swap_manager = TrainableBlockStreamer(model.layers, device, boundary, master_dtype=None,
+                                                              h2d_engine=h2d_engine)
         return
     swapped = {}
     for index, layer in enumerate(model.layers):

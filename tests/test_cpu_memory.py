@@ -99,3 +99,26 @@ def test_offloaded_block_copies_parameters_to_the_input_device_each_call() -> No
     assert layer.weight.grad is not None and x.grad is not None
     with torch.no_grad():
         assert torch.equal(offloaded_block(layer, x), layer(x))
+
+
+def test_trainable_streamer_rejects_non_cuda_without_initializing_cuda() -> None:
+    from moss_offload.trainable_offload import TrainableBlockStreamer
+
+    model = _tiny()
+    with pytest.raises(ValueError, match="requires a CUDA device"):
+        TrainableBlockStreamer(model.layers, "cpu")
+    with pytest.raises(ValueError, match="requires a CUDA device"):
+        place_model(model, torch.device("cpu"), 2, block_swap_mode="async_full")
+    assert all(p.device.type == "cpu" for p in model.parameters())
+
+
+def test_async_full_rejects_shared_and_integer_parameters_before_mutating() -> None:
+    model = _tiny()
+    model.layers[3].proj["q"].weight = model.layers[2].proj["q"].weight
+    with pytest.raises(ValueError, match="shared across streamed blocks"):
+        place_model(model, torch.device("cuda"), 2, block_swap_mode="async_full")
+    model = _tiny()
+    model.layers[3].register_parameter("steps", torch.nn.Parameter(torch.zeros(2, dtype=torch.int64), requires_grad=False))
+    with pytest.raises(TypeError, match="non-floating parameter"):
+        place_model(model, torch.device("cuda"), 2, block_swap_mode="async_full")
+    assert not hasattr(model, "block_swap_manager")
