@@ -172,6 +172,10 @@ SIGNATURES: dict[str, tuple] = {
     "mo_streamer_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
     "mo_streamer_get_stats": (ctypes.c_int, [ctypes.c_void_p, _P(MoStreamerStats)]),
     "mo_streamer_reset_stats": (ctypes.c_int, [ctypes.c_void_p]),
+    "mo_int8_linear_forward": (ctypes.c_int, [_u64, _u64, _u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32,
+                                              ctypes.c_uint32, _u64]),
+    "mo_int8_linear_backward": (ctypes.c_int, [_u64, _u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32,
+                                               ctypes.c_uint32, _u64]),
 }
 
 _lock = threading.Lock()

@@ -441,31 +441,54 @@ class LoRALinear(nn.Module):
 
 
 class _FrozenInt8Function(torch.autograd.Function):
-    """Weight-only int8 linear; saves the int8 weight and fp32 scales (quantization.py:27-65)."""
+    """Weight-only int8 linear; saves the int8 weight and fp32 scales (quantization.py:27-65).
+
+    ``backend``: ``hip`` runs the gfx950 MFMA kernels of ``moss_offload.quant_kernels`` (the
+    reference's ``triton`` backend), ``eager`` decodes the weight and calls ``F.linear``,
+    ``auto`` picks ``hip`` whenever the call is supported.
+    """
 
     @staticmethod
-    def forward(ctx, tokens, weight, scale, dtype):
+    def forward(ctx, tokens, weight, scale, dtype, backend):
+        from . import quant_kernels
+
         ctx.save_for_backward(weight, scale)
         ctx.input_dtype, ctx.weight_dtype = tokens.dtype, dtype
-        result = F.linear(tokens.to(dtype), weight.to(dtype) * scale.to(dtype)[:, None])
+        ctx.input_shape = tokens.shape
+        prepared = tokens.to(dtype)
+        selected = quant_kernels.resolve_backend(backend, prepared, weight, scale, dtype)
+        if selected == "hip" and torch.is_autocast_enabled(tokens.device.type):
+            if torch.get_autocast_dtype(tokens.device.type) != dtype:
+                selected = "eager" if backend == "auto" else selected
+        ctx.backend = selected
+        if selected == "hip":
+            result = quant_kernels.int8_linear_forward(prepared, weight, scale)
+        else:
+            result = F.linear(prepared, quant_kernels.decode(weight, scale, dtype))
         ctx.compute_dtype = result.dtype
         return result
 
     @staticmethod
     def backward(ctx, gradient):
+        from . import quant_kernels
+
         weight, scale = ctx.saved_tensors
+        if ctx.backend == "hip":
+            grad = quant_kernels.int8_linear_backward(gradient, weight, scale, ctx.input_shape).to(ctx.input_dtype)
+            return grad, None, None, None, None
         with torch.autocast(device_type=gradient.device.type, enabled=False):
-            dequantized = (weight.to(ctx.weight_dtype) * scale.to(ctx.weight_dtype)[:, None]).to(ctx.compute_dtype)
-            grad = gradient.to(ctx.compute_dtype).matmul(dequantized).to(ctx.input_dtype)
-        return grad, None, None, None
+            decoded = quant_kernels.decode(weight, scale, ctx.weight_dtype).to(ctx.compute_dtype)
+            grad = gradient.to(ctx.compute_dtype).matmul(decoded).to(ctx.input_dtype)
+        return grad, None, None, None, None
 
 
 class FrozenInt8Linear(nn.Module):
     """Per-output-channel symmetric int8 weights, fp32 scales, no bias (quantization.py:68-131)."""
 
-    def __init__(self, weight_int8: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> None:
+    def __init__(self, weight_int8: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype, backend: str = "auto") -> None:
         super().__init__()
         self.out_features, self.in_features = weight_int8.shape
+        self.quantized_backend = backend
         self.register_buffer("weight_int8", weight_int8)
         self.register_buffer("weight_scale", scale.float())
         self.register_buffer("_dtype_anchor", torch.empty(0, device=weight_int8.device, dtype=dtype), persistent=False)
@@ -474,8 +497,31 @@ class FrozenInt8Linear(nn.Module):
     def compute_dtype(self):
         return self._dtype_anchor.dtype
 
+    def _apply(self, fn, recurse=True):
+        # scales stay fp32 when the model is cast (quantization.py:113-118)
+        scale = self.weight_scale
+        result = super()._apply(fn, recurse=recurse)
+        self.weight_scale = scale.to(device=self.weight_int8.device, dtype=torch.float32)
+        return result
+
     def forward(self, tokens):
-        return _FrozenInt8Function.apply(tokens, self.weight_int8, self.weight_scale, self.compute_dtype)
+        return _FrozenInt8Function.apply(tokens, self.weight_int8, self.weight_scale, self.compute_dtype,
+                                         self.quantized_backend)
+
+
+def configure_quantized_backend(model: nn.Module, backend: str) -> list[str]:
+    """Set the backend of every frozen int8 module; return their names (quantization.py:134-144)."""
+
+    from .quant_kernels import BACKENDS
+
+    if backend not in BACKENDS:
+        raise ValueError("quantized backend must be auto, eager or hip.")
+    names = []
+    for name, module in model.named_modules():
+        if isinstance(module, FrozenInt8Linear):
+            module.quantized_backend = backend
+            names.append(name)
+    return names
 
 
 def joint_linear_names(model: MOSSImageTransformer) -> list[str]:

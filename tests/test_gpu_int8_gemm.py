@@ -1,0 +1,128 @@
+"""Weight-only int8 GEMMs on MFMA (mo_int8_linear_forward / backward) on the GPU.
+
+- Decode parity: with one-hot inputs each output element is a single product, so the kernels
+  must reproduce the decoded weight bit for bit: bf16(q * bf16(scale)), the decode of the
+  reference's Triton kernels (training/quant_kernels.py:126-131) and of its eager path
+  (quantization.py:23-24).
+- Products: random shapes including ragged rows, columns and reduction lengths (partial
+  tiles and reduction steps), against an fp64 reference of the same decoded weight, within
+  the bound of fp32 accumulation plus the final bf16 rounding.
+- Module level: the harness's int8 LoRA model trains the same with the HIP backend and with
+  the eager backend (the reference's own parity criterion between its backends).
+"""
+
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+from moss_offload import dit, quant_kernels
+
+from gpu_util import requires_gpu
+
+pytestmark = requires_gpu
+
+DEV = torch.device("cuda", 0)
+
+
+def _operands(rows, in_f, out_f, seed, bias=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(rows, in_f, generator=g).to(torch.bfloat16).to(DEV)
+    w = torch.randint(-127, 128, (out_f, in_f), dtype=torch.int8, generator=g).to(DEV)
+    scale = torch.empty(out_f).uniform_(0.001, 0.02, generator=g).to(DEV)
+    b = torch.randn(out_f, generator=g).to(torch.bfloat16).to(DEV) if bias else None
+    return x, w, scale, b
+
+
+def _within_accumulation_bound(actual, exact, magnitude, terms):
+    err = (actual.double() - exact).abs()
+    bound = 2.0**-8 * exact.abs() + terms * 2.0**-23 * magnitude + 1e-30
+    bad = err > bound
+    assert not bad.any(), f"{int(bad.sum())} elements outside the bound; worst excess {(err - bound).max().item()}"
+
+
+@pytest.mark.parametrize("in_f,out_f", [(16, 16), (64, 128), (80, 48), (256, 384)])
+def test_forward_reproduces_the_decoded_weight_bitwise(in_f, out_f) -> None:
+    _, w, scale, _ = _operands(1, in_f, out_f, seed=in_f + out_f)
+    eye = torch.eye(in_f, dtype=torch.bfloat16, device=DEV)
+    y = quant_kernels.int8_linear_forward(eye, w, scale)
+    decoded = quant_kernels.decode(w, scale, torch.bfloat16)
+    assert torch.equal(y.view(torch.int16), decoded.t().contiguous().view(torch.int16))
+
+
+@pytest.mark.parametrize("in_f,out_f", [(16, 16), (64, 128), (80, 48), (256, 384)])
+def test_backward_reproduces_the_decoded_weight_bitwise(in_f, out_f) -> None:
+    _, w, scale, _ = _operands(1, in_f, out_f, seed=in_f * 3 + out_f)
+    eye = torch.eye(out_f, dtype=torch.bfloat16, device=DEV)
+    dx = quant_kernels.int8_linear_backward(eye, w, scale, torch.Size((out_f, in_f)))
+    decoded = quant_kernels.decode(w, scale, torch.bfloat16)
+    assert torch.equal(dx.view(torch.int16), decoded.view(torch.int16))
+
+
+SHAPES = [(1, 16, 16), (100, 80, 48), (128, 64, 128), (257, 256, 384), (300, 1040, 208), (1024, 3072, 3072)]
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", SHAPES)
+@pytest.mark.parametrize("bias", [False, True])
+def test_forward_matches_fp64_reference(rows, in_f, out_f, bias) -> None:
+    x, w, scale, b = _operands(rows, in_f, out_f, seed=rows + 7 * in_f + out_f, bias=bias)
+    y = quant_kernels.int8_linear_forward(x, w, scale, b)
+    assert y.shape == (rows, out_f) and y.dtype == torch.bfloat16
+    decoded = quant_kernels.decode(w, scale, torch.bfloat16).double()
+    exact = x.double() @ decoded.t()
+    if b is not None:
+        exact = exact + b.double()
+    magnitude = x.double().abs() @ decoded.abs().t()
+    _within_accumulation_bound(y, exact, magnitude, in_f)
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", SHAPES)
+def test_backward_matches_fp64_reference(rows, in_f, out_f) -> None:
+    _, w, scale, _ = _operands(rows, in_f, out_f, seed=rows + 11 * in_f + out_f)
+    g = torch.Generator().manual_seed(rows)
+    dy = torch.randn(rows, out_f, generator=g).to(torch.bfloat16).to(DEV)
+    dx = quant_kernels.int8_linear_backward(dy, w, scale, torch.Size((rows, in_f)))
+    decoded = quant_kernels.decode(w, scale, torch.bfloat16).double()
+    exact = dy.double() @ decoded
+    magnitude = dy.double().abs() @ decoded.abs()
+    _within_accumulation_bound(dx, exact, magnitude, out_f)
+
+
+def test_unsupported_calls_are_reported_and_auto_falls_back_to_eager() -> None:
+    x, w, scale, _ = _operands(4, 24, 16, seed=5)  # in_features not a multiple of 16
+    assert quant_kernels.unsupported_reason(x, w, scale, torch.bfloat16) is not None
+    assert quant_kernels.resolve_backend("auto", x, w, scale, torch.bfloat16) == "eager"
+    with pytest.raises(RuntimeError, match="HIP int8 backend is unavailable"):
+        quant_kernels.resolve_backend("hip", x, w, scale, torch.bfloat16)
+    x, w, scale, _ = _operands(4, 32, 16, seed=6)
+    assert quant_kernels.resolve_backend("auto", x, w, scale, torch.bfloat16) == "hip"
+    assert quant_kernels.resolve_backend("auto", x.float(), w, scale, torch.float32) == "eager"
+
+
+def test_int8_lora_model_hip_backend_matches_eager() -> None:
+    torch.manual_seed(121)
+    model = dit.MOSSImageTransformer(dim=64, ffn_dim=128, num_heads=4, num_layers=2, text_dim=16, freq_dim=8,
+                                     latent_channels=4, gradient_checkpointing=True)
+    model = model.to(DEV).to(torch.bfloat16)
+    dit.init_weights(model)
+    dit.quantize_joint_linears(model, torch.Generator(device=DEV).manual_seed(5))
+    dit.inject_lora(model, rank=4, alpha=4.0)
+    results = {}
+    g = torch.Generator().manual_seed(3)
+    latent = torch.randn(1, 4, 6, 8, generator=g).to(DEV)
+    context = torch.randn(1, 5, 16, generator=g).to(DEV)
+    for backend in ("eager", "hip"):
+        m = copy.deepcopy(model).train()
+        assert dit.configure_quantized_backend(m, backend)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = m(latent, torch.tensor([400.0], device=DEV), context)
+            loss = out.float().square().mean()
+        loss.backward()
+        results[backend] = (out.detach().float(), {n: p.grad.float() for n, p in m.named_parameters() if p.grad is not None})
+    (eo, eg), (ho, hg) = results["eager"], results["hip"]
+    torch.testing.assert_close(ho, eo, rtol=2e-2, atol=2e-2)
+    assert eg.keys() == hg.keys() and eg
+    for name in eg:
+        torch.testing.assert_close(hg[name], eg[name], rtol=5e-2, atol=1e-3, msg=name)
