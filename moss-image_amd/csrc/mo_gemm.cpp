@@ -1,5 +1,11 @@
 // Host side of the int8 weight-only GEMMs (csrc/mo_gemm.hip): argument checks, module loading
-// from the embedded gfx950 code object, launches. C ABI: mo_int8_linear_forward/backward.
+// from the embedded gfx950 code object, the launch plan. C ABI: mo_int8_linear_forward/backward.
+//
+// Launch plan: the large tile (256 x 256) carries the work; when its grid would leave the GPU's
+// last round of workgroups less than half full, the rows of that partial round go to a second
+// launch with the small tile (128 x 128, two workgroups a CU), and a grid smaller than one
+// round of large tiles uses the small tile throughout. Every output element is computed by one
+// workgroup with the same reduction order in either tile, so the plan does not change results.
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
 
@@ -18,18 +24,24 @@ int set_hip_error(int e, const char* what);
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kTile = 128;
+constexpr uint32_t kLarge = 256, kSmall = 128;  // output tile edges (mo_gemm.hip Cfg)
+
+struct Kernel {
+  hipFunction_t fn = nullptr;
+  uint32_t threads = 0, tile = 0;
+};
 
 struct GemmModule {
   hipModule_t module = nullptr;
-  hipFunction_t fwd = nullptr, bwd = nullptr;
+  int cus = 0;
+  // [backward][small][tail]
+  Kernel k[2][2][2];
 };
 
 std::mutex g_mu;
 std::map<int, GemmModule> g_modules;
 
-int gemm_kernels(GemmModule* out) {
+int gemm_module(GemmModule* out) {
   int device = 0;
   hipError_t e = hipGetDevice(&device);
   if (e != hipSuccess) return mo::set_hip_error((int)e, "hipGetDevice");
@@ -39,9 +51,19 @@ int gemm_kernels(GemmModule* out) {
     GemmModule m;
     if ((e = hipModuleLoadData(&m.module, mo_gemm_code)) != hipSuccess)
       return mo::set_hip_error((int)e, "hipModuleLoadData (int8 GEMM code object)");
-    if ((e = hipModuleGetFunction(&m.fwd, m.module, "mo_int8_linear_fwd_kernel")) != hipSuccess ||
-        (e = hipModuleGetFunction(&m.bwd, m.module, "mo_int8_linear_bwd_kernel")) != hipSuccess)
-      return mo::set_hip_error((int)e, "hipModuleGetFunction (int8 GEMM)");
+    if ((e = hipDeviceGetAttribute(&m.cus, hipDeviceAttributeMultiprocessorCount, device)) != hipSuccess)
+      return mo::set_hip_error((int)e, "hipDeviceGetAttribute (CU count)");
+    for (int bwd = 0; bwd < 2; ++bwd)
+      for (int small = 0; small < 2; ++small)
+        for (int tail = 0; tail < 2; ++tail) {
+          const std::string name = std::string("mo_int8_linear_") + (bwd ? "bwd" : "fwd") + (small ? "_small" : "_large") +
+                                   (tail ? "_tail" : "");
+          Kernel& k = m.k[bwd][small][tail];
+          if ((e = hipModuleGetFunction(&k.fn, m.module, name.c_str())) != hipSuccess)
+            return mo::set_hip_error((int)e, "hipModuleGetFunction (int8 GEMM)");
+          k.tile = small ? kSmall : kLarge;
+          k.threads = small ? 256 : (bwd ? 256 : 512);  // waves of each configuration x 64
+        }
     it = g_modules.emplace(device, m).first;
   }
   *out = it->second;
@@ -56,17 +78,50 @@ int check(uint64_t a, uint64_t w, uint64_t scale, uint64_t c, uint32_t rows, uin
                                            std::to_string(in_f) + ", " + std::to_string(out_f) + ")");
   if ((a | w | c) % 16) return mo::set_error(MO_E_INVALID, "matrix pointers must be 16-byte aligned");
   if (scale % 4) return mo::set_error(MO_E_INVALID, "scale pointer must be 4-byte aligned");
-  if ((uint64_t)rows * (out_f > in_f ? out_f : in_f) >= (1ull << 40))
-    return mo::set_error(MO_E_INVALID, "matrix too large");
+  // 32-bit buffer offsets: one tile's rows of either activation, and the whole weight
+  if (in_f > (1u << 20) || out_f > (1u << 20) || (uint64_t)in_f * out_f >= (1ull << 31))
+    return mo::set_error(MO_E_INVALID, "weight too large (in_features, out_features <= 2^20 and in * out < 2^31)");
+  if ((uint64_t)rows * (out_f > in_f ? out_f : in_f) >= (1ull << 40)) return mo::set_error(MO_E_INVALID, "matrix too large");
   return 0;
 }
 
-int launch(hipFunction_t fn, void** params, uint32_t rows, uint32_t cols, uint64_t stream) {
-  const uint64_t tiles_m = (rows + kTile - 1) / kTile, tiles_c = (cols + kTile - 1) / kTile;
+struct Part {
+  bool small;
+  uint32_t row0, rows;
+};
+
+// Split [0, rows) between the large and the small tile (see the file comment).
+int plan(uint32_t rows, uint32_t cols, int cus, Part parts[2]) {
+  const uint64_t tm = (rows + kLarge - 1) / kLarge, tc = (cols + kLarge - 1) / kLarge, total = tm * tc;
+  const uint64_t rounds = total / (uint64_t)cus, rem = total % (uint64_t)cus;
+  if (rounds == 0) {
+    parts[0] = {true, 0, rows};
+    return 1;
+  }
+  if (rem == 0 || 2 * rem >= (uint64_t)cus) {
+    parts[0] = {false, 0, rows};
+    return 1;
+  }
+  const uint64_t main_rows = (rounds * (uint64_t)cus / tc) * kLarge;
+  if (main_rows == 0) {
+    parts[0] = {true, 0, rows};
+    return 1;
+  }
+  if (main_rows >= rows) {
+    parts[0] = {false, 0, rows};
+    return 1;
+  }
+  parts[0] = {false, 0, (uint32_t)main_rows};
+  parts[1] = {true, (uint32_t)main_rows, rows - (uint32_t)main_rows};
+  return 2;
+}
+
+int launch(const Kernel& k, void** params, uint32_t rows, uint32_t cols, uint64_t stream) {
+  const uint64_t tiles_m = (rows + k.tile - 1) / k.tile, tiles_c = (cols + k.tile - 1) / k.tile;
   const uint64_t grid = tiles_m * tiles_c;
   if (grid >= (1ull << 31)) return mo::set_error(MO_E_INVALID, "grid too large");
-  const hipError_t e = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, kThreads, 1, 1, 0, (hipStream_t)stream, params,
-                                             nullptr);
+  const hipError_t e =
+      hipModuleLaunchKernel(k.fn, (uint32_t)grid, 1, 1, k.threads, 1, 1, 0, (hipStream_t)stream, params, nullptr);
   if (e != hipSuccess) return mo::set_hip_error((int)e, "int8 GEMM launch");
   return 0;
 }
@@ -80,31 +135,45 @@ int mo_int8_linear_forward(uint64_t x, uint64_t w, uint64_t scale, uint64_t bias
   if (int rc = check(x, w, scale, y, rows, in_features, out_features)) return rc;
   if (bias % 2) return mo::set_error(MO_E_INVALID, "bias pointer must be 2-byte aligned");
   GemmModule m;
-  if (int rc = gemm_kernels(&m)) return rc;
-  const void* A = (const void*)x;
-  const void* B = (const void*)w;
-  const void* S = (const void*)scale;
-  const void* Bi = (const void*)bias;
-  void* C = (void*)y;
-  int M = (int)rows, NC = (int)out_features, R = (int)in_features;
-  int tiles_m = (int)((rows + kTile - 1) / kTile);
-  void* params[] = {&A, &B, &S, &Bi, &C, &M, &NC, &R, &tiles_m};
-  return launch(m.fwd, params, rows, out_features, stream);
+  if (int rc = gemm_module(&m)) return rc;
+  Part parts[2];
+  const int n = plan(rows, out_features, m.cus, parts);
+  const int tail = in_features % 64 != 0;
+  for (int p = 0; p < n; ++p) {
+    const Kernel& k = m.k[0][parts[p].small][tail];
+    const void* A = (const void*)(x + (uint64_t)parts[p].row0 * in_features * 2);
+    const void* B = (const void*)w;
+    const void* S = (const void*)scale;
+    const void* Bi = (const void*)bias;
+    void* C = (void*)(y + (uint64_t)parts[p].row0 * out_features * 2);
+    int M = (int)parts[p].rows, NC = (int)out_features, R = (int)in_features;
+    int tiles_m = (int)((parts[p].rows + k.tile - 1) / k.tile);
+    void* params[] = {&A, &B, &S, &Bi, &C, &M, &NC, &R, &tiles_m};
+    if (int rc = launch(k, params, parts[p].rows, out_features, stream)) return rc;
+  }
+  return 0;
 }
 
 int mo_int8_linear_backward(uint64_t dy, uint64_t w, uint64_t scale, uint64_t dx, uint32_t rows, uint32_t in_features,
                             uint32_t out_features, uint64_t stream) {
   if (int rc = check(dy, w, scale, dx, rows, in_features, out_features)) return rc;
   GemmModule m;
-  if (int rc = gemm_kernels(&m)) return rc;
-  const void* A = (const void*)dy;
-  const void* B = (const void*)w;
-  const void* S = (const void*)scale;
-  void* C = (void*)dx;
-  int M = (int)rows, NC = (int)in_features, R = (int)out_features;
-  int tiles_m = (int)((rows + kTile - 1) / kTile);
-  void* params[] = {&A, &B, &S, &C, &M, &NC, &R, &tiles_m};
-  return launch(m.bwd, params, rows, in_features, stream);
+  if (int rc = gemm_module(&m)) return rc;
+  Part parts[2];
+  const int n = plan(rows, in_features, m.cus, parts);
+  const int tail = out_features % 64 != 0;
+  for (int p = 0; p < n; ++p) {
+    const Kernel& k = m.k[1][parts[p].small][tail];
+    const void* A = (const void*)(dy + (uint64_t)parts[p].row0 * out_features * 2);
+    const void* B = (const void*)w;
+    const void* S = (const void*)scale;
+    void* C = (void*)(dx + (uint64_t)parts[p].row0 * in_features * 2);
+    int M = (int)parts[p].rows, NC = (int)in_features, R = (int)out_features;
+    int tiles_m = (int)((parts[p].rows + k.tile - 1) / k.tile);
+    void* params[] = {&A, &B, &S, &C, &M, &NC, &R, &tiles_m};
+    if (int rc = launch(k, params, parts[p].rows, in_features, stream)) return rc;
+  }
+  return 0;
 }
 
 }  // extern "C"

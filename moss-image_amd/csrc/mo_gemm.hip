@@ -11,169 +11,399 @@
 //                    (kTransB: the reduction runs along Bq's rows; the tile is transposed into
 //                     LDS so that both MFMA operands are read reduction-contiguous)
 //
-// Tiling: a 256-lane workgroup (4 wave64, 2 x 2) owns a 128 x 128 output tile; each wave owns
-// 64 x 64 = 2 x 2 MFMA 32x32 tiles. The reduction advances 64 per step; the next step's A and
-// Bq tiles are loaded into registers while the current step's MFMAs run from LDS.
+// Tiling (Cfg): a workgroup owns a kBM x kBC output tile, split over a grid of waves; each wave
+// owns (kWM x 32) x (kWC x 32) as kWM x kWC MFMA 32x32 tiles. The reduction advances 64 per
+// step through a double-buffered LDS (two A tiles kBM x 64 and two decoded weight tiles
+// kBC x 64, bf16). Within a step (four 16-deep MFMA slices):
+//   - the A tile one step ahead is copied global -> LDS by the DMA path of buffer loads
+//     (buffer_load ... lds, 16 bytes a lane), with no register round trip;
+//   - the weight tile one step ahead, loaded into registers a step earlier, is decoded into the
+//     other LDS buffer during slices 0-2, while the weight tile two steps ahead is loaded into
+//     the other register set (two sets, alternating by step parity);
+//   - after slice 2 every wave has finished its reads of this step's buffers and its writes of
+//     the next step's, so the barrier sits there and slice 3 overlaps the next step's first
+//     fragment reads.
+// Rows of 64 bf16 are stored as eight 16-byte chunks at position chunk ^ ((row ^ row / 8) % 8),
+// which keeps the fragment reads (32 rows, one chunk), the decoded writes (strided rows) and the
+// DMA rows free of bank conflicts. The input-gradient weight tile is read 8 reduction rows x
+// kTn columns per lane; the decode packs pairs of reduction rows into each bf16x2, which
+// transposes the tile on the way into LDS.
+// Per-lane global offsets are fixed for the whole reduction; the reduction position is the
+// scalar offset of the buffer instructions. Tiles are numbered in groups of kGroupM row tiles
+// and then XCD-aware, so that the workgroups one XCD receives (blockIdx % 8) form a contiguous
+// run of a few row and column tiles in that XCD's L2.
 // MFMA 32x32x16 bf16 lane layout (checked on the device): A lane l holds row l%32,
 // k = 8*(l/32)+j; B lane l holds column l%32, k = 8*(l/32)+j; D register r of lane l holds
 // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace mo_gemm {
 
-constexpr int kThreads = 256;
-constexpr int kBM = 128;  // output rows per workgroup
-constexpr int kBC = 128;  // output columns per workgroup
-constexpr int kBR = 64;   // reduction per step
-constexpr int kLds = kBR + 8;  // LDS row pitch in bf16 (padding spreads banks)
+constexpr int kBR = 64;     // reduction per step (one LDS row: eight 16-byte chunks)
+constexpr int kGroupM = 8;  // row tiles per group of the tile numbering
+constexpr int kXcds = 8;    // MI355X: workgroup i is dispatched to XCD i % 8
+
+template <int BM, int BC, int WAVES_M, int WAVES_C>
+struct Cfg {
+  static constexpr int kBM = BM, kBC = BC, kWavesM = WAVES_M;
+  static constexpr int kWaves = WAVES_M * WAVES_C, kThreads = 64 * kWaves;
+  static constexpr int kRowsW = BM / WAVES_M, kColsW = BC / WAVES_C;
+  static constexpr int kWM = kRowsW / 32, kWC = kColsW / 32;  // MFMA tiles per wave
+  static constexpr int kDma = BM / 8 / kWaves;                 // 1 KiB A blocks per wave and step
+  static constexpr int kF = BC * 4 / kThreads;                 // forward: 16-byte weight pieces a lane
+  static constexpr int kFcols = kThreads / 4;                  // forward: columns per piece index
+  static constexpr int kTn = 8 * BC / kThreads;                // transposed: weight columns a lane
+  static_assert(kDma >= 1 && BM % (8 * kWaves) == 0, "A DMA blocks must divide over the waves");
+  static_assert(kF >= 1 && kFcols % 64 == 0, "forward weight pieces");
+  static_assert(kTn == 4 || kTn == 8, "transposed weight columns per lane");
+  static_assert(kWM >= 1 && kWC >= 1 && kWM <= 4 && kWC <= 4, "wave tile");
+};
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-#define MO_GLOBAL __attribute__((address_space(1)))
 #define MO_LDS __attribute__((address_space(3)))
 
-__device__ __forceinline__ u32x4 gload16(const void* p) { return *(const MO_GLOBAL u32x4*)p; }
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw buffer descriptors (gfx9 word 3 = 0x00020000): a read at a vector offset at or beyond
+// num_records returns zero (and moves no data) and a write there is dropped. The scalar offset
+// is added to the address only, so every in-range vector offset must stay in range with it.
+constexpr uint32_t kOob = 0x80000000u;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+}
+
+// s_waitcnt immediate (gfx9): wait until at most n vector-memory operations are outstanding
+// (lgkm: 0 = also wait for all LDS operations, 15 = do not).
+constexpr int wait_vm(int n, int lgkm) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (lgkm << 8); }
 
 // bf16(q * bf16(s)): the product of an int8 and a bf16 is exact in fp32; one rounding to bf16.
-__device__ __forceinline__ __bf16 decode(int q, float s_bf16) { return (__bf16)((float)q * s_bf16); }
+__device__ __forceinline__ __bf16 decode(uint32_t word, int byte, float s_bf16) {
+  return (__bf16)((float)(int)(int8_t)(word >> (8 * byte)) * s_bf16);
+}
+__device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
 
-template <bool kTransB>
+// Element offset of (row, 16-byte chunk) in a swizzled LDS tile of rows of 64 bf16.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kBR + ((chunk ^ ((row ^ (row >> 3)) & 7)) << 3); }
+
+template <class G, bool kTransB, bool kFullR, int kVpm>
 __device__ __forceinline__ void gemm_body(const __bf16* __restrict__ A, const int8_t* __restrict__ Bq,
                                           const float* __restrict__ scale, const __bf16* __restrict__ bias,
                                           __bf16* __restrict__ C, int M, int NC, int R, int tiles_m) {
-  __shared__ __attribute__((aligned(16))) __bf16 As[kBM * kLds];
-  __shared__ __attribute__((aligned(16))) __bf16 Bs[kBC * kLds];
+  constexpr int kBM = G::kBM, kBC = G::kBC, kWM = G::kWM, kWC = G::kWC, kDma = G::kDma, kF = G::kF,
+                kFcols = G::kFcols, kTn = G::kTn;
+  // two buffers of each operand; distinct objects, so their accesses are known not to alias
+  __shared__ __attribute__((aligned(16))) __bf16 lds_a0[kBM * kBR];
+  __shared__ __attribute__((aligned(16))) __bf16 lds_a1[kBM * kBR];
+  __shared__ __attribute__((aligned(16))) __bf16 lds_b0[kBC * kBR];
+  __shared__ __attribute__((aligned(16))) __bf16 lds_b1[kBC * kBR];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave & 1, wc = wave >> 1;
-  const int tile_m = blockIdx.x % tiles_m;
-  const int tile_c = blockIdx.x / tiles_m;
-  const int m0 = tile_m * kBM, c0 = tile_c * kBC;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % G::kWavesM, wc = wave / G::kWavesM;
+  const int lr = lane & 31, h = lane >> 5;
 
-  // ---- global load assignment ----
-  // A: 128 rows x 64 bf16; lane pair per row, 4 chunks of 8 bf16 each.
-  const int a_row = tid >> 1, a_k = (tid & 1) * 32;
-  // Bq, forward: 128 columns x 64 int8, lane pair per column, 2 chunks of 16.
-  // Bq, transposed: 64 reduction rows x 128 columns, 4 lanes per row, 2 chunks of 16.
-  const int b_col = kTransB ? (tid & 3) * 32 : tid >> 1;
-  const int b_red = kTransB ? tid >> 2 : (tid & 1) * 32;
+  // ---- tile numbering: XCD-aware, then grouped ----
+  const int tiles = gridDim.x;
+  const int tiles_c = tiles / tiles_m;
+  int t;
+  {
+    const int b = blockIdx.x, xcd = b % kXcds, idx = b / kXcds;
+    const int per = tiles / kXcds, rem = tiles % kXcds;
+    t = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+  }
+  const int group_tiles = kGroupM * tiles_c;
+  const int first_m = (t / group_tiles) * kGroupM;
+  const int gm = min(tiles_m - first_m, kGroupM);
+  const int in_group = t % group_tiles;
+  const int m0 = (first_m + in_group % gm) * kBM;
+  const int c0 = (in_group / gm) * kBC;
 
-  u32x4 ra[4], rb[2];
-  float rs = 0.f;  // bf16-rounded scale for this lane's Bq values
+  // ---- buffer descriptors over this tile's rows of A and columns of Bq ----
+  // Rows past M and columns past NC fall outside the descriptors (vector offsets). With kFullR
+  // (R % 64 == 0) the reduction position is the scalar offset and stays inside a row; a step
+  // past R (the odd extra step) uses the empty descriptor. Without kFullR every load checks
+  // its own reduction index and carries it in the vector offset.
+  const rsrc_t ra_src = make_rsrc(A + (size_t)m0 * R, (uint32_t)(min(M - m0, kBM) * R * 2));
+  const rsrc_t rb_src = kTransB ? make_rsrc(Bq + c0, (uint32_t)((R - 1) * NC + (NC - c0)))
+                                : make_rsrc(Bq + (size_t)c0 * R, (uint32_t)(min(NC - c0, kBC) * R));
+  const rsrc_t rs_src = make_rsrc(scale, (uint32_t)((kTransB ? R : NC) * 4));
+  const rsrc_t none = make_rsrc(A, 0u);
 
-  auto load = [&](int r0) {
-    const int am = m0 + a_row;
+  // A by DMA: wave w fills 1 KiB blocks w * kDma + j (8 rows each); lane i writes LDS slot i % 8
+  // of row 8 * block + i / 8, which holds logical chunk slot ^ swizzle(row).
+  uint32_t a_off[kDma];
+  int a_k[kDma];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int k = r0 + a_k + 8 * i;
-      ra[i] = (am < M && k < R) ? gload16(A + (size_t)am * R + k) : u32x4{0, 0, 0, 0};
+  for (int j = 0; j < kDma; ++j) {
+    const int row = (wave * kDma + j) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
+    a_k[j] = 8 * c;
+    a_off[j] = (uint32_t)(row * R + 8 * c) * 2;
+  }
+  // Bq forward ([NC][R]): 4 lanes per column (16 int8 each), columns tid / 4 + kFcols i.
+  const int f_col = tid >> 2, f_part = tid & 3;
+  uint32_t f_off[kF];
+#pragma unroll
+  for (int i = 0; i < kF; ++i) f_off[i] = (uint32_t)((f_col + kFcols * i) * R + 16 * f_part);
+  // Bq transposed ([R][NC]): lane covers reduction rows 8 t_rg + 0..7 and columns
+  // kTn t_ng + 0..kTn-1 (one load of kTn bytes per row).
+  const int t_rg = tid / (kBC / kTn), t_ng = tid % (kBC / kTn);
+  const bool t_col_ok = c0 + kTn * t_ng < NC;  // NC % 16 == 0: all kTn columns in or out
+
+  // LDS element offsets, loop-invariant: fragment reads [i % 2][q] (i + 2 adds 64 rows, which
+  // keeps the swizzle) and decoded weight writes
+  int rd_a[2][4], rd_b[2][4];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      rd_a[p][q] = swz(wm * G::kRowsW + 32 * p + lr, 2 * q + h);
+      rd_b[p][q] = swz(wc * G::kColsW + 32 * p + lr, 2 * q + h);
     }
-    if (!kTransB) {
-      const int n = c0 + b_col;
+  int wr_b[8];  // forward: [0..1] = chunks 2 f_part + 0/1 of column f_col (i adds kFcols rows);
+                // transposed: [c] = column kTn t_ng + c, chunk t_rg
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int k = r0 + b_red + 16 * i;
-        rb[i] = (n < NC && k < R) ? gload16(Bq + (size_t)n * R + k) : u32x4{0, 0, 0, 0};
-      }
-      rs = n < NC ? (float)(__bf16)scale[n] : 0.f;
-    } else {
-      const int r = r0 + b_red;
+  for (int c = 0; c < 8; ++c)
+    wr_b[c] = kTransB ? swz(kTn * t_ng + (c % kTn), t_rg) : swz(f_col, 2 * f_part + (c & 1));
+
+  // weight tile registers, two sets (tile t in set t % 2)
+  u32x4 rf[2][kF];             // forward weight bytes
+  uint32_t rt[2][8][kTn / 4];  // transposed weight bytes
+  float st[2][8];              // transposed: bf16-rounded scales of the lane's reduction rows
+  float sf[kF];                // forward: bf16-rounded scales of the lane's columns
+  if (!kTransB) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int c = c0 + b_col + 16 * i;
-        rb[i] = (r < R && c < NC) ? gload16(Bq + (size_t)r * NC + c) : u32x4{0, 0, 0, 0};
-      }
-      rs = r < R ? (float)(__bf16)scale[r] : 0.f;
+    for (int i = 0; i < kF; ++i) {
+      const int n = c0 + f_col + kFcols * i;
+      sf[i] = bf16_round(__builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rs_src, n < NC ? n * 4 : (int)kOob, 0, 0)));
+    }
+  }
+
+  // A tile at reduction r0 straight into LDS.
+  auto dma_a = [&](MO_LDS __bf16* As, int r0) {
+    const rsrc_t src = r0 < R ? ra_src : none;
+#pragma unroll
+    for (int j = 0; j < kDma; ++j) {
+      MO_LDS void* dst = (MO_LDS void*)(As + (wave * kDma + j) * 512);
+      if (kFullR)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(src, dst, 16, a_off[j], r0 * 2, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(src, dst, 16, (r0 + a_k[j] < R) ? a_off[j] + r0 * 2 : kOob, 0, 0,
+                                                 0);
     }
   };
 
-  auto store_lds = [&]() {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *(MO_LDS u32x4*)(As + a_row * kLds + a_k + 8 * i) = ra[i];
+  // Weight loads of the tile at reduction r0 into register set S.
+  auto load = [&](auto set, int r0) {
+    constexpr int S = decltype(set)::value;
+    const rsrc_t src = r0 < R ? rb_src : none;
     if (!kTransB) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int8_t* q = (const int8_t*)&rb[i];
+      for (int i = 0; i < kF; ++i)
+        rf[S][i] = kFullR ? __builtin_amdgcn_raw_buffer_load_b128(src, (int)f_off[i], r0, 0)
+                          : __builtin_amdgcn_raw_buffer_load_b128(
+                                src, (r0 + 16 * f_part < R) ? (int)(f_off[i] + r0) : (int)kOob, 0, 0);
+    } else {
+      const rsrc_t ssrc = r0 < R ? rs_src : none;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int rl = 8 * t_rg + i;
+        const bool ok = kFullR || r0 + rl < R;
+        const uint32_t off = t_col_ok ? (uint32_t)(rl * NC + kTn * t_ng) : kOob;
+        const int voff = kFullR ? (int)off : (ok ? (int)(off + (uint32_t)(r0 * NC)) : (int)kOob);
+        const int soff = kFullR ? r0 * NC : 0;
+        if (kTn == 8) {
+          const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(src, voff, soff, 0);
+          rt[S][i][0] = v[0];
+          rt[S][i][kTn / 8] = v[1];
+        } else {
+          rt[S][i][0] = __builtin_amdgcn_raw_buffer_load_b32(src, voff, soff, 0);
+        }
+        const int sv = kFullR ? rl * 4 : (ok ? (r0 + rl) * 4 : (int)kOob);
+        st[S][i] = bf16_round(
+            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ssrc, sv, kFullR ? r0 * 4 : 0, 0)));
+      }
+    }
+  };
+  constexpr int kLoads = kTransB ? 16 : kF;  // vector-memory operations of one load()
+
+  // Decode register set S into an LDS buffer, part p of 3 (p = -1: all parts).
+  auto stage = [&](auto set, MO_LDS __bf16* Bs, int p) {
+    constexpr int S = decltype(set)::value;
+    if (!kTransB) {
+#pragma unroll
+      for (int i = 0; i < kF; ++i) {
+        if (p >= 0 && i * 3 / kF != p) continue;
         bf16x8 lo, hi;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          lo[j] = decode(q[j], rs);
-          hi[j] = decode(q[8 + j], rs);
+          lo[j] = decode(rf[S][i][j >> 2], j & 3, sf[i]);
+          hi[j] = decode(rf[S][i][2 + (j >> 2)], j & 3, sf[i]);
         }
-        *(MO_LDS bf16x8*)(Bs + b_col * kLds + b_red + 16 * i) = lo;
-        *(MO_LDS bf16x8*)(Bs + b_col * kLds + b_red + 16 * i + 8) = hi;
+        *(MO_LDS bf16x8*)(Bs + wr_b[0] + i * kFcols * kBR) = lo;
+        *(MO_LDS bf16x8*)(Bs + wr_b[1] + i * kFcols * kBR) = hi;
       }
     } else {
-      // transposed: Bs[column][reduction]
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int8_t* q = (const int8_t*)&rb[i];
+      for (int c = 0; c < kTn; ++c) {
+        if (p >= 0 && c * 3 / kTn != p) continue;
+        bf16x8 v;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) *(MO_LDS __bf16*)(Bs + (b_col + 16 * i + j) * kLds + b_red) = decode(q[j], rs);
+        for (int i = 0; i < 8; ++i) v[i] = decode(rt[S][i][c >> 2], c & 3, st[S][i]);
+        *(MO_LDS bf16x8*)(Bs + wr_b[c]) = v;
       }
     }
   };
 
-  f32x16 acc[2][2];
+  // Instruction interleave of one slice (kWM x kWC MFMAs): fragment reads first, two per MFMA;
+  // in slice 0 the A DMA (with its M0 writes) and the weight loads; in slices 0-2 the decode
+  // VALU spread over the MFMAs and the decoded-tile LDS writes last.
+  auto schedule_slice = [&](int q) {
+    constexpr int kMfma = 0x008, kValu = 0x002, kDsRead = 0x100, kDsWrite = 0x200, kVmem = 0x020, kSalu = 0x004;
+    constexpr int kMf = kWM * kWC, kReadSlots = (kWM + kWC + 1) / 2;
+    constexpr int kWrites = kTransB ? 3 : 2;
+    if (kMf < 2 + kDma) return;  // too few MFMAs to interleave: leave it to the scheduler
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-  const int steps = (R + kBR - 1) / kBR;
-  load(0);
-  for (int s = 0; s < steps; ++s) {
-    __syncthreads();  // previous step's MFMAs are done reading LDS
-    store_lds();
-    __syncthreads();
-    if (s + 1 < steps) load((s + 1) * kBR);  // in flight during the MFMAs below
-    const int row_a = wm * 64 + (lane & 31);
-    const int row_b = wc * 64 + (lane & 31);
-    const int kq = 8 * (lane >> 5);
-#pragma unroll
-    for (int kk = 0; kk < kBR; kk += 16) {
-      bf16x8 a0 = *(MO_LDS bf16x8*)(As + row_a * kLds + kk + kq);
-      bf16x8 a1 = *(MO_LDS bf16x8*)(As + (row_a + 32) * kLds + kk + kq);
-      bf16x8 b0 = *(MO_LDS bf16x8*)(Bs + row_b * kLds + kk + kq);
-      bf16x8 b1 = *(MO_LDS bf16x8*)(Bs + (row_b + 32) * kLds + kk + kq);
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[1][1], 0, 0, 0);
+    for (int m = 0; m < kMf; ++m) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+      if (m < kReadSlots) __builtin_amdgcn_sched_group_barrier(kDsRead, 2, 0);
+      if (q == 0 && m >= 1 && m < 1 + kDma) {
+        __builtin_amdgcn_sched_group_barrier(kSalu, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(kVmem, 1, 0);
+      }
+      if (q == 0 && m == 1 + kDma) __builtin_amdgcn_sched_group_barrier(kVmem, kLoads, 0);
+      if (q < 3 && m >= kReadSlots) __builtin_amdgcn_sched_group_barrier(kValu, kVpm, 0);
+      if (q < 3 && m >= kMf - kWrites - 1 && m < kMf - 1) __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
     }
+  };
+
+  f32x16 acc[kWM][kWC];
+#pragma unroll
+  for (int i = 0; i < kWM; ++i)
+#pragma unroll
+    for (int j = 0; j < kWC; ++j) acc[i][j] = f32x16{};
+
+  bf16x8 fa[2][kWM], fb[2][kWC];  // fragments of two slices
+  auto read_frags = [&](const MO_LDS __bf16* As, const MO_LDS __bf16* Bs, int q, int slot) {
+#pragma unroll
+    for (int i = 0; i < kWM; ++i) fa[slot][i] = *(const MO_LDS bf16x8*)(As + rd_a[i & 1][q] + (i >> 1) * 64 * kBR);
+#pragma unroll
+    for (int j = 0; j < kWC; ++j) fb[slot][j] = *(const MO_LDS bf16x8*)(Bs + rd_b[j & 1][q] + (j >> 1) * 64 * kBR);
+  };
+
+  // One reduction step over (Ac, Bc); r_next is the reduction offset of the next step.
+  auto step = [&](const MO_LDS __bf16* Ac, const MO_LDS __bf16* Bc, MO_LDS __bf16* An, MO_LDS __bf16* Bn, int r_next,
+                  auto stage_set, auto load_set) {
+#pragma unroll
+    for (int q = 0; q < kBR / 16; ++q) {
+      const int cq = q & 1, nq = cq ^ 1;
+      if (q < 3)
+        read_frags(Ac, Bc, q + 1, nq);
+      else
+        read_frags(An, Bn, 0, nq);  // after the barrier: the next step's buffers are complete
+      if (q == 0) {
+        dma_a(An, r_next);
+        load(load_set, r_next + kBR);
+      }
+      if (q < 3) stage(stage_set, Bn, q);
+#pragma unroll
+      for (int i = 0; i < kWM; ++i)
+#pragma unroll
+        for (int j = 0; j < kWC; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cq][i], fb[cq][j], acc[i][j], 0, 0, 0);
+      schedule_slice(q);
+      __builtin_amdgcn_sched_barrier(0);
+      if (q == 2) {
+        // this wave's A DMA has landed (only its weight loads, issued after it, may be in
+        // flight) and its LDS reads and writes are done; then the whole workgroup
+        __builtin_amdgcn_s_waitcnt(wait_vm(kLoads, 0));
+        __syncthreads();
+      }
+    }
+  };
+
+  using set0 = std::integral_constant<int, 0>;
+  using set1 = std::integral_constant<int, 1>;
+  typedef MO_LDS __bf16* lp;
+  typedef const MO_LDS __bf16* clp;
+  const int steps = (R + kBR - 1) / kBR;
+  dma_a((lp)lds_a0, 0);
+  load(set0{}, 0);
+  stage(set0{}, (lp)lds_b0, -1);
+  load(set1{}, kBR);  // past R when steps == 1: zeros
+  __builtin_amdgcn_s_waitcnt(wait_vm(kLoads, 0));
+  __syncthreads();
+  read_frags((clp)lds_a0, (clp)lds_b0, 0, 0);
+  // Steps run in pairs (one per buffer) with no branch between them; an odd step count gets one
+  // more step over tiles past R, which read as zeros and add nothing.
+  for (int s = 0; s < steps; s += 2) {
+    step((clp)lds_a0, (clp)lds_b0, (lp)lds_a1, (lp)lds_b1, (s + 1) * kBR, set1{}, set0{});
+    step((clp)lds_a1, (clp)lds_b1, (lp)lds_a0, (lp)lds_b0, (s + 2) * kBR, set0{}, set1{});
   }
 
   // ---- epilogue: bias, bf16, store ----
+  // Lanes hold consecutive columns, so each store instruction writes two contiguous 64-byte
+  // row pieces.
+  const rsrc_t rc_src = make_rsrc(C + (size_t)m0 * NC, (uint32_t)(min(M - m0, kBM) * NC * 2));
+  // no bias: an empty descriptor, every read returns zero
+  const rsrc_t rbias_src = make_rsrc(bias, bias ? (uint32_t)NC * 2 : 0u);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = c0 + wc * 64 + j * 32 + (lane & 31);
-    if (col >= NC) continue;
-    const float b = bias ? (float)bias[col] : 0.f;
+  for (int j = 0; j < kWC; ++j) {
+    const int col = c0 + wc * G::kColsW + j * 32 + lr;
+    const bool col_ok = col < NC;
+    const float b = (float)__builtin_bit_cast(
+        __bf16, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rbias_src, col_ok ? col * 2 : (int)kOob, 0, 0));
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kWM; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < M) *(MO_GLOBAL __bf16*)(C + (size_t)row * NC + col) = (__bf16)(acc[i][j][r] + b);
+        const int row = wm * G::kRowsW + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);  // rows past M: outside
+        const __bf16 v = (__bf16)(acc[i][j][r] + b);
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), rc_src,
+                                              col_ok ? (int)((uint32_t)(row * NC + col) * 2) : (int)kOob, 0, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);  // one accumulator tile at a time (register pressure)
     }
   }
 }
 
+// Configurations: forward 256 x 256 over 2 x 4 waves (two waves a SIMD); input gradient
+// 256 x 256 over 2 x 2 waves; both directions 128 x 128 over 2 x 2 waves for grids too small
+// or too ragged for the large tile.
+using FwdLarge = Cfg<256, 256, 2, 4>;
+using BwdLarge = Cfg<256, 256, 2, 2>;
+using Small = Cfg<128, 128, 2, 2>;
+
 }  // namespace mo_gemm
 
-extern "C" __global__ __launch_bounds__(mo_gemm::kThreads) void mo_int8_linear_fwd_kernel(
-    const __bf16* A, const int8_t* Bq, const float* scale, const __bf16* bias, __bf16* C, int M, int NC, int R,
-    int tiles_m) {
-  mo_gemm::gemm_body<false>(A, Bq, scale, bias, C, M, NC, R, tiles_m);
-}
+#define MO_GEMM_FWD(NAME, G, FULL, VPM)                                                                            \
+  extern "C" __global__ __launch_bounds__(G::kThreads) void NAME(const __bf16* A, const int8_t* Bq,              \
+                                                                 const float* scale, const __bf16* bias,         \
+                                                                 __bf16* C, int M, int NC, int R, int tiles_m) { \
+    mo_gemm::gemm_body<G, false, FULL, VPM>(A, Bq, scale, bias, C, M, NC, R, tiles_m);                          \
+  }
+#define MO_GEMM_BWD(NAME, G, FULL, VPM)                                                                          \
+  extern "C" __global__ __launch_bounds__(G::kThreads) void NAME(const __bf16* A, const int8_t* Bq,            \
+                                                                 const float* scale, __bf16* C, int M, int NC, \
+                                                                 int R, int tiles_m) {                         \
+    mo_gemm::gemm_body<G, true, FULL, VPM>(A, Bq, scale, nullptr, C, M, NC, R, tiles_m);                       \
+  }
 
-extern "C" __global__ __launch_bounds__(mo_gemm::kThreads) void mo_int8_linear_bwd_kernel(
-    const __bf16* A, const int8_t* Bq, const float* scale, __bf16* C, int M, int NC, int R, int tiles_m) {
-  mo_gemm::gemm_body<true>(A, Bq, scale, nullptr, C, M, NC, R, tiles_m);
-}
+// full: R % 64 == 0; _tail: any multiple of 16
+MO_GEMM_FWD(mo_int8_linear_fwd_large, mo_gemm::FwdLarge, true, 6)
+MO_GEMM_FWD(mo_int8_linear_fwd_large_tail, mo_gemm::FwdLarge, false, 6)
+MO_GEMM_FWD(mo_int8_linear_fwd_small, mo_gemm::Small, true, 6)
+MO_GEMM_FWD(mo_int8_linear_fwd_small_tail, mo_gemm::Small, false, 6)
+MO_GEMM_BWD(mo_int8_linear_bwd_large, mo_gemm::BwdLarge, true, 6)
+MO_GEMM_BWD(mo_int8_linear_bwd_large_tail, mo_gemm::BwdLarge, false, 6)
+MO_GEMM_BWD(mo_int8_linear_bwd_small, mo_gemm::Small, true, 6)
+MO_GEMM_BWD(mo_int8_linear_bwd_small_tail, mo_gemm::Small, false, 6)

@@ -90,6 +90,52 @@ def test_backward_matches_fp64_reference(rows, in_f, out_f) -> None:
     _within_accumulation_bound(dx, exact, magnitude, out_f)
 
 
+# Launch plans on a 256-CU MI355X (csrc/mo_gemm.cpp): the large tile alone (a grid of exactly
+# 256 large tiles), the large tile plus a small-tile launch for the rows of a partial last round
+# (17792 x 3072: 840 tiles), the small tile alone (small shapes above); each with a reduction
+# length that is and is not a multiple of 64.
+PLAN_SHAPES = [(4096, 4096, 4096), (4096, 1040, 4096), (17792, 3072, 3072), (17792, 1040, 3072)]
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", PLAN_SHAPES)
+def test_forward_launch_plans_match_fp64_reference(rows, in_f, out_f) -> None:
+    x, w, scale, b = _operands(rows, in_f, out_f, seed=rows + in_f + 3 * out_f, bias=True)
+    y = quant_kernels.int8_linear_forward(x, w, scale, b)
+    decoded = quant_kernels.decode(w, scale, torch.bfloat16).double()
+    exact = x.double() @ decoded.t() + b.double()
+    magnitude = x.double().abs() @ decoded.abs().t()
+    _within_accumulation_bound(y, exact, magnitude, in_f)
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", [(4096, 4096, 4096), (4096, 4096, 1040), (17792, 3072, 3072),
+                                             (17792, 3072, 1040)])
+def test_backward_launch_plans_match_fp64_reference(rows, in_f, out_f) -> None:
+    _, w, scale, _ = _operands(1, in_f, out_f, seed=rows + 5 * in_f + out_f)
+    g = torch.Generator().manual_seed(rows + 1)
+    dy = torch.randn(rows, out_f, generator=g).to(torch.bfloat16).to(DEV)
+    dx = quant_kernels.int8_linear_backward(dy, w, scale, torch.Size((rows, in_f)))
+    decoded = quant_kernels.decode(w, scale, torch.bfloat16).double()
+    exact = dy.double() @ decoded
+    magnitude = dy.double().abs() @ decoded.abs()
+    _within_accumulation_bound(dx, exact, magnitude, out_f)
+
+
+def test_tile_choice_does_not_change_results() -> None:
+    # 17792 rows: large tiles for rows < 16384, small tiles after; 4096 and 1408 rows alone run
+    # on small tiles only. Each output element has one reduction order in every plan.
+    rows, in_f, out_f = 17792, 3072, 3072
+    x, w, scale, b = _operands(rows, in_f, out_f, seed=77, bias=True)
+    full = quant_kernels.int8_linear_forward(x, w, scale, b)
+    assert torch.equal(quant_kernels.int8_linear_forward(x[:4096], w, scale, b).view(torch.int16),
+                       full[:4096].view(torch.int16))
+    assert torch.equal(quant_kernels.int8_linear_forward(x[16384:], w, scale, b).view(torch.int16),
+                       full[16384:].view(torch.int16))
+    dy = x[:, :out_f].contiguous()
+    dfull = quant_kernels.int8_linear_backward(dy, w, scale, torch.Size((rows, in_f)))
+    part = quant_kernels.int8_linear_backward(dy[:4096], w, scale, torch.Size((4096, in_f)))
+    assert torch.equal(part.view(torch.int16), dfull[:4096].view(torch.int16))
+
+
 def test_unsupported_calls_are_reported_and_auto_falls_back_to_eager() -> None:
     x, w, scale, _ = _operands(4, 24, 16, seed=5)  # in_features not a multiple of 16
     assert quant_kernels.unsupported_reason(x, w, scale, torch.bfloat16) is not None
