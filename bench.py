@@ -16,7 +16,9 @@ sees each block's inputs. Regime B: no checkpointing, so the hook sees every act
 
 Prints ONE JSON line (stdout). Progress goes to stderr.
 
-  python bench.py [--steps K] [--warmup W] [--regimes M,A,B] [--micro-iters N]
+Leg Q: the config-5 int8 weight-only GEMMs on the HIP MFMA kernels against the eager path.
+
+  python bench.py [--steps K] [--warmup W] [--regimes M,Q,A,B] [--micro-iters N]
 """
 
 from __future__ import annotations
@@ -565,6 +567,84 @@ def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: 
     return out
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+# config-5 joint-block linears (out_features, in_features) and their count per block
+C5_GEMMS = {"qkvo": ((3072, 3072), 4), "ffn_up_gate": ((2 * 12288, 3072), 1), "ffn_down": ((3072, 12288), 1)}
+
+
+def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
+    """Config-5 int8 weight-only GEMMs (moss_offload.quant_kernels) on the packed token count of
+    one config-5 batch: forward and input gradient on the HIP kernels against the eager path
+    (decode the weight, then F.linear / matmul on hipBLASLt). Timed with HIP events on the stream
+    the kernels run on; TFLOP/s = 2 rows in out / average call time."""
+
+    import torch
+    import torch.nn.functional as F
+
+    from moss_offload import quant_kernels as qk
+
+    rows = sum(h * w + t for (h, w), t in zip(C5_BUCKETS, C5_TEXT))
+    g = torch.Generator(device=device).manual_seed(5)
+    stream = torch.cuda.current_stream(device)
+    calibration_copy(device, stream.cuda_stream)  # scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(iters):
+            fn()
+        stop.record(stream)
+        stop.synchronize()
+        return start.elapsed_time(stop) / 1e3 / iters
+
+    shapes = {}
+    block = {"hip": 0.0, "eager": 0.0}
+    block_flop = 0.0
+    for name, ((out_f, in_f), count) in C5_GEMMS.items():
+        x = torch.randn(rows, in_f, device=device, generator=g).to(torch.bfloat16)
+        dy = torch.randn(rows, out_f, device=device, generator=g).to(torch.bfloat16)
+        w = torch.randint(-127, 128, (out_f, in_f), dtype=torch.int8, device=device, generator=g)
+        s = torch.empty(out_f, device=device).uniform_(1e-3, 2e-2, generator=g)
+        assert qk.resolve_backend("auto", x, w, s, torch.bfloat16) == "hip"
+        flop = 2.0 * rows * in_f * out_f
+        t = {
+            "hip_fwd": timed(lambda: qk.int8_linear_forward(x, w, s)),
+            "hip_bwd": timed(lambda: qk.int8_linear_backward(dy, w, s, x.shape)),
+            "eager_fwd": timed(lambda: F.linear(x, qk.decode(w, s, torch.bfloat16))),
+            "eager_bwd": timed(lambda: dy.matmul(qk.decode(w, s, torch.bfloat16))),
+        }
+        with torch.no_grad():
+            wd = qk.decode(w, s, torch.bfloat16)
+            yh, ye = qk.int8_linear_forward(x, w, s).float(), F.linear(x, wd).float()
+            gh, ge = qk.int8_linear_backward(dy, w, s, x.shape).float(), dy.matmul(wd).float()
+        rec = {"rows": rows, "in_features": in_f, "out_features": out_f, "per_block": count}
+        for k, sec in t.items():
+            rec[k + "_ms"] = round(sec * 1e3, 4)
+            rec[k + "_tflops"] = round(flop / sec / 1e12, 1)
+        rec["fwd_vs_eager_max_rel_diff"] = ((yh - ye).abs().max() / ye.abs().max()).item()
+        rec["bwd_vs_eager_max_rel_diff"] = ((gh - ge).abs().max() / ge.abs().max()).item()
+        shapes[name] = rec
+        block["hip"] += count * (t["hip_fwd"] + t["hip_bwd"])
+        block["eager"] += count * (t["eager_fwd"] + t["eager_bwd"])
+        block_flop += count * 2 * flop
+        log(f"int8 GEMM {name} ({out_f}x{in_f}, {rows} rows): hip fwd {rec['hip_fwd_tflops']} bwd "
+            f"{rec['hip_bwd_tflops']} | eager fwd {rec['eager_fwd_tflops']} bwd {rec['eager_bwd_tflops']} TFLOP/s")
+        del x, dy, w, s, wd, yh, ye, gh, ge
+    achieved = block_flop / block["hip"] / 1e12
+    return {
+        "shapes": shapes,
+        "block_ms": {k: round(v * 1e3, 3) for k, v in block.items()},
+        "block_speedup_vs_eager": round(block["eager"] / block["hip"], 4),
+        "roofline": {"bound": "mfma", "kernels": "mo_int8_linear_{fwd,bwd}_{large,small}",
+                     "workload": "one config-5 joint block: 4 x qkvo + ffn_up_gate + ffn_down, forward and "
+                                 f"input gradient, {rows} rows",
+                     "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4)},
+    }
+
+
 def cpu_baseline(recorder, threads: int, budget_s: float = 15.0):
     """The oracle's restatement of the reference hooks with CPU payloads, on the host cores.
 
@@ -652,6 +732,10 @@ def run(args) -> dict:
             f"{m['unpack_hbm_gbps']:.0f} GB/s, bitwise {m['bitwise_first'] and m['bitwise_last']}")
         del tensors
 
+    if "Q" in args.regimes:
+        result["int8_gemm"] = int8_gemm_leg(device)
+        torch.cuda.empty_cache()
+
     c5 = {}
     full = {}
 
@@ -736,7 +820,7 @@ def run(args) -> dict:
             return model_f, opt_f, inputs, config3_forward, "A"
         raise ValueError(f"unknown regime {name}")
 
-    for regime_name in (r for r in args.regimes if r != "M"):
+    for regime_name in (r for r in args.regimes if r not in ("M", "Q")):
         wl_model, wl_opt, wl_inputs, forward, regime = workload(regime_name)
         manifest = record_manifest(wl_model, wl_inputs, regime, forward)
         payload_unique = manifest.payload_bytes(unique=True)
@@ -838,8 +922,9 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--steps-b", type=int, default=2)
     parser.add_argument("--warmup-b", type=int, default=1)
-    parser.add_argument("--regimes", default="M,A,B",
-                        help="M = config-2 block microbench, A/B = config-3 steps (checkpointed / not), "
+    parser.add_argument("--regimes", default="M,Q,A,B",
+                        help="M = config-2 block microbench, Q = config-5 int8 GEMMs (HIP vs eager), "
+                        "A/B = config-3 steps (checkpointed / not), "
                         "A4 = config 4 (2048^2, regime A), C5U/C5P = config 5 unpacked / packed (regime A), "
                         "S5 = config 5 packed with every block streamed from pinned host masters, "
                         "F3/F3S = full-parameter training at config-3 dims, resident / every block on the trainable ring")
@@ -942,6 +1027,7 @@ def main() -> int:
         "copy_hidden_fraction": eng.get("hidden_fraction"),
         "link_frac_of_spec": round(min(eng.get("d2h_gbps", 0.0), eng.get("h2d_gbps", 0.0)) / LINK_SPEC_GBPS, 4),
         "roofline": pack_bound,
+        "int8_gemm_roofline": result.get("int8_gemm", {}).get("roofline"),
         "cpu_baseline": cpu,
         "detail": result,
     }

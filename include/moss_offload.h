@@ -237,8 +237,9 @@ int mo_streamer_reset_stats(mo_streamer* streamer);
 /* y[rows][out] = x[rows][in] . decode(w)^T (+ bias), on bf16 MFMA with fp32 accumulation, where
  * decode(w)[n][k] = bf16(w[n][k] * bf16(scale[n])), the decode of quant_kernels.py:126-131.
  * x, y, bias: bf16 (bias may be 0); w: int8 [out][in] row-major; scale: fp32 [out].
- * in_features and out_features multiples of 16; x, w, y 16-byte aligned. Replaces
- * _int8_linear_forward_kernel (quant_kernels.py:100-157). */
+ * in_features and out_features multiples of 16, each at most 2^20, in * out < 2^31; x, w, y
+ * 16-byte aligned. Enqueued on `stream` (one or two kernel launches), no allocation, no host
+ * synchronisation. Replaces _int8_linear_forward_kernel (quant_kernels.py:100-157). */
 int mo_int8_linear_forward(uint64_t x, uint64_t w, uint64_t scale, uint64_t bias, uint64_t y, uint32_t rows,
                            uint32_t in_features, uint32_t out_features, uint64_t stream);
 

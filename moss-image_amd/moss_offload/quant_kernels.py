@@ -9,6 +9,14 @@ supported (bf16 activations and weight dtype on a HIP device, int8 weights, fp32
 feature sizes multiples of 16, contiguous operands) and the eager path otherwise; an explicit
 ``hip`` request that is not supported raises. The eager path is the reference's own eager
 backend (decode the weight, then ``F.linear``), not a substitute for a missing library.
+
+The reference's module interface for this path is kept under its own names, so that
+``training/quantization.py`` runs unchanged on top of this module: ``validate_quantized_backend``,
+``resolve_quantized_backend`` (``"triton"`` names the fused-kernel backend, here the HIP
+kernels), ``autocast_compute_dtype``, ``triton_is_available``, ``triton_int8_linear_forward``
+and ``triton_int8_linear_backward`` (reference ``quant_kernels.py:30-99, 294-374``). The HIP
+kernels take bf16 activations and a bf16 weight dtype; the reference's Triton kernels also take
+fp16 and fp32, which ``auto`` sends to the eager path here.
 """
 
 from __future__ import annotations
@@ -17,7 +25,7 @@ import torch
 
 from . import _native
 
-BACKENDS = {"auto", "eager", "hip"}
+BACKENDS = {"auto", "eager", "hip", "triton"}  # "triton": the reference's name for "hip"
 
 
 def unsupported_reason(tokens: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
@@ -50,6 +58,8 @@ def resolve_backend(backend: str, tokens: torch.Tensor, weight: torch.Tensor, sc
 
     if backend not in BACKENDS:
         raise ValueError("quantized backend must be auto, eager or hip.")
+    if backend == "triton":
+        backend = "hip"
     if backend == "eager":
         return backend
     reason = unsupported_reason(tokens, weight, scale, weight_dtype)
@@ -70,15 +80,24 @@ def _stream(tensor: torch.Tensor) -> int:
     return torch.cuda.current_stream(tensor.device).cuda_stream
 
 
+def _output(out: torch.Tensor | None, shape: tuple[int, int], device: torch.device, what: str) -> torch.Tensor:
+    if out is None:
+        return torch.empty(shape, dtype=torch.bfloat16, device=device)
+    if out.dtype != torch.bfloat16 or not out.is_contiguous() or out.numel() != shape[0] * shape[1] \
+            or out.device != device:
+        raise ValueError(f"HIP {what} buffer has the wrong dtype, size or device, or is not contiguous.")
+    return out.view(shape)
+
+
 def int8_linear_forward(tokens: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
-                        bias: torch.Tensor | None = None) -> torch.Tensor:
+                        bias: torch.Tensor | None = None, *, out: torch.Tensor | None = None) -> torch.Tensor:
     """``tokens @ decode(weight).T (+ bias)`` on the HIP kernel; the call must be supported."""
 
     lib = _native.load()
     matrix = tokens.reshape(-1, tokens.shape[-1]).contiguous()
     rows, in_features = matrix.shape
     out_features = weight.shape[0]
-    out = torch.empty((rows, out_features), dtype=torch.bfloat16, device=tokens.device)
+    out = _output(out, (rows, out_features), tokens.device, "output")
     if bias is not None:
         bias = bias.to(torch.bfloat16).contiguous()
     _native.check(
@@ -91,17 +110,90 @@ def int8_linear_forward(tokens: torch.Tensor, weight: torch.Tensor, scale: torch
 
 
 def int8_linear_backward(gradient: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
-                         input_shape: torch.Size) -> torch.Tensor:
+                         input_shape: torch.Size, *, out: torch.Tensor | None = None) -> torch.Tensor:
     """``gradient @ decode(weight)``: the input gradient of the frozen int8 linear."""
 
     lib = _native.load()
     matrix = gradient.reshape(-1, gradient.shape[-1]).to(torch.bfloat16).contiguous()
     rows, out_features = matrix.shape
     in_features = weight.shape[1]
-    out = torch.empty((rows, in_features), dtype=torch.bfloat16, device=gradient.device)
+    out = _output(out, (rows, in_features), gradient.device, "input-gradient")
     _native.check(
         "mo_int8_linear_backward",
         lib.mo_int8_linear_backward(matrix.data_ptr(), weight.data_ptr(), scale.data_ptr(), out.data_ptr(), rows,
                                     in_features, out_features, _stream(gradient)),
     )
     return out.reshape(input_shape)
+
+
+# ---- the reference module's interface (training/quant_kernels.py), same names and meaning ----
+
+def validate_quantized_backend(backend: str) -> str:
+    """``auto``, ``eager`` or ``triton`` (reference ``quant_kernels.py:30-33``)."""
+
+    if backend not in {"auto", "eager", "triton"}:
+        raise ValueError("quantized backend must be auto, eager or triton.")
+    return backend
+
+
+def triton_is_available() -> bool:
+    """Whether the fused-kernel backend can run: the HIP library loads and a HIP device is
+    present (reference ``quant_kernels.py:36-38``, with the HIP kernels in place of Triton)."""
+
+    if not torch.cuda.is_available():
+        return False
+    try:
+        _native.load()
+    except (OSError, RuntimeError):
+        return False
+    return True
+
+
+def resolve_quantized_backend(backend: str, tokens: torch.Tensor, weight: torch.Tensor,
+                              scale: torch.Tensor) -> str:
+    """``auto`` -> ``triton`` when the fused kernels support the call, else ``eager``; an explicit
+    ``triton`` must be supported (reference ``quant_kernels.py:64-79``). The weight dtype is
+    the input's, as the reference's callers convert the input to it before the kernel."""
+
+    selected = validate_quantized_backend(backend)
+    if selected == "eager":
+        return selected
+    reason = unsupported_reason(tokens, weight, scale, tokens.dtype)
+    if reason is None and not triton_is_available():
+        reason = "the HIP library or device is unavailable"
+    if selected == "auto":
+        return "eager" if reason is not None else "triton"
+    if reason is not None:
+        raise RuntimeError(f"Triton quantized backend is unavailable: {reason}.")
+    return selected
+
+
+def autocast_compute_dtype(tokens: torch.Tensor, module_dtype: torch.dtype) -> torch.dtype:
+    """The dtype autocast gives a linear on ``tokens`` (reference ``quant_kernels.py:82-96``)."""
+
+    if tokens.device.type != "cuda" or not torch.is_autocast_enabled("cuda"):
+        return module_dtype
+    return torch.get_autocast_dtype("cuda")
+
+
+def triton_int8_linear_forward(tokens: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
+                               bias: torch.Tensor | None, output_dtype: torch.dtype, weight_dtype: torch.dtype,
+                               *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Reference ``quant_kernels.py:294-334`` on the HIP kernel: bf16 output and weight dtype."""
+
+    if output_dtype != torch.bfloat16 or weight_dtype != torch.bfloat16:
+        raise TypeError(f"HIP int8 kernels compute in bf16 (got output {output_dtype}, weight {weight_dtype}).")
+    if bias is not None and (bias.device != tokens.device or not bias.is_contiguous()):
+        raise RuntimeError("Triton quantized bias must be contiguous and on the input device.")
+    return int8_linear_forward(tokens, weight, scale, bias, out=out)
+
+
+def triton_int8_linear_backward(gradient: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
+                                input_shape: torch.Size, input_dtype: torch.dtype, weight_dtype: torch.dtype,
+                                *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Reference ``quant_kernels.py:337-373`` on the HIP kernel: the input gradient only."""
+
+    if input_dtype != torch.bfloat16 or weight_dtype != torch.bfloat16:
+        raise TypeError(f"HIP int8 kernels compute in bf16 (got input {input_dtype}, weight {weight_dtype}).")
+    return int8_linear_backward(gradient.contiguous(), weight, scale, input_shape, out=out)
+

@@ -147,6 +147,56 @@ def test_unsupported_calls_are_reported_and_auto_falls_back_to_eager() -> None:
     assert quant_kernels.resolve_backend("auto", x.float(), w, scale, torch.float32) == "eager"
 
 
+@pytest.mark.parametrize("case,reason", [
+    ("dtype", "only bf16"), ("wdtype", "int8 and scales float32"), ("shape", "dimensions do not match"),
+    ("ragged", "multiples of 16"), ("strided", "contiguous"), ("empty", "empty input"),
+])
+def test_unsupported_reasons_name_the_cause(case, reason) -> None:
+    x, w, scale, _ = _operands(4, 32, 16, seed=9)
+    dtype = torch.bfloat16
+    if case == "dtype":
+        x, dtype = x.float(), torch.float32
+    elif case == "wdtype":
+        scale = scale.double()
+    elif case == "shape":
+        w = torch.zeros(16, 48, dtype=torch.int8, device=DEV)
+    elif case == "ragged":
+        x, w, scale, _ = _operands(4, 24, 16, seed=9)
+    elif case == "strided":
+        w = torch.zeros(32, 16, dtype=torch.int8, device=DEV).t()
+    elif case == "empty":
+        x = x[:0]
+    got = quant_kernels.unsupported_reason(x, w, scale, dtype)
+    assert got is not None and reason in got
+    assert quant_kernels.resolve_quantized_backend("auto", x, w, scale) == "eager"
+
+
+def test_reference_interface_runs_the_hip_kernels() -> None:
+    # the sequence of the reference's _FrozenInt8Linear (quantization.py:28-61) on this module
+    x, w, scale, b = _operands(300, 1040, 208, seed=31, bias=True)
+    assert quant_kernels.triton_is_available()
+    assert quant_kernels.resolve_quantized_backend("auto", x, w, scale) == "triton"
+    assert quant_kernels.resolve_quantized_backend("triton", x, w, scale) == "triton"
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out_dtype = quant_kernels.autocast_compute_dtype(x, torch.bfloat16)
+    assert out_dtype == torch.bfloat16
+    y = quant_kernels.triton_int8_linear_forward(x, w, scale, b, out_dtype, torch.bfloat16)
+    assert torch.equal(y.view(torch.int16), quant_kernels.int8_linear_forward(x, w, scale, b).view(torch.int16))
+    buf = torch.empty(300 * 208, dtype=torch.bfloat16, device=DEV)
+    y2 = quant_kernels.triton_int8_linear_forward(x, w, scale, b, out_dtype, torch.bfloat16, out=buf)
+    assert y2.data_ptr() == buf.data_ptr() and torch.equal(y2.view(torch.int16), y.view(torch.int16))
+    g = torch.randn(300, 208, device=DEV).to(torch.bfloat16)
+    dx = quant_kernels.triton_int8_linear_backward(g, w, scale, x.shape, torch.bfloat16, torch.bfloat16)
+    assert dx.shape == x.shape
+    assert torch.equal(dx.view(torch.int16),
+                       quant_kernels.int8_linear_backward(g, w, scale, x.shape).view(torch.int16))
+    with pytest.raises(TypeError, match="bf16"):
+        quant_kernels.triton_int8_linear_forward(x.float(), w, scale, None, torch.float32, torch.float32)
+    with pytest.raises(ValueError, match="buffer"):
+        quant_kernels.triton_int8_linear_forward(x, w, scale, None, out_dtype, torch.bfloat16,
+                                                 out=torch.empty(5, dtype=torch.bfloat16, device=DEV))
+
+
 def test_int8_lora_model_hip_backend_matches_eager() -> None:
     torch.manual_seed(121)
     model = dit.MOSSImageTransformer(dim=64, ffn_dim=128, num_heads=4, num_layers=2, text_dim=16, freq_dim=8,
