@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 4
+#define MO_ABI_VERSION 5
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -248,6 +248,49 @@ int mo_int8_linear_forward(uint64_t x, uint64_t w, uint64_t scale, uint64_t bias
  * (quant_kernels.py:160-209). */
 int mo_int8_linear_backward(uint64_t dy, uint64_t w, uint64_t scale, uint64_t dx, uint32_t rows,
                             uint32_t in_features, uint32_t out_features, uint64_t stream);
+
+/* ---- host gradient accumulation (training/fused_adafactor.py:327-369) -------------------- */
+
+/* Gradient element types: the reference's value-kind codes (quant_kernels.py:280-287). */
+enum { MO_DTYPE_F16 = 0, MO_DTYPE_BF16 = 1, MO_DTYPE_F32 = 2 };
+
+typedef struct mo_gradacc mo_gradacc;
+
+typedef struct mo_gradacc_stats {
+  uint64_t calls;          /* mo_gradacc_accumulate calls */
+  uint64_t chunks;         /* staging-slot copies they issued */
+  uint64_t bytes;          /* gradient bytes issued over the link */
+  uint64_t elements;       /* elements accumulated on the host */
+  uint64_t d2h_done_bytes; /* completed, timed D2H bytes */
+  double d2h_ms;           /* SDMA busy time of those copies */
+  double accumulate_ms;    /* host time converting and adding */
+  uint64_t host_blocks;    /* calls that blocked the host (no free slot, or mo_gradacc_wait) */
+  double host_block_ms;
+  uint64_t pending_chunks; /* copies not yet accumulated */
+  uint64_t copy_failures;
+} mo_gradacc_stats;
+
+/* An accumulator on `device`: `slots` device staging slots of `slot_bytes` (a multiple of 4096)
+ * each with a pinned host twin, an SDMA D2H link on engine `d2h_engine`, and `host_threads`
+ * threads for the host additions. Replaces the blocking pinned copy of
+ * FusedAdafactor._stash_gradient_on_host (fused_adafactor.py:337-346). */
+int mo_gradacc_create(int device, uint32_t slots, uint64_t slot_bytes, uint32_t host_threads, uint32_t d2h_engine,
+                      mo_gradacc** out);
+/* Waits (bounded) for every pending accumulation, then frees the accumulator. */
+int mo_gradacc_destroy(mo_gradacc* acc);
+/* dst[i] = x[i] (first != 0) or dst[i] += x[i], i < count, where x = fp32(src) and src is a
+ * device gradient of `dtype` and dst a host fp32 buffer (pinned or pageable). The gradient is
+ * copied into staging slots on `stream` before the call returns, so the caller may free it
+ * afterwards under the stream's ordering; the D2H and the host additions run in the
+ * background, in call order, one IEEE fp32 add per element and call (the reference's
+ * accumulated.add_(host_gradient), fused_adafactor.py:347-352). Blocks the host only while
+ * every slot is in flight. `dst` must not be read or written until mo_gradacc_wait(acc, dst). */
+int mo_gradacc_accumulate(mo_gradacc* acc, uint64_t dst, uint32_t first, uint64_t src, uint32_t dtype,
+                          uint64_t count, uint64_t stream);
+/* Block until every accumulation into `dst` (the `dst` a call passed; 0 = all) is complete. */
+int mo_gradacc_wait(mo_gradacc* acc, uint64_t dst);
+int mo_gradacc_get_stats(mo_gradacc* acc, mo_gradacc_stats* out);
+int mo_gradacc_reset_stats(mo_gradacc* acc);
 
 #ifdef __cplusplus
 }

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 4
+MO_ABI_VERSION = 5
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -126,6 +126,25 @@ class MoStreamerStats(ctypes.Structure):
         return {name: getattr(self, name) for name, _ in self._fields_}
 
 
+class MoGradaccStats(ctypes.Structure):
+    _fields_ = [
+        ("calls", ctypes.c_uint64),
+        ("chunks", ctypes.c_uint64),
+        ("bytes", ctypes.c_uint64),
+        ("elements", ctypes.c_uint64),
+        ("d2h_done_bytes", ctypes.c_uint64),
+        ("d2h_ms", ctypes.c_double),
+        ("accumulate_ms", ctypes.c_double),
+        ("host_blocks", ctypes.c_uint64),
+        ("host_block_ms", ctypes.c_double),
+        ("pending_chunks", ctypes.c_uint64),
+        ("copy_failures", ctypes.c_uint64),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
 class EngineError(RuntimeError):
     """A non-zero status from the engine library, with its message."""
 
@@ -172,6 +191,14 @@ SIGNATURES: dict[str, tuple] = {
     "mo_streamer_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
     "mo_streamer_get_stats": (ctypes.c_int, [ctypes.c_void_p, _P(MoStreamerStats)]),
     "mo_streamer_reset_stats": (ctypes.c_int, [ctypes.c_void_p]),
+    "mo_gradacc_create": (ctypes.c_int, [ctypes.c_int, ctypes.c_uint32, _u64, ctypes.c_uint32, ctypes.c_uint32,
+                                         _P(ctypes.c_void_p)]),
+    "mo_gradacc_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "mo_gradacc_accumulate": (ctypes.c_int, [ctypes.c_void_p, _u64, ctypes.c_uint32, _u64, ctypes.c_uint32, _u64,
+                                             _u64]),
+    "mo_gradacc_wait": (ctypes.c_int, [ctypes.c_void_p, _u64]),
+    "mo_gradacc_get_stats": (ctypes.c_int, [ctypes.c_void_p, _P(MoGradaccStats)]),
+    "mo_gradacc_reset_stats": (ctypes.c_int, [ctypes.c_void_p]),
     "mo_int8_linear_forward": (ctypes.c_int, [_u64, _u64, _u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32,
                                               ctypes.c_uint32, _u64]),
     "mo_int8_linear_backward": (ctypes.c_int, [_u64, _u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32,

@@ -47,6 +47,7 @@ def _c_layouts(tmp_path: Path) -> dict[str, int]:
         "mo_ref": [f for f, _ in _native.MoRef._fields_],
         "mo_stats": [f for f, _ in _native.MoStats._fields_],
         "mo_streamer_stats": [f for f, _ in _native.MoStreamerStats._fields_],
+        "mo_gradacc_stats": [f for f, _ in _native.MoGradaccStats._fields_],
     }
     lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {"]
     for struct, names in fields.items():
@@ -65,7 +66,8 @@ def _c_layouts(tmp_path: Path) -> dict[str, int]:
 def test_struct_layouts_match_ctypes(tmp_path) -> None:
     c = _c_layouts(tmp_path)
     for struct, cls in (("mo_tensor", _native.MoTensor), ("mo_config", _native.MoConfig), ("mo_ref", _native.MoRef),
-                        ("mo_stats", _native.MoStats), ("mo_streamer_stats", _native.MoStreamerStats)):
+                        ("mo_stats", _native.MoStats), ("mo_streamer_stats", _native.MoStreamerStats),
+                        ("mo_gradacc_stats", _native.MoGradaccStats)):
         assert c[struct] == ctypes.sizeof(cls), struct
         for name, _ in cls._fields_:
             assert c[f"{struct}.{name}"] == getattr(cls, name).offset, f"{struct}.{name}"
