@@ -645,6 +645,87 @@ def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
     }
 
 
+def host_grad_leg(device, layers: int, steps: int, warmup: int, threads: int) -> dict:
+    """Host fp32 gradient accumulation (FusedAdafactor's CPU accumulation mode) on full-parameter
+    training at config-3 dims (regime A): each logical step is two micro-batches; the first
+    runs with the step disabled, so every gradient is stashed on the host, and the second
+    applies an in-backward SGD update from the current gradient plus the host sum.
+
+      device     early gradients stay on the device (the reference's default mode)
+      engine     moss_offload.host_gradients.HostGradientAccumulator (16 x 64 MiB staging slots +
+                 SDMA + background fp32 adds; the take through pop_to_device, prefetched by SDMA)
+      reference  the reference's stash restated: fp32 pinned tensor, blocking copy_, host add_
+    """
+
+    import torch
+
+    from moss_offload.harness_optim import HostModeSGD
+    from moss_offload.host_gradients import HostGradientAccumulator
+
+    model = build_full_model(device, layers)
+    model.gradient_checkpointing = True
+    model.checkpoint_fraction = 1.0
+    model.activation_offload = False
+    micro = [make_inputs(device, seed=0), make_inputs(device, seed=1)]
+    trainable = [p for p in model.parameters() if p.requires_grad]
+    grad_bytes = sum(p.numel() * p.element_size() for p in trainable)
+    out = {"layers": layers, "micro_batches": 2, "parameters": sum(p.numel() for p in trainable),
+           "gradient_bytes_per_micro_batch": grad_bytes, "host_threads": threads}
+    gc.collect()
+    gc.freeze()
+
+    def logical_step(opt):
+        opt.set_step_enabled(False)
+        loss_and_backward(model, micro[0])
+        opt.set_step_enabled(True)
+        loss_and_backward(model, micro[1])
+        opt.finish_backward()
+
+    for mode in ("device", "engine", "reference"):
+        acc = HostGradientAccumulator(device, slots=16, host_threads=threads) if mode == "engine" else None
+        opt = HostModeSGD(trainable, 1e-6, stash=mode, accumulator=acc)
+        for i in range(warmup):
+            t0 = time.perf_counter()
+            logical_step(opt)
+            torch.cuda.synchronize()
+            log(f"G/{mode}: warmup {i + 1}/{warmup} {time.perf_counter() - t0:.3f} s")
+        if acc is not None:
+            acc.synchronize()
+            acc.reset_stats()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        start = time.perf_counter()
+        for _ in range(steps):
+            logical_step(opt)
+        torch.cuda.synchronize()
+        elapsed = (time.perf_counter() - start) / steps
+        rec = {"s_per_step": elapsed, "peak_device_bytes": torch.cuda.max_memory_allocated()}
+        if acc is not None:
+            st = acc.stats()
+            rec.update(
+                link_bytes_per_step=st["bytes"] / steps,
+                d2h_gbps=st["d2h_done_bytes"] / max(st["d2h_ms"], 1e-9) / 1e6,
+                d2h_busy_s_per_step=st["d2h_ms"] / 1e3 / steps,
+                host_accumulate_s_per_step=st["accumulate_ms"] / 1e3 / steps,
+                host_accumulate_gelems_per_s=st["elements"] / max(st["accumulate_ms"], 1e-9) / 1e6,
+                host_blocks_per_step=st["host_blocks"] / steps,
+                host_block_s_per_step=st["host_block_ms"] / 1e3 / steps,
+                copy_failures=st["copy_failures"],
+            )
+        log(f"G/{mode}: {elapsed:.4f} s per logical step (2 micro-batches), peak device "
+            f"{rec['peak_device_bytes'] / 2**30:.1f} GiB")
+        opt.close()
+        del opt, acc
+        gc.collect()
+        torch.cuda.synchronize()
+        torch._C._host_emptyCache()
+        out[mode] = rec
+    base = out["device"]["s_per_step"]
+    for mode in ("engine", "reference"):
+        out[mode]["exposed_s"] = out[mode]["s_per_step"] - base
+    return out
+
+
 def cpu_baseline(recorder, threads: int, budget_s: float = 15.0):
     """The oracle's restatement of the reference hooks with CPU payloads, on the host cores.
 
@@ -735,6 +816,10 @@ def run(args) -> dict:
     if "Q" in args.regimes:
         result["int8_gemm"] = int8_gemm_leg(device)
         torch.cuda.empty_cache()
+    if "G" in args.regimes:
+        result["host_gradients"] = host_grad_leg(device, args.layers, max(1, args.steps_b), max(1, args.warmup_b),
+                                                 args.gradacc_threads)
+        torch.cuda.empty_cache()
 
     c5 = {}
     full = {}
@@ -820,7 +905,7 @@ def run(args) -> dict:
             return model_f, opt_f, inputs, config3_forward, "A"
         raise ValueError(f"unknown regime {name}")
 
-    for regime_name in (r for r in args.regimes if r not in ("M", "Q")):
+    for regime_name in (r for r in args.regimes if r not in ("M", "Q", "G")):
         wl_model, wl_opt, wl_inputs, forward, regime = workload(regime_name)
         manifest = record_manifest(wl_model, wl_inputs, regime, forward)
         payload_unique = manifest.payload_bytes(unique=True)
@@ -924,7 +1009,8 @@ def main() -> int:
     parser.add_argument("--warmup-b", type=int, default=1)
     parser.add_argument("--regimes", default="M,Q,A,B",
                         help="M = config-2 block microbench, Q = config-5 int8 GEMMs (HIP vs eager), "
-                        "A/B = config-3 steps (checkpointed / not), "
+                        "A/B = config-3 steps (checkpointed / not), G = host gradient accumulation "
+                        "(full-parameter config-3 dims, 2 micro-batches: device / engine / reference stash), "
                         "A4 = config 4 (2048^2, regime A), C5U/C5P = config 5 unpacked / packed (regime A), "
                         "S5 = config 5 packed with every block streamed from pinned host masters, "
                         "F3/F3S = full-parameter training at config-3 dims, resident / every block on the trainable ring")
@@ -939,6 +1025,7 @@ def main() -> int:
     parser.add_argument("--no-staged-restore", action="store_true")
     parser.add_argument("--kernel-copy", action="store_true", help="copy kernel on HIP streams instead of SDMA")
     parser.add_argument("--cpu-threads", type=int, default=16)
+    parser.add_argument("--gradacc-threads", type=int, default=12, help="host threads of the G leg's accumulator")
     parser.add_argument("--cpu-budget", type=float, default=15.0)
     args = parser.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))

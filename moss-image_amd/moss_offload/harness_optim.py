@@ -9,12 +9,15 @@ Control flow restated from ``training/fused_adafactor.py``:
   (``_stash_gradient_on_host``, ``:327-355``). While it is enabled (the boundary micro-batch),
   a hook applies the update (``step_parameter``, ``:456-471``).
 - the update uses the current gradient plus the popped host sum, ``current.float() +
-  previous.to(device)`` (``_take_accumulated_gradient``, ``:357-369``).
+  previous.to(device)`` (``_take_accumulated_gradient``, ``:357-369``); with the engine the sum
+  comes from ``pop_to_device`` (prefetched over SDMA) instead of a blocking copy.
 - ``finish_backward`` (``:515-524``) updates the parameters that only have a host sum.
 
-Two stashes:
+Stashes:
 
 - ``"engine"``: :class:`moss_offload.host_gradients.HostGradientAccumulator`.
+- ``"device"``: none; early gradients stay in ``parameter.grad`` on the device (the reference's
+  default ``gradient_accumulation_device="device"``), the point of comparison.
 - ``"reference"``: the reference's own, an fp32 pinned ``torch.empty`` per stash, a blocking
   ``copy_`` and a host ``add_`` into a plain dict (``:336-352``). It is the baseline of the bench's
   host-gradient leg and the oracle of the GPU tests.
@@ -35,8 +38,8 @@ class HostModeSGD:
 
     def __init__(self, parameters: Iterable[nn.Parameter], lr: float, *, stash: str = "engine",
                  accumulator: MutableMapping | None = None) -> None:
-        if stash not in ("engine", "reference"):
-            raise ValueError("stash must be 'engine' or 'reference'")
+        if stash not in ("engine", "reference", "device"):
+            raise ValueError("stash must be 'engine', 'reference' or 'device'")
         self.lr = float(lr)
         self.stash_kind = stash
         self.parameters = [p for p in parameters if p.requires_grad]
@@ -53,7 +56,7 @@ class HostModeSGD:
     def _hook(self, parameter: nn.Parameter) -> None:
         if self.step_enabled:
             self.step_parameter(parameter)
-        else:
+        elif self.stash_kind != "device":
             self.stash(parameter)
 
     @torch.no_grad()
@@ -80,7 +83,11 @@ class HostModeSGD:
     @torch.no_grad()
     def take(self, parameter: nn.Parameter) -> torch.Tensor | None:
         current = parameter.grad
-        previous = self.host_gradients.pop(id(parameter), None)
+        pop_to_device = getattr(self.host_gradients, "pop_to_device", None)
+        if pop_to_device is not None:  # the engine: prefetched by SDMA, no blocking copy
+            previous = pop_to_device(id(parameter), None if current is None else current.device)
+        else:
+            previous = self.host_gradients.pop(id(parameter), None)
         if previous is None:
             return current
         if current is None:

@@ -24,6 +24,13 @@ own path (``gradient.to(cpu, fp32).clone()`` then ``add_``).
 
 An entry's fp32 buffer is pinned, allocated at the key's first use and reused by later steps:
 a tensor read from the mapping stays valid until the next ``accumulate`` into the same key.
+
+:meth:`~HostGradientAccumulator.pop_to_device` replaces the take's blocking
+``previous.to(device, non_blocking=False)`` (``:369``). It returns the entry as a device fp32
+tensor and starts SDMA copies of the next entries, in the order of their first contribution,
+while the caller computes. That is the order the next micro-batch's hooks ask for them. The
+copies use a frozen-block streamer (``mo_streamer_*``): each is ordered after the compute
+stream's work on the fresh device tensor, and the host waits for it only when it is popped.
 """
 
 from __future__ import annotations
@@ -55,7 +62,8 @@ class HostGradientAccumulator(MutableMapping):
     """``key -> fp32 host tensor`` of the gradients accumulated in the current step."""
 
     def __init__(self, device: torch.device | str | int | None = None, *, slots: int = 4,
-                 slot_bytes: int = 64 << 20, host_threads: int = 8, d2h_engine: int = 0) -> None:
+                 slot_bytes: int = 64 << 20, host_threads: int = 8, d2h_engine: int = 0,
+                 prefetch: int = 4) -> None:
         if device is not None:
             device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
             if device.type != "cuda":
@@ -70,6 +78,12 @@ class HostGradientAccumulator(MutableMapping):
         self._device_keys: set[Hashable] = set()  # entries filled by the native path
         self._lock = threading.Lock()
         self._closed = False
+        self._order: list[Hashable] = []  # keys of this step in the order of their first contribution
+        self._pos: dict[Hashable, int] = {}  # key -> index in _order
+        self._prefetch_slots = int(prefetch)
+        self._streamer: ctypes.c_void_p | None = None
+        self._free_slots: list[int] = []
+        self._prefetched: dict[Hashable, tuple[int, torch.Tensor]] = {}
 
     # ---- native accumulator ------------------------------------------------------------------
     def _native(self, device: torch.device):
@@ -125,8 +139,12 @@ class HostGradientAccumulator(MutableMapping):
             if code is None:
                 raise TypeError(f"HostGradientAccumulator takes fp16, bf16 or fp32 gradients, not {gradient.dtype}.")
             lib, handle = self._native(gradient.device)
+            self._discard_prefetch(key)
             numel = gradient.numel()
             first = key not in self._entries
+            if first:
+                self._pos[key] = len(self._order)
+                self._order.append(key)
             if not first and key not in self._device_keys:
                 # a CPU-path or assigned entry: continue it in the native buffer
                 self._adopt(key, numel)
@@ -158,6 +176,87 @@ class HostGradientAccumulator(MutableMapping):
         self._entries[key] = buffer.flat.view(value.shape)
         self._device_keys.add(key)
 
+    # ---- the take on the device --------------------------------------------------------------
+    def _h2d_streamer(self):
+        if self._streamer is None:
+            streamer = ctypes.c_void_p()
+            _native.check("mo_streamer_create", self._lib.mo_streamer_create(
+                self._device.index or 0, max(self._prefetch_slots, 1), 0, ctypes.byref(streamer)))
+            self._streamer = streamer
+            self._free_slots = list(range(max(self._prefetch_slots, 1)))
+        return self._streamer
+
+    def _issue(self, key: Hashable, stream: int) -> None:
+        """Start the SDMA copy of ``key``'s completed sum into a fresh device tensor."""
+
+        streamer = self._h2d_streamer()
+        self._wait(key)
+        value = self._entries[key]
+        slot = self._free_slots.pop()
+        tensor = torch.empty(value.shape, dtype=torch.float32, device=self._device)
+        # the fill waits for the compute stream to pass this point: the fresh tensor's memory
+        # is no longer in use by earlier kernels
+        _native.check("mo_streamer_release", self._lib.mo_streamer_release(streamer, slot, stream))
+        _native.check("mo_streamer_fill", self._lib.mo_streamer_fill(
+            streamer, slot, tensor.data_ptr(), self._buffers[key].address, value.numel() * 4))
+        self._prefetched[key] = (slot, tensor)
+
+    def _claim(self, key: Hashable, stream: int) -> torch.Tensor:
+        slot, tensor = self._prefetched.pop(key)
+        try:
+            _native.check("mo_streamer_acquire", self._lib.mo_streamer_acquire(self._streamer, slot, stream))
+        finally:
+            self._free_slots.append(slot)
+        return tensor
+
+    def _discard_prefetch(self, key: Hashable) -> None:
+        if key in self._prefetched:
+            stream = torch.cuda.current_stream(self._device).cuda_stream
+            self._claim(key, stream)
+
+    def pop_to_device(self, key: Hashable, device: torch.device | str | None = None) -> torch.Tensor | None:
+        """``pop(key)`` as an fp32 tensor on the device, or None without an entry.
+
+        Waits for the key's own copy only (usually already done), then prefetches the entries
+        that follow it in first-contribution order into free slots. A CPU-path entry is moved
+        with a plain copy.
+        """
+
+        with self._lock:
+            if key not in self._entries:
+                return None
+            if key not in self._device_keys or self._handle is None:
+                # a CPU-path entry: moved only when a device is named (the reference keeps a
+                # host-only sum on the host, fused_adafactor.py:365-366)
+                value = self._entries.pop(key)
+                self._end_of_step()
+                return value if device is None else value.to(device=device, dtype=torch.float32, non_blocking=False)
+            if device is not None and torch.device(device) != self._device:
+                raise RuntimeError(f"HostGradientAccumulator serves {self._device}; asked for {device}.")
+            stream = torch.cuda.current_stream(self._device).cuda_stream
+            if key not in self._prefetched:
+                self._h2d_streamer()
+                if not self._free_slots:  # every slot holds a prefetch of another key: take one back
+                    self._claim(next(reversed(self._prefetched)), stream)
+                self._issue(key, stream)
+            tensor = self._claim(key, stream)
+            del self._entries[key]
+            self._device_keys.discard(key)
+            # the following keys, while the caller computes
+            index = self._pos.pop(key, len(self._order)) + 1
+            while self._free_slots and index < len(self._order):
+                other = self._order[index]
+                if other in self._device_keys and other not in self._prefetched:
+                    self._issue(other, stream)
+                index += 1
+            self._end_of_step()
+            return tensor
+
+    def _end_of_step(self) -> None:
+        if not self._entries:
+            self._order.clear()
+            self._pos.clear()
+
     # ---- the mapping ------------------------------------------------------------------------
     def __getitem__(self, key: Hashable) -> torch.Tensor:
         with self._lock:
@@ -178,8 +277,10 @@ class HostGradientAccumulator(MutableMapping):
             if key not in self._entries:
                 raise KeyError(key)
             self._wait(key)
+            self._discard_prefetch(key)
             del self._entries[key]
             self._device_keys.discard(key)
+            self._end_of_step()
 
     def __contains__(self, key: object) -> bool:
         return key in self._entries
@@ -193,8 +294,11 @@ class HostGradientAccumulator(MutableMapping):
     def clear(self) -> None:
         with self._lock:
             self._wait(None)
+            for key in list(self._prefetched):
+                self._discard_prefetch(key)
             self._entries.clear()
             self._device_keys.clear()
+            self._end_of_step()
 
     def synchronize(self) -> None:
         """Wait for every pending addition."""
@@ -227,8 +331,14 @@ class HostGradientAccumulator(MutableMapping):
             if self._closed:
                 return
             self._closed = True
+            for key in list(self._prefetched):
+                self._discard_prefetch(key)
             self._entries.clear()
             self._device_keys.clear()
+            self._end_of_step()
+            if self._streamer is not None:
+                streamer, self._streamer = self._streamer, None
+                _native.check("mo_streamer_destroy", self._lib.mo_streamer_destroy(streamer))
             if self._handle is not None:
                 handle, self._handle = self._handle, None
                 _native.check("mo_gradacc_destroy", self._lib.mo_gradacc_destroy(handle))

@@ -175,3 +175,30 @@ def test_host_entry_continued_by_a_device_gradient_and_dtype_errors() -> None:
     with pytest.raises(ValueError, match="changed size"):
         acc.accumulate("p", torch.zeros(5, device=DEV))
     acc.close()
+
+
+def test_pop_to_device_prefetches_in_first_contribution_order_and_is_exact() -> None:
+    acc = HostGradientAccumulator(DEV, slots=4, slot_bytes=1 << 20, prefetch=3)
+    shapes = [(17,), (300, 7), (1 << 18,), (64, 64), (5,), (2048, 33), (3,)]
+    for step in range(2):
+        grads = {k: [torch.randn(sh, device=DEV).to(torch.bfloat16) for _ in range(2)] for k, sh in enumerate(shapes)}
+        for rnd in range(2):
+            for k in grads:
+                acc.accumulate(k, grads[k][rnd])
+        order = list(grads) if step == 0 else [3, 0, 6, 1, 5, 2, 4]  # in order, then out of order
+        for i, k in enumerate(order):
+            got = acc.pop_to_device(k, DEV)
+            assert got.device == DEV and got.dtype == torch.float32 and got.shape == shapes[k]
+            assert torch.equal(_bits(got.cpu()), _bits(_oracle(grads[k])))
+            if step == 0 and i == 0:
+                assert len(acc._prefetched) == 3  # the next three entries are on their way
+        assert acc == {} and acc.pop_to_device(0) is None
+    # a prefetched entry that gets another contribution is re-read, not stale
+    a, b = torch.randn(1000, device=DEV), torch.randn(1000, device=DEV)
+    acc.accumulate("x", a)
+    acc.accumulate("y", a)
+    acc.pop_to_device("x")  # prefetches "y"
+    acc.accumulate("y", b)
+    assert torch.equal(_bits(acc.pop_to_device("y").cpu()), _bits(_oracle([a, b])))
+    acc.close()
+
