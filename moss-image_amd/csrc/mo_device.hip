@@ -114,13 +114,10 @@ __device__ __forceinline__ void st16_out(char* p, uint4 v) {
   else st16(p, v);
 }
 
+// One 16 KiB tile (`tile`, numbered within the launch) of piece `d`.
 template <bool kPack>
-__device__ __forceinline__ void copy_body(const LaunchArgs& args) {
+__device__ __forceinline__ void copy_tile(const KDesc& d, uint32_t tile) {
   __shared__ uint4 lds[kTileBytes / 16];
-  const uint32_t tile = blockIdx.x;
-  uint32_t i = 0;
-  while (i + 1 < args.ndesc && args.d[i + 1].tile0 <= tile) ++i;
-  const KDesc& d = args.d[i];
   const uint32_t tid = threadIdx.x;
   const uint64_t tile_off = (uint64_t)(tile - d.tile0) * kTileBytes;  // bytes into the piece
   const uint64_t left = d.nbytes - tile_off;
@@ -192,6 +189,15 @@ __device__ __forceinline__ void copy_body(const LaunchArgs& args) {
   }
 }
 
+// Several pieces: the workgroup finds its piece with a scalar search over the descriptors.
+template <bool kPack>
+__device__ __forceinline__ void copy_body(const LaunchArgs& args) {
+  const uint32_t tile = blockIdx.x;
+  uint32_t i = 0;
+  while (i + 1 < args.ndesc && args.d[i + 1].tile0 <= tile) ++i;
+  copy_tile<kPack>(args.d[i], tile);
+}
+
 }  // namespace mo
 
 extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_pack_kernel(const mo::LaunchArgs args) {
@@ -200,6 +206,17 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_pack_kernel(const 
 
 extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_unpack_kernel(const mo::LaunchArgs args) {
   mo::copy_body<false>(args);
+}
+
+// One piece (tile0 == 0): the same work with a single descriptor as the kernel argument, which
+// cuts the argument block a launch carries from sizeof(LaunchArgs) to sizeof(KDesc). Most
+// launches move one saved tensor.
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_pack1_kernel(const mo::KDesc d) {
+  mo::copy_tile<true>(d, blockIdx.x);
+}
+
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_unpack1_kernel(const mo::KDesc d) {
+  mo::copy_tile<false>(d, blockIdx.x);
 }
 
 // Device <-> pinned-host copy through the shader engines instead of a DMA engine.

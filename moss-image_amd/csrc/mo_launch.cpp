@@ -34,6 +34,7 @@ namespace {
 struct DeviceModule {
   hipModule_t module = nullptr;
   hipFunction_t pack = nullptr, unpack = nullptr, link = nullptr;
+  hipFunction_t pack1 = nullptr, unpack1 = nullptr;  // single-piece launches
 };
 
 std::mutex g_modules_mu;
@@ -45,12 +46,29 @@ int load_functions(DeviceModule& m) {
   if ((e = hipModuleGetFunction(&m.pack, m.module, "mo_pack_kernel")) != hipSuccess) return (int)e;
   if ((e = hipModuleGetFunction(&m.unpack, m.module, "mo_unpack_kernel")) != hipSuccess) return (int)e;
   if ((e = hipModuleGetFunction(&m.link, m.module, "mo_link_copy_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.pack1, m.module, "mo_pack1_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.unpack1, m.module, "mo_unpack1_kernel")) != hipSuccess) return (int)e;
   return 0;
 }
 
 }  // namespace
 
 // Kernels of the current device, loading the code object on first use.
+static int module_of_device(DeviceModule* out) {
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return (int)e;
+  std::lock_guard<std::mutex> lock(g_modules_mu);
+  auto it = g_modules.find(device);
+  if (it == g_modules.end()) {
+    DeviceModule m;
+    if (int rc = load_functions(m)) return rc;
+    it = g_modules.emplace(device, m).first;
+  }
+  *out = it->second;
+  return 0;
+}
+
 static int kernels(hipFunction_t* pack, hipFunction_t* unpack, hipFunction_t* link) {
   int device = 0;
   hipError_t e = hipGetDevice(&device);
@@ -166,11 +184,16 @@ void Launcher::add(const KDesc& kd) {
 int Launcher::flush() {
   if (args_.ndesc == 0) return 0;
   hipFunction_t fn = nullptr;
-  if (status_ == 0) status_ = pack_ ? kernels(&fn, nullptr, nullptr) : kernels(nullptr, &fn, nullptr);
+  const bool single = args_.ndesc == 1;  // tile0 == 0: the single-descriptor kernel
+  if (status_ == 0) {
+    DeviceModule m;
+    status_ = module_of_device(&m);
+    fn = single ? (pack_ ? m.pack1 : m.unpack1) : (pack_ ? m.pack : m.unpack);
+  }
   hipEvent_t t0 = nullptr, t1 = nullptr;
   if (status_ == 0 && timer_) status_ = timer_->events(&t0, &t1);
   if (status_ == 0) {
-    void* params[] = {&args_};
+    void* params[] = {single ? (void*)&args_.d[0] : (void*)&args_};
     // The extended launch takes the grid in work-items (tiles_ <= kMaxTilesPerLaunch + kMaxDesc,
     // so tiles_ * kThreads stays far below 2^32).
     const hipError_t e = t0 ? hipExtModuleLaunchKernel(fn, tiles_ * kThreads, 1, 1, kThreads, 1, 1, 0, stream_,
