@@ -146,8 +146,9 @@ def make_inputs(device, grid=GRID, text=TEXT_TOKENS, seed=0):
     return clean, noise, sigma, context
 
 
-def build_c5_model(device, layers: int):
-    """Config 5: config-3 dims with int8 weight-only joint-block bases and LoRA r16."""
+def build_c5_model(device, layers: int, int8_backend: str = "auto"):
+    """Config 5: config-3 dims with int8 weight-only joint-block bases and LoRA r16; the bases
+    run on ``int8_backend`` (auto: the HIP MFMA kernels, eager: decode + hipBLASLt)."""
 
     import torch
     from moss_offload import dit
@@ -160,6 +161,7 @@ def build_c5_model(device, layers: int):
     dit.init_weights(model, std=0.02)
     dit.quantize_joint_linears(model, torch.Generator(device=device).manual_seed(5))
     dit.inject_lora(model, rank=C5_RANK, alpha=float(C5_RANK), b_std=0.03)
+    dit.configure_quantized_backend(model, int8_backend)
     return model.train()
 
 
@@ -833,7 +835,7 @@ def run(args) -> dict:
             return model, opt, make_inputs(device, C4_GRID, C4_TEXT, seed=4), config3_forward, "A"
         if name in ("C5U", "C5P"):
             if not c5:
-                c5["model"] = build_c5_model(device, args.layers)
+                c5["model"] = build_c5_model(device, args.layers, args.int8_backend)
                 c5["opt"] = torch.optim.AdamW([p for p in c5["model"].parameters() if p.requires_grad], lr=1e-4,
                                               foreach=True)
                 c5["batch"] = make_c5_batch(device)
@@ -1026,6 +1028,8 @@ def main() -> int:
     parser.add_argument("--kernel-copy", action="store_true", help="copy kernel on HIP streams instead of SDMA")
     parser.add_argument("--cpu-threads", type=int, default=16)
     parser.add_argument("--gradacc-threads", type=int, default=12, help="host threads of the G leg's accumulator")
+    parser.add_argument("--int8-backend", default="auto", choices=("auto", "eager", "hip"),
+                        help="backend of config 5's int8 bases (auto = the HIP MFMA kernels when supported)")
     parser.add_argument("--cpu-budget", type=float, default=15.0)
     args = parser.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
