@@ -831,6 +831,8 @@ def run(args) -> dict:
 
         if name in ("A", "B"):
             return model, opt, inputs, config3_forward, name
+        if name == "BK":  # regime B with the engine keeping the last --keep-last-blocks blocks resident
+            return model, opt, inputs, config3_forward, "B"
         if name == "A4":
             return model, opt, make_inputs(device, C4_GRID, C4_TEXT, seed=4), config3_forward, "A"
         if name in ("C5U", "C5P"):
@@ -917,17 +919,24 @@ def run(args) -> dict:
             f"unique ({payload_copied / 1e9:.2f} GB as the reference copies it)")
         steps = args.steps if regime_name == "A" else max(1, args.steps_b)
         warmup = args.warmup if regime_name == "A" else max(1, args.warmup_b)
+        if regime_name == "BK":
+            entry_extra = {"keep_last_blocks": args.keep_last_blocks}
+        else:
+            entry_extra = {}
         block = [r for r in manifest.block if not r.resident]
         entry = {"payload_unique_bytes": payload_unique, "payload_copied_bytes": payload_copied,
                  "saves": len(manifest.records),
                  "block_payload_unique_bytes": sum(r.payload_bytes for r in block if r.dup_of is None),
-                 "block_payload_copied_bytes": sum(r.payload_bytes for r in block)}
+                 "block_payload_copied_bytes": sum(r.payload_bytes for r in block), **entry_extra}
         if regime_name == "B":
             entry["cpu_sample"] = manifest
         streamer = getattr(wl_model, "block_swap_manager", None)
         for mode in args.modes:
+            if regime_name == "BK" and mode == "reference":
+                continue  # the reference offloads every block
             configure_mode(wl_model, mode, regime)
             engine = get_engine(device)
+            engine.config.keep_last_blocks = args.keep_last_blocks if regime_name == "BK" else 0
             engine.reset_stats()
             if streamer is not None:
                 streamer.reset_stats()
@@ -1011,7 +1020,8 @@ def main() -> int:
     parser.add_argument("--warmup-b", type=int, default=1)
     parser.add_argument("--regimes", default="M,Q,A,B",
                         help="M = config-2 block microbench, Q = config-5 int8 GEMMs (HIP vs eager), "
-                        "A/B = config-3 steps (checkpointed / not), G = host gradient accumulation "
+                        "A/B = config-3 steps (checkpointed / not), BK = regime B keeping the last "
+                        "--keep-last-blocks blocks' saves resident, G = host gradient accumulation "
                         "(full-parameter config-3 dims, 2 micro-batches: device / engine / reference stash), "
                         "A4 = config 4 (2048^2, regime A), C5U/C5P = config 5 unpacked / packed (regime A), "
                         "S5 = config 5 packed with every block streamed from pinned host masters, "
@@ -1028,6 +1038,8 @@ def main() -> int:
     parser.add_argument("--kernel-copy", action="store_true", help="copy kernel on HIP streams instead of SDMA")
     parser.add_argument("--cpu-threads", type=int, default=16)
     parser.add_argument("--gradacc-threads", type=int, default=12, help="host threads of the G leg's accumulator")
+    parser.add_argument("--keep-last-blocks", type=int, default=16,
+                        help="BK leg: the engine keeps the saves of the last N blocks on the device")
     parser.add_argument("--int8-backend", default="auto", choices=("auto", "eager", "hip"),
                         help="backend of config 5's int8 bases (auto = the HIP MFMA kernels when supported)")
     parser.add_argument("--cpu-budget", type=float, default=15.0)

@@ -148,11 +148,19 @@ class _ActivationOffload:
         self._shared: set[int] = set()  # groups holding saves made more than once
         self._hooks = torch.autograd.graph.saved_tensors_hooks(self.pack, self.unpack)
         self._block_handles: list = []
+        # keep_last_blocks: block index of each layer, and the first index whose saves stay
+        self._layer_index: dict[int, int] = {}
+        self._keep_from: int | None = None
+        self._block: int | None = None  # the block running now (between its forward hooks)
 
     # ------------------------------------------------------------------ context
     def __enter__(self):
         layers = getattr(self.model, "layers", None)
         if isinstance(layers, (nn.ModuleList, nn.Sequential)):
+            keep = max(0, int(self.engine.config.keep_last_blocks))
+            if keep:
+                self._layer_index = {id(layer): i for i, layer in enumerate(layers)}
+                self._keep_from = len(layers) - keep
             for layer in layers:
                 self._block_handles.append(layer.register_forward_pre_hook(self._boundary))
                 self._block_handles.append(layer.register_forward_hook(self._boundary_post))
@@ -180,9 +188,11 @@ class _ActivationOffload:
 
     def _boundary(self, module, args):
         self.engine.commit(torch.cuda.current_stream(self.device).cuda_stream)
+        self._block = self._layer_index.get(id(module))
 
     def _boundary_post(self, module, args, output):
         self.engine.commit(torch.cuda.current_stream(self.device).cuda_stream)
+        self._block = None
 
     # ------------------------------------------------------------------ hooks
     def is_weight_backed(self, tensor: torch.Tensor) -> bool:
@@ -200,6 +210,8 @@ class _ActivationOffload:
     def pack(self, tensor: torch.Tensor):
         if tensor.device.type != "cuda" or tensor.layout != torch.strided or self.is_weight_backed(tensor):
             return tensor
+        if self._keep_from is not None and self._block is not None and self._block >= self._keep_from:
+            return tensor  # keep_last_blocks: needed first by backward
         view = _offload_view(tensor)
         if view is None or tensor.dim() > _native.MO_MAX_DIMS:
             return tensor

@@ -46,6 +46,11 @@ class EngineConfig:
     staged_restore: bool = True
     prefetch: bool = True
     dedupe: bool = True
+    # Saves made inside the last `keep_last_blocks` blocks of `model.layers` stay on the device
+    # (0: offload every block, as the reference does). Backward needs them first, so offloading
+    # them only sends them out and straight back; keeping them trades device memory for link
+    # time in both directions. Restores stay bitwise: a kept save is the saved tensor itself.
+    keep_last_blocks: int = 0
 
     def native(self) -> _native.MoConfig:
         cfg = _native.MoConfig()

@@ -263,3 +263,27 @@ def test_weight_backed_and_staging_buffers_stay_resident() -> None:
         assert ctx.pack(overlapping) is overlapping
         handle = ctx.pack(torch.randn(4, 0, device=device))
         assert isinstance(handle, _OffloadedTensor) and ctx.unpack(handle).shape == (4, 0)
+
+
+def test_keep_last_blocks_keeps_the_tail_resident_and_matches_no_offload() -> None:
+    device = torch.device("cuda", 0)
+    torch.manual_seed(911)
+    base = _tiny(layers=3, checkpointing=False).to(device).train()
+    latents, contexts = _inputs(device, seed=912)
+    expected = _run(copy.deepcopy(base), moss_offload.activation_cpu_offload, False, latents, contexts)
+    engine = moss_offload.get_engine(device)
+    packed = {}
+    try:
+        for keep in (0, 1, 3):
+            engine.config.keep_last_blocks = keep
+            engine.synchronize()
+            engine.reset_stats()
+            actual = _run(copy.deepcopy(base), moss_offload.activation_cpu_offload, True, latents, contexts)
+            engine.synchronize()
+            packed[keep] = engine.stats()["bytes_packed"]
+            _compare(actual, expected, rtol=5e-5, atol=5e-6)
+    finally:
+        engine.config.keep_last_blocks = 0
+    # one of three blocks kept: about a third less; every block kept: only the saves outside blocks
+    assert 0 < packed[1] < packed[0] and packed[3] < packed[1]
+    assert packed[1] <= packed[0] * 0.8
