@@ -76,6 +76,28 @@ def _offload_view(tensor: torch.Tensor) -> tuple[torch.Tensor, tuple[int, ...]] 
     return source, tuple(payload_shape)
 
 
+def _payload_key(source: torch.Tensor) -> tuple[int, tuple[tuple[int, int], ...], int]:
+    """The bytes a payload holds, independent of the view that names them.
+
+    ``(byte offset in the storage, ((size, byte stride), ...), element size)``: the dimensions
+    of size > 1 in storage order (decreasing stride), adjacent ones merged where the outer
+    stride equals the inner extent. Two views of one storage with equal keys have identical
+    payloads over the same bytes (a ``[1,H,T,hd]`` transposed view and the ``[1,T,D]`` view of
+    the same attention output, say), so one copy serves both.
+    """
+
+    es = source.element_size()
+    dims = sorted(((size, stride * es) for size, stride in zip(source.shape, source.stride()) if size > 1),
+                  key=lambda d: -d[1])
+    merged: list[tuple[int, int]] = []
+    for size, stride in dims:
+        if merged and merged[-1][1] == size * stride:
+            merged[-1] = (merged[-1][0] * size, stride)
+        else:
+            merged.append((size, stride))
+    return source.storage_offset() * es, tuple(merged), es
+
+
 def _restore_layout(
     payload: torch.Tensor,
     device: torch.device,
@@ -222,7 +244,9 @@ class _ActivationOffload:
             return _OffloadedTensor(None, None, 0, device, tensor.dtype, shape, stride, payload_shape)
         key = None
         if self.dedupe:
-            key = (tensor.untyped_storage().data_ptr(), source.storage_offset(), payload_shape, stride, tensor.dtype)
+            # by payload bytes, not by view: any view of the same bytes in the same storage order
+            # reuses the entry (unpack re-strides the restored storage to the asking view)
+            key = (tensor.untyped_storage().data_ptr(), _payload_key(source), tensor.dtype)
             hit = self._seen.get(key)
             if hit is not None:
                 ref, version, gid, idx = hit

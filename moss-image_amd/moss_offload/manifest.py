@@ -4,8 +4,9 @@ A ``saved_tensors_hooks`` probe (the instrument the reference's own tests use to
 ``training/tests/test_quantization.py:19-31``) that records, for every pack call, the shape,
 stride, dtype, storage identity and version, whether the reference rules would keep it
 resident (weight-backed, non-CUDA, or not offloadable, ``activation_offload.py:101-121``),
-its payload bytes after narrowing, and which earlier save it duplicates (same storage,
-offset, layout and version). The probe returns tensors unchanged, so the forward and
+its payload bytes after narrowing, and which earlier save it duplicates: same storage, dtype
+and version, and the same payload bytes (any view of them, as the engine's hook dedupes), or,
+for a save that stays resident, the same view. The probe returns tensors unchanged, so the forward and
 backward it observes are exactly the un-hooked ones.
 """
 
@@ -16,7 +17,7 @@ from dataclasses import dataclass
 import torch
 from torch import nn
 
-from .activation_offload import _offload_view, _storage_key
+from .activation_offload import _offload_view, _payload_key, _storage_key
 
 
 @dataclass
@@ -60,6 +61,7 @@ class ManifestRecorder:
         resident = ""
         payload_shape = None
         payload_bytes = 0
+        layout_key = (tensor.storage_offset(), tuple(tensor.shape), tuple(tensor.stride()))
         if tensor.device.type != self.device_type:
             resident = "device"
         elif _storage_key(tensor) in self._resident:
@@ -70,18 +72,12 @@ class ManifestRecorder:
                 resident = "layout"
             else:
                 payload_shape = view[1]
+                layout_key = _payload_key(view[0])
                 numel = 1
                 for size in payload_shape:
                     numel *= size
                 payload_bytes = numel * tensor.element_size()
-        key = (
-            tensor.untyped_storage().data_ptr(),
-            tensor.storage_offset(),
-            tuple(tensor.shape),
-            tuple(tensor.stride()),
-            tensor.dtype,
-            tensor._version,
-        )
+        key = (tensor.untyped_storage().data_ptr(), layout_key, tensor.dtype, tensor._version)
         dup_of = self._seen.get(key)
         index = len(self.records)
         if dup_of is None:
@@ -94,8 +90,8 @@ class ManifestRecorder:
                 tensor.dtype,
                 tensor.device.type,
                 key[0],
-                key[1],
-                key[5],
+                tensor.storage_offset(),
+                tensor._version,
                 payload_shape,
                 payload_bytes,
                 resident,

@@ -9,6 +9,9 @@
   with CPU payloads. Every restored tensor is bitwise equal to its save, and the loss and
   every gradient are bitwise equal to the run without hooks. The manifest probe records the
   same offloaded set the hooks packed.
+- The dedupe key of the engine's hook (``_payload_key``): equal for every view of the same
+  bytes (transposed, reshaped, expanded), different for a shifted, strided, partial or
+  same-size view of other bytes; the manifest counts aliasing views once.
 - The manifest probe lets the graph go when the forward is dropped (regression: a pack hook
   that returns its argument ties outputs saved by their own node into an uncollectable cycle).
 """
@@ -23,6 +26,7 @@ import torch
 
 import moss_offload
 from moss_offload import dit, engine
+from moss_offload.activation_offload import _offload_view, _payload_key
 from moss_offload.manifest import ManifestRecorder
 from oracle import reference_hooks
 
@@ -126,6 +130,50 @@ def test_manifest_matches_the_hooks_offloaded_set() -> None:
     # dup structure: fp32 RMSNorm saves its rsqrt statistic twice (square and mul)
     assert any(r.dup_of is not None for r in offloaded)
     assert probe.payload_bytes(unique=True) < probe.payload_bytes(unique=False)
+
+
+def _key(tensor):
+    return _payload_key(_offload_view(tensor)[0])
+
+
+def test_payload_key_names_bytes_not_views() -> None:
+    a = torch.randn(1, 7, 4, 5)
+    same = (a.view(1, 7, 20), a.permute(0, 2, 1, 3), a.view(7, 20).t(), a.unsqueeze(0), a.view(140))
+    assert all(_key(v) == _key(a) for v in same)
+    assert _key(a) == (0, ((140, 4),), 4)
+    other = (a[:, 1:], a[..., :4], a[:, ::2], a.view(35, 4)[:, :2], a.view(140)[1:], a.view(140)[:-1])
+    keys = {_key(v) for v in other}
+    assert _key(a) not in keys and len(keys) == len(other)
+    # expanded dimensions are narrowed before keying: a broadcast view names its source's bytes
+    c = torch.randn(2, 3)
+    assert _key(c[:, None, :].expand(2, 4, 3)) == _key(c)
+    # equal element counts at different positions
+    x = torch.randn(6, 8)
+    assert _key(x[:, :4]) != _key(x[:3])
+    # half of a [B,T,H,hd] tensor by head vs by token: same count, different bytes
+    y = torch.randn(2, 6, 4, 8)
+    assert _key(y[:, :, :2]) != _key(y[:, :3])
+
+
+def test_manifest_counts_aliasing_views_once() -> None:
+    class SavesViews(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x):
+            ctx.save_for_backward(x, x.view(x.shape[0], -1, 4, 8).transpose(1, 2), x.view(-1), x[:, 1:])
+            return x.clone()
+
+        @staticmethod
+        def backward(ctx, grad):
+            return grad
+
+    x = torch.randn(2, 6, 32) * 1.0
+    probe = ManifestRecorder(device_type="cpu")
+    with probe:
+        SavesViews.apply(x.requires_grad_())
+    offloaded = probe.offloaded()
+    assert len(offloaded) == 4
+    assert [r.dup_of for r in offloaded] == [None, offloaded[0].index, offloaded[0].index, None]
+    assert probe.payload_bytes(unique=True) == (x.numel() + x[:, 1:].numel()) * 4
 
 
 def _live_tensor_ids():

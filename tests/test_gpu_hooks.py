@@ -287,3 +287,49 @@ def test_keep_last_blocks_keeps_the_tail_resident_and_matches_no_offload() -> No
     # one of three blocks kept: about a third less; every block kept: only the saves outside blocks
     assert 0 < packed[1] < packed[0] and packed[3] < packed[1]
     assert packed[1] <= packed[0] * 0.8
+
+
+class _SavesAliasingViews(torch.autograd.Function):
+    """Saves three views of one storage (the same bytes in the same order) and one slice of
+    another region; backward reads every save through its own view."""
+
+    @staticmethod
+    def forward(ctx, x):
+        heads = x.view(x.shape[0], x.shape[1], 4, -1).permute(0, 2, 1, 3)  # [B,H,T,hd] over [B,T,D]
+        flat = x.view(-1, x.shape[-1])
+        tail = x[:, 1:]
+        ctx.save_for_backward(x, heads, flat, tail)
+        return x * 2.0
+
+    @staticmethod
+    def backward(ctx, grad):
+        x, heads, flat, tail = ctx.saved_tensors
+        assert heads.shape[1] == 4 and heads.stride() == (x.stride(0), x.shape[-1] // 4, x.stride(1), 1)
+        merged = heads.permute(0, 2, 1, 3).reshape(x.shape) + flat.view(x.shape) - x
+        out = grad * 2.0 + merged * 0.0
+        out[:, 1:] += tail * 0.0
+        return out + (merged - x).abs().sum() + (tail - x[:, 1:]).abs().sum()
+
+
+def test_views_of_the_same_bytes_cross_the_link_once() -> None:
+    """Dedupe by payload bytes: a transposed or reshaped view of an already offloaded tensor
+    reuses its host copy; a slice covering other bytes is copied on its own."""
+
+    device = torch.device("cuda", 0)
+    model = _tiny().to(device)
+    torch.manual_seed(913)
+    x = torch.randn(2, 24, 32, device=device, requires_grad=True)
+    base = x * 1.0
+    engine = moss_offload.get_engine(device)
+    engine.synchronize()
+    engine.reset_stats()
+    _Recording.log, _Recording.checked = {}, 0
+    with _Recording(model, device):
+        y = _SavesAliasingViews.apply(base)
+    engine.synchronize()
+    packed = engine.stats()["bytes_packed"]
+    element = base.element_size()
+    assert packed == base.numel() * element + base[:, 1:].numel() * element
+    y.sum().backward()
+    assert _Recording.checked == 4
+    torch.testing.assert_close(x.grad, torch.full_like(x, 2.0), rtol=0, atol=0)
