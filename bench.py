@@ -485,7 +485,8 @@ def calibration_copy(device, stream: int, repeats: int = 3) -> None:
     del buf
 
 
-def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: int, restore_slots: int):
+def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: int, restore_slots: int,
+          batch_packs: bool = True):
     """one regime-B block's saved set through pack -> D2H -> H2D -> unpack.
 
     Every iteration packs the block's tensors into one group (staging ring + SDMA D2H), commits
@@ -500,7 +501,7 @@ def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: 
 
     engine = OffloadEngine(device, EngineConfig(
         stage_slot_bytes=slot_mib << 20, stage_slots=stage_slots, restore_slots=restore_slots,
-        timing=True, kernel_timing=True, staged_restore=False, prefetch=False))
+        timing=True, kernel_timing=True, staged_restore=False, prefetch=False, batch_packs=batch_packs))
     stream = torch.cuda.current_stream(device).cuda_stream
     payload = sum(t.numel() * t.element_size() for t in tensors)
     storages = {}
@@ -782,6 +783,7 @@ def run(args) -> dict:
         stage_slot_bytes=args.slot_mib << 20,
         staged_restore=not args.no_staged_restore,
         kernel_copy=args.kernel_copy,
+        batch_packs=not args.eager_pack,
     )
     model = build_model(device, args.layers)
     inputs = make_inputs(device)
@@ -808,7 +810,7 @@ def run(args) -> dict:
         payload = sum(t.numel() * t.element_size() for t in tensors)
         log(f"micro: one regime-B block, {len(tensors)} unique saves, {payload / 1e6:.1f} MB")
         result["micro"] = micro(device, tensors, args.micro_iters, args.micro_warmup, args.slot_mib,
-                                args.stage_slots, args.restore_slots)
+                                args.stage_slots, args.restore_slots, batch_packs=not args.eager_pack)
         m = result["micro"]
         log(f"micro: {m['s_per_iter'] * 1e3:.2f} ms/iter, D2H {m['d2h_gbps']:.1f} GB/s, H2D {m['h2d_gbps']:.1f} GB/s, "
             f"pack {m['pack_hbm_gbps']:.0f} GB/s ({m['pack_avg_launch_us']:.1f} us/launch), unpack "
@@ -972,7 +974,12 @@ def run(args) -> dict:
                 engine.synchronize()
                 st = engine.stats()
                 n = steps + warmup  # reset before warmup: stats cover warmup + timed steps
+                # the staging and restore rings are the engine's own hipMalloc, outside torch's
+                # allocator and so outside peak_device_bytes
+                rings = (engine.config.stage_slots + engine.config.restore_slots) * engine.config.stage_slot_bytes
                 record.update(
+                    engine_ring_bytes=rings,
+                    peak_device_bytes_with_rings=peak + rings,
                     d2h_bytes_per_step=st["bytes_d2h"] / n,
                     h2d_bytes_per_step=st["bytes_h2d"] / n,
                     d2h_s_per_step=st["d2h_ms"] / 1e3 / n,
@@ -1033,8 +1040,10 @@ def main() -> int:
     parser.add_argument("--no-parity", action="store_true")
     parser.add_argument("--stage-slots", type=int, default=4)
     parser.add_argument("--restore-slots", type=int, default=4)
-    parser.add_argument("--slot-mib", type=int, default=64)
+    parser.add_argument("--slot-mib", type=int, default=128)
     parser.add_argument("--no-staged-restore", action="store_true")
+    parser.add_argument("--eager-pack", action="store_true",
+                        help="one gather launch per save instead of one per staging segment")
     parser.add_argument("--kernel-copy", action="store_true", help="copy kernel on HIP streams instead of SDMA")
     parser.add_argument("--cpu-threads", type=int, default=16)
     parser.add_argument("--gradacc-threads", type=int, default=12, help="host threads of the G leg's accumulator")

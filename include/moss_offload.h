@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 5
+#define MO_ABI_VERSION 6
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -49,6 +49,8 @@ extern "C" {
 #define MO_FLAG_KERNEL_TIMING 0x4  /* time every pack/unpack launch with HIP events       */
 #define MO_FLAG_NO_STAGED_RESTORE 0x8 /* always restore through H2D, even when a segment is
                                          still intact in its staging slot                  */
+#define MO_FLAG_EAGER_PACK 0x10    /* launch each mo_pack call's gather kernels before it
+                                      returns instead of batching them per segment        */
 
 /*
  * A strided tensor view on the device. `ptr` is the address of logical element (0,...,0),
@@ -66,7 +68,7 @@ typedef struct mo_tensor {
 
 /* Engine configuration (mo_create). Zero fields take the defaults in brackets. */
 typedef struct mo_config {
-  uint64_t stage_slot_bytes;    /* [64 MiB] device staging slot size (forward arena)   */
+  uint64_t stage_slot_bytes;    /* [128 MiB] device staging and restore slot size      */
   uint32_t stage_slots;         /* [4] slots in the forward staging ring               */
   uint32_t restore_slots;       /* [4] slots in the backward restore ring              */
   uint64_t host_limit_bytes;    /* [0 = no limit] cap on pinned host memory             */
@@ -140,8 +142,23 @@ int mo_destroy(mo_engine* engine);
 
 /* Pack n saved tensors into the open group (a new group opens if none is). Each tensor is
  * gathered into the staging ring on `stream` and refs[i] says where it went. Replaces
- * pack(), activation_offload.py:116-134. */
+ * pack(), activation_offload.py:116-134.
+ *
+ * The gather kernels of consecutive calls on one stream are batched: they are launched, in
+ * stream order, as one kernel per staging segment when the segment closes (its slot fills, or
+ * mo_commit / mo_unpack of the group closes it), before a call on another stream, and at
+ * mo_synchronize or mo_pack_flush. The caller therefore keeps the memory of every tensor it
+ * passed valid (not freed, not written) until mo_pack_progress reports the call as launched;
+ * after that the usual stream-ordered reuse applies. MO_FLAG_EAGER_PACK launches every call's
+ * kernels before it returns. Releasing the open group drops its gathers not yet launched. */
 int mo_pack(mo_engine* engine, const mo_tensor* tensors, int n, uint64_t stream, mo_ref* refs);
+
+/* *calls = mo_pack calls made so far; every call numbered (from 1) at most *launched has all
+ * of its gather kernels enqueued. No reference counterpart: the reference copies at once. */
+int mo_pack_progress(mo_engine* engine, uint64_t* calls, uint64_t* launched);
+
+/* Launch every pending gather kernel now (on the stream of the calls that made them). */
+int mo_pack_flush(mo_engine* engine);
 
 /* Close the open group: the compute stream records an event, the D2H stream waits for it and
  * streams the group's staging segments into pinned host memory. *group receives the id

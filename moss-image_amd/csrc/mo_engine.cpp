@@ -329,6 +329,44 @@ struct Engine {
     }
   };
 
+  // ---- batched pack launches ----
+  // Gather descriptors of consecutive mo_pack calls on one stream wait here and go out as one
+  // launch when the open segment closes (before its D2H is issued), when a call comes on
+  // another stream, or on synchronize / mo_pack_flush. The caller keeps each call's sources
+  // valid until pack_launched reaches the call's number (mo_pack_progress).
+  KernelTimer pack_timer{this, true};
+  std::unique_ptr<Launcher> pend;
+  hipStream_t pend_stream = nullptr;
+  uint64_t pack_calls = 0;     // mo_pack calls so far (1-based numbers)
+  uint64_t pack_launched = 0;  // every call numbered <= this has all its kernels enqueued
+  bool in_pack = false;        // a flush inside a call leaves that call's later pieces pending
+
+  int flush_packs() {
+    if (pend) {
+      const int rc = pend->flush();
+      st.pack_launches += pend->launches();
+      pend.reset();
+      if (rc) return hip_fail(rc, "pack kernel launch");
+    }
+    pack_launched = in_pack ? pack_calls - 1 : pack_calls;
+    return 0;
+  }
+
+  // The open group is released before its D2H: its pending gathers never need to run.
+  void discard_packs() {
+    if (pend) st.pack_launches += pend->launches();
+    pend.reset();
+    pack_launched = pack_calls;
+  }
+
+  Launcher& pack_launcher(hipStream_t stream) {
+    if (!pend) {
+      pend.reset(new Launcher(true, stream, &pack_timer));
+      pend_stream = stream;
+    }
+    return *pend;
+  }
+
   void process_timings(bool wait) {
     while (!timings.empty()) {
       Timing& t = timings.front();
@@ -385,9 +423,9 @@ struct Engine {
   }
 
   // ---- forward ----
-  int close_segment(Launcher& L, hipStream_t stream) {
+  int close_segment(hipStream_t stream) {
     if (!open_group || open_seg < 0) return 0;
-    if (int rc = L.flush()) return hip_fail(rc, "pack kernel launch");
+    if (int rc = flush_packs()) return rc;
     Segment& seg = open_group->segs[open_seg];
     StageSlot& slot = stage[seg.stage_slot];
     seg.bytes = slot.used - seg.stage_off;
@@ -436,8 +474,21 @@ struct Engine {
       st.groups_created++;
     }
     Group& g = *open_group;
-    KernelTimer timer(this, true);
-    Launcher L(true, stream, &timer);
+    if (pend && pend_stream != stream)
+      if (int rc = flush_packs()) return rc;
+    ++pack_calls;
+    in_pack = true;
+    const int rc = pack_into(g, canons, stream, refs);
+    in_pack = false;
+    if (rc) return rc;
+    if (cfg.flags & MO_FLAG_EAGER_PACK) return flush_packs();
+    if (!pend) pack_launched = pack_calls;  // nothing of this call is pending
+    return 0;
+  }
+
+  int pack_into(Group& g, const std::vector<Canon>& canons, hipStream_t stream, mo_ref* refs) {
+    std::string err;
+    const int n = (int)canons.size();
     const uint64_t slot_bytes = cfg.stage_slot_bytes;
     for (int i = 0; i < n; ++i) {
       const Canon& c = canons[i];
@@ -453,7 +504,7 @@ struct Engine {
         const uint64_t pos = align_up(s.used, kPayloadAlign);
         const uint64_t space = pos < slot_bytes ? slot_bytes - pos : 0;
         if (space == 0 || (space < remaining && space < kMinPiece)) {
-          if (int rc = close_segment(L, stream)) return rc;
+          if (int rc = close_segment(stream)) return rc;
           if (int rc = advance_slot(stream)) return rc;
           continue;
         }
@@ -473,7 +524,11 @@ struct Engine {
         KDesc kd;
         if (int rc = make_kdesc(c, c.base, first, take, (uint64_t)(s.dev + pos), kd, err))
           return fail(rc, "mo_pack: " + err);
+        if (pend && pend->full())  // launch through flush_packs so pack_launched stays exact
+          if (int rc = flush_packs()) return rc;
+        Launcher& L = pack_launcher(stream);
         L.add(kd);
+        if (L.status()) return hip_fail(L.status(), "pack kernel launch");
         seg.pieces.push_back(Piece{idx, first, take, pos - seg.stage_off});
         s.used = pos + take;
         first += take;
@@ -481,16 +536,14 @@ struct Engine {
         st.bytes_packed += take;
       }
     }
-    if (int rc = L.flush()) return hip_fail(rc, "pack kernel launch");
-    st.pack_launches += L.launches();
     return 0;
   }
 
   int commit(hipStream_t stream, uint64_t* gid) {
     *gid = kNone;
-    if (!open_group) return 0;
-    Launcher L(true, stream);
-    if (int rc = close_segment(L, stream)) return rc;
+    if (!open_group) return flush_packs();
+    if (int rc = close_segment(stream)) return rc;
+    if (int rc = flush_packs()) return rc;  // a group with no segment yet
     open_group->open = false;
     *gid = open_group->id;
     open_group = nullptr;
@@ -646,7 +699,9 @@ struct Engine {
     Group* g = find(gid);
     if (!g) return fail(MO_E_INVALID, "mo_release: unknown group " + std::to_string(gid));
     if (g == open_group) {
-      // Pack kernels were enqueued but no D2H: abandon the staging space.
+      // No D2H was issued: abandon the staging space and the gathers not launched yet
+      // (their sources may be freed as soon as this returns).
+      discard_packs();
       open_group = nullptr;
       open_seg = -1;
     }
@@ -665,6 +720,7 @@ struct Engine {
   }
 
   int synchronize() {
+    if (int rc = flush_packs()) return rc;
     MO_LINK(link->synchronize());
     if (int rc = process_pending(true)) return rc;
     process_timings(true);
@@ -701,7 +757,7 @@ struct Engine {
   int init(int dev, const mo_config* c) {
     device = dev;
     if (c) cfg = *c;
-    if (!cfg.stage_slot_bytes) cfg.stage_slot_bytes = 64ull << 20;
+    if (!cfg.stage_slot_bytes) cfg.stage_slot_bytes = 128ull << 20;
     if (!cfg.stage_slots) cfg.stage_slots = 4;
     if (!cfg.restore_slots) cfg.restore_slots = 4;
     if (!cfg.host_chunk_bytes) cfg.host_chunk_bytes = 1ull << 30;
@@ -738,6 +794,7 @@ struct Engine {
     DeviceGuard guard(device);
     // Drain the link first: compute streams may wait on copies that are still queued.
     if (link) (void)link->synchronize();
+    discard_packs();
     (void)hipDeviceSynchronize();
     groups.clear();
     (void)process_pending(true);
@@ -905,6 +962,13 @@ int mo_pack(mo_engine* engine, const mo_tensor* tensors, int n, uint64_t stream,
   if (n < 0 || (n > 0 && (!tensors || !refs))) return mo::fail(MO_E_INVALID, "mo_pack: bad arguments");
   MO_ENGINE_CALL(engine, engine->e.pack(tensors, n, (hipStream_t)stream, refs));
 }
+
+int mo_pack_progress(mo_engine* engine, uint64_t* calls, uint64_t* launched) {
+  if (!calls || !launched) return mo::fail(MO_E_INVALID, "mo_pack_progress: null output");
+  MO_ENGINE_CALL(engine, (*calls = engine->e.pack_calls, *launched = engine->e.pack_launched, 0));
+}
+
+int mo_pack_flush(mo_engine* engine) { MO_ENGINE_CALL(engine, engine->e.flush_packs()); }
 
 int mo_commit(mo_engine* engine, uint64_t stream, uint64_t* group) {
   if (!group) return mo::fail(MO_E_INVALID, "mo_commit: null output");

@@ -34,6 +34,7 @@ class Launcher {
   int status() const { return status_; }
   uint64_t launches() const { return launches_; }
   uint64_t bytes() const { return bytes_; }
+  bool full() const { return args_.ndesc == (uint32_t)kMaxDesc; }  // the next add launches
 
  private:
   bool pack_;

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 5
+MO_ABI_VERSION = 6
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -27,6 +27,7 @@ MO_FLAG_TIMING = 0x1
 MO_FLAG_KERNEL_COPY = 0x2
 MO_FLAG_KERNEL_TIMING = 0x4
 MO_FLAG_NO_STAGED_RESTORE = 0x8
+MO_FLAG_EAGER_PACK = 0x10
 
 NO_GROUP = (1 << 64) - 1
 
@@ -167,6 +168,8 @@ SIGNATURES: dict[str, tuple] = {
     "mo_create": (ctypes.c_int, [ctypes.c_int, _P(MoConfig), _P(ctypes.c_void_p)]),
     "mo_destroy": (ctypes.c_int, [ctypes.c_void_p]),
     "mo_pack": (ctypes.c_int, [ctypes.c_void_p, _P(MoTensor), ctypes.c_int, _u64, _P(MoRef)]),
+    "mo_pack_progress": (ctypes.c_int, [ctypes.c_void_p, _P(_u64), _P(_u64)]),
+    "mo_pack_flush": (ctypes.c_int, [ctypes.c_void_p]),
     "mo_commit": (ctypes.c_int, [ctypes.c_void_p, _u64, _P(_u64)]),
     "mo_prefetch": (ctypes.c_int, [ctypes.c_void_p, _u64, _u64]),
     "mo_unpack": (ctypes.c_int, [ctypes.c_void_p, _u64, _P(_u64), ctypes.c_uint32, _u64]),

@@ -21,6 +21,7 @@ import atexit
 import bisect
 import ctypes
 import threading
+from collections import deque
 from dataclasses import dataclass, fields
 
 import torch
@@ -32,7 +33,7 @@ from . import _native
 class EngineConfig:
     """Sizes and switches of one device engine (see ``mo_config`` in moss_offload.h)."""
 
-    stage_slot_bytes: int = 64 << 20
+    stage_slot_bytes: int = 128 << 20
     stage_slots: int = 4
     restore_slots: int = 4
     host_limit_bytes: int = 0
@@ -46,6 +47,11 @@ class EngineConfig:
     staged_restore: bool = True
     prefetch: bool = True
     dedupe: bool = True
+    # Gather kernels of consecutive saves are launched together, one kernel per staging segment
+    # when it closes (before its D2H), instead of one per save: fewer, larger launches that run
+    # nearer the HBM copy rate. The engine keeps each save's source tensor alive until its
+    # kernel is launched (at most one staging slot of saves). False: launch at every save.
+    batch_packs: bool = True
     # Saves made inside the last `keep_last_blocks` blocks of `model.layers` stay on the device
     # (0: offload every block, as the reference does). Backward needs them first, so offloading
     # them only sends them out and straight back; keeping them trades device memory for link
@@ -64,6 +70,7 @@ class EngineConfig:
             | (_native.MO_FLAG_KERNEL_COPY if self.kernel_copy else 0)
             | (_native.MO_FLAG_KERNEL_TIMING if self.kernel_timing else 0)
             | (0 if self.staged_restore else _native.MO_FLAG_NO_STAGED_RESTORE)
+            | (0 if self.batch_packs else _native.MO_FLAG_EAGER_PACK)
         )
         cfg.copy_kernel_blocks = self.copy_kernel_blocks
         cfg.d2h_engine = self.d2h_engine
@@ -114,6 +121,11 @@ class OffloadEngine:
         self._desc = (_native.MoTensor * 1)()
         self._ref = (_native.MoRef * 1)()
         self._gid_out = ctypes.c_uint64()
+        # sources of gathers not launched yet, as (pack call number, tensor, its version at the
+        # save), oldest first
+        self._held: deque[tuple[int, torch.Tensor, int]] = deque()
+        self._calls = ctypes.c_uint64()
+        self._launched = ctypes.c_uint64()
 
     # ------------------------------------------------------------------ forward
     def pack(self, source: torch.Tensor, stream: int) -> tuple[int, int]:
@@ -122,6 +134,8 @@ class OffloadEngine:
         with self._lock:
             _native.describe(source, self._desc[0])
             _native.check("mo_pack", self._lib.mo_pack(self._handle, self._desc, 1, stream, self._ref))
+            if self.config.batch_packs:
+                self._hold(source)
             gid, idx = int(self._ref[0].group), int(self._ref[0].entry)
             group = self._groups.get(gid)
             if group is None:
@@ -142,12 +156,12 @@ class OffloadEngine:
         with self._lock:
             _native.check("mo_commit", self._lib.mo_commit(self._handle, stream, ctypes.byref(self._gid_out)))
             gid = int(self._gid_out.value)
-            if gid == _native.NO_GROUP:
-                return None
             group = self._groups.get(gid)
             if group is not None:
                 group.committed = True
-            return gid
+            if self._held:
+                self._hold()
+            return None if gid == _native.NO_GROUP else gid
 
     def acquire(self, gid: int, idx: int) -> bool:
         """Add a reference to a live entry (a deduplicated save). False if it is gone."""
@@ -178,6 +192,41 @@ class OffloadEngine:
                 if pos < len(self._live) and self._live[pos] == gid:
                     del self._live[pos]
                 _native.check("mo_release", self._lib.mo_release(self._handle, gid))
+                if self._held:
+                    self._hold()
+
+    def _hold(self, source: torch.Tensor | None = None) -> None:
+        """Keep ``source`` (of the pack call just made) alive while its gather is pending, and
+        let go of the sources whose gathers the engine has launched. Launched kernels are
+        stream-ordered before anything that later reuses their memory.
+
+        A pending gather reads its source when it is launched, not at the save. A source that
+        was modified in place in between (its version counter moved: autograd's own test of a
+        saved tensor, which it skips while saved-tensor hooks are installed) would be offloaded
+        with its new bytes, where a copy at the save keeps the old ones. That raises here: the
+        same program without offloading fails autograd's check in backward, and
+        ``batch_packs=False`` copies at the save."""
+
+        _native.check("mo_pack_progress", self._lib.mo_pack_progress(
+            self._handle, ctypes.byref(self._calls), ctypes.byref(self._launched)))
+        if source is not None and self._calls.value > self._launched.value:
+            self._held.append((self._calls.value, source, source._version))
+        launched = self._launched.value
+        while self._held and self._held[0][0] <= launched:
+            _, tensor, version = self._held.popleft()
+            if tensor._version != version:
+                raise RuntimeError(
+                    "a tensor saved for backward was modified in place before the offload engine "
+                    "gathered it (autograd would reject this without offloading); "
+                    "use moss_offload.configure(batch_packs=False) to copy every save at once")
+
+    def flush(self) -> None:
+        """Launch every pending gather kernel now."""
+
+        with self._lock:
+            _native.check("mo_pack_flush", self._lib.mo_pack_flush(self._handle))
+            if self._held:
+                self._hold()
 
     # ------------------------------------------------------------------ backward
     def restore(self, gid: int, idx: int, stream: int) -> torch.Tensor:
@@ -202,6 +251,8 @@ class OffloadEngine:
                 if other.nbytes:
                     dst[j] = tensor.data_ptr()
             _native.check("mo_unpack", self._lib.mo_unpack(self._handle, gid, dst, n, stream))
+            if self._held:  # unpacking the open group commits it
+                self._hold()
             if self.config.prefetch:
                 nxt = self._predict_next(gid)
                 if nxt is not None:
@@ -243,6 +294,8 @@ class OffloadEngine:
     def synchronize(self) -> None:
         with self._lock:
             _native.check("mo_synchronize", self._lib.mo_synchronize(self._handle))
+            if self._held:
+                self._hold()
 
     def stats(self) -> dict:
         with self._lock:
@@ -273,6 +326,7 @@ class OffloadEngine:
             if self._handle:
                 _native.check("mo_destroy", self._lib.mo_destroy(self._handle))
                 self._handle = ctypes.c_void_p()
+                self._held.clear()
                 self._groups.clear()
                 self._live.clear()
 

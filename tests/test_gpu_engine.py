@@ -146,3 +146,132 @@ def test_host_limit_raises_clear_error() -> None:
             engine.commit(stream)
     torch.cuda.synchronize(device)
     engine.close()
+
+
+def _scribble_like(t: torch.Tensor) -> None:
+    """Allocate and fill a tensor the size of ``t``'s storage: if ``t``'s memory had been
+    returned to the caching allocator, this would overwrite it."""
+
+    torch.full((t.untyped_storage().nbytes() // 4 + 1,), -7.0, device=t.device)
+
+
+@pytest.mark.parametrize("batch", [True, False])
+def test_batched_packs_keep_freed_sources_until_launched(batch) -> None:
+    """Saves whose only reference is dropped right after mo_pack: their gathers may still be
+    pending, so the engine must keep them alive; the restores are bitwise either way, and
+    batching launches fewer kernels for the same saves."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine(batch_packs=batch)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    rng = random.Random(11)
+    handles, expected = [], []
+    pending_seen = 0
+    for g in range(4):
+        for t in _tensors(rng, 10, device, big=g % 2 == 0):
+            expected.append((t.clone(), t.stride()))
+            gid, idx = engine.pack(t, stream)
+            handles.append((gid, idx))
+            pending_seen = max(pending_seen, len(engine._held))
+            del t
+            _scribble_like(expected[-1][0])
+        engine.commit(stream)
+        assert not engine._held  # a commit launches every pending gather
+    assert (pending_seen > 0) == batch
+    for (gid, idx), (original, stride) in reversed(list(zip(handles, expected))):
+        restored = engine.restore(gid, idx, stream)
+        assert restored.stride() == stride
+        assert_bitwise(restored, original)
+    stats = engine.stats()
+    launches = stats["pack_launches"]
+    assert stats["bytes_unpacked"] == stats["bytes_packed"]
+    for gid, idx in handles:
+        engine.drop(gid, idx)
+    engine.synchronize()
+    assert engine.stats()["host_bytes_in_use"] == 0
+    engine.close()
+    if batch:
+        assert launches < len(handles)
+    else:
+        assert launches >= len(handles)
+
+
+def test_batched_packs_on_two_streams() -> None:
+    """A pack on another stream launches the pending gathers of the first stream first."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine()
+    main = torch.cuda.current_stream(device)
+    side = torch.cuda.Stream(device)
+    rng = random.Random(12)
+    tensors = _tensors(rng, 12, device, big=False)
+    side.wait_stream(main)
+    handles = []
+    for k, t in enumerate(tensors):
+        stream = side if k % 3 == 2 else main
+        with torch.cuda.stream(stream):
+            handles.append(engine.pack(t, stream.cuda_stream))
+            t.record_stream(stream)
+    main.wait_stream(side)
+    engine.commit(main.cuda_stream)
+    assert not engine._held
+    for (gid, idx), original in reversed(list(zip(handles, tensors))):
+        assert_bitwise(engine.restore(gid, idx, main.cuda_stream), original)
+    for gid, idx in handles:
+        engine.drop(gid, idx)
+    engine.synchronize()
+    engine.close()
+
+
+def test_release_of_the_open_group_drops_pending_gathers() -> None:
+    device = torch.device("cuda", 0)
+    engine = _engine()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    small = [torch.randn(1000 + k, device=device) for k in range(5)]
+    handles = [engine.pack(t, stream) for t in small]
+    assert len(engine._held) == 5
+    for gid, idx in handles:
+        engine.drop(gid, idx)
+    assert not engine._held and engine.live_groups() == 0
+    assert engine.stats()["pack_launches"] == 0  # nothing was launched for the abandoned group
+    # the engine carries on: a new group packs, commits and restores
+    t = torch.randn(3000, 7, device=device)
+    gid, idx = engine.pack(t, stream)
+    engine.commit(stream)
+    assert_bitwise(engine.restore(gid, idx, stream), t)
+    engine.drop(gid, idx)
+    engine.synchronize()
+    assert engine.stats()["host_bytes_in_use"] == 0
+    engine.close()
+
+
+@pytest.mark.parametrize("batch", [True, False])
+def test_save_modified_in_place_before_its_gather(batch) -> None:
+    """Saved-tensor hooks switch off autograd's version check, so a save modified in place
+    afterwards still reaches backward. Copying at the save keeps the bytes of the save; a
+    batched gather not launched yet would read the new bytes, and raises instead."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine(batch_packs=batch)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    t = torch.randn(4096, device=device)
+    saved = t.clone()
+    gid, idx = engine.pack(t, stream)
+    t.mul_(2.0)
+    if batch:
+        with pytest.raises(RuntimeError, match="modified in place"):
+            engine.commit(stream)
+    else:
+        engine.commit(stream)
+        assert_bitwise(engine.restore(gid, idx, stream), saved)
+    # a modification after the commit (the gather is launched) is no longer the engine's concern
+    u = torch.randn(4096, device=device)
+    gid2, idx2 = engine.pack(u, stream)
+    engine.commit(stream)
+    expected = u.clone()
+    u.mul_(3.0)
+    assert_bitwise(engine.restore(gid2, idx2, stream), expected)
+    engine.drop(gid, idx)
+    engine.drop(gid2, idx2)
+    engine.synchronize()
+    engine.close()
