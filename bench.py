@@ -784,6 +784,7 @@ def run(args) -> dict:
         staged_restore=not args.no_staged_restore,
         kernel_copy=args.kernel_copy,
         batch_packs=not args.eager_pack,
+        d2h_engine=args.d2h_engine,
     )
     model = build_model(device, args.layers)
     inputs = make_inputs(device)
@@ -982,6 +983,8 @@ def run(args) -> dict:
                     peak_device_bytes_with_rings=peak + rings,
                     d2h_bytes_per_step=st["bytes_d2h"] / n,
                     h2d_bytes_per_step=st["bytes_h2d"] / n,
+                    d2h_copies_per_step=st["d2h_copies"] / n,
+                    h2d_copies_per_step=st["h2d_copies"] / n,
                     d2h_s_per_step=st["d2h_ms"] / 1e3 / n,
                     h2d_s_per_step=st["h2d_ms"] / 1e3 / n,
                     d2h_gbps=st["timed_d2h_bytes"] / max(st["d2h_ms"], 1e-9) / 1e6,
@@ -1042,6 +1045,8 @@ def main() -> int:
     parser.add_argument("--restore-slots", type=int, default=4)
     parser.add_argument("--slot-mib", type=int, default=128)
     parser.add_argument("--no-staged-restore", action="store_true")
+    parser.add_argument("--d2h-engine", type=lambda v: int(v, 0), default=0,
+                        help="SDMA engine bits for D2H (0: two engines, copies split in halves)")
     parser.add_argument("--eager-pack", action="store_true",
                         help="one gather launch per save instead of one per staging segment")
     parser.add_argument("--kernel-copy", action="store_true", help="copy kernel on HIP streams instead of SDMA")

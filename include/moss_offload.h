@@ -75,8 +75,11 @@ typedef struct mo_config {
   uint64_t host_chunk_bytes;    /* [1 GiB] granularity of hipHostMalloc reservations   */
   uint32_t flags;               /* MO_FLAG_*                                          */
   uint32_t copy_kernel_blocks;  /* [16] workgroups of the copy kernel (KERNEL_COPY)  */
-  uint32_t d2h_engine;          /* [0 = first available] SDMA engine bit for D2H      */
-  uint32_t h2d_engine;          /* [0 = first available other than D2H's] for H2D     */
+  uint32_t d2h_engine;          /* [0 = the two lowest available] SDMA engine bits for
+                                   D2H; with two, a copy of 2 MiB or more is split in
+                                   halves, one per engine                              */
+  uint32_t h2d_engine;          /* [0 = the lowest available not used by D2H] SDMA
+                                   engine bits for H2D (two bits: split the same way)  */
 } mo_config;
 
 /* Where one packed tensor lives: its group (one block's saves) and index in the group. */
@@ -220,8 +223,8 @@ typedef struct mo_streamer_stats {
 } mo_streamer_stats;
 
 /* A streamer with `slots` device staging slots (the buffers themselves belong to the caller)
- * and its own SDMA queues (h2d_engine: SDMA engine bit for fills, 0 = first available other than
- * the write-back engine). Replaces the copy stream and slot events of AsyncBlockStreamer
+ * and its own SDMA queues (h2d_engine: SDMA engine bits for fills, 0 = the lowest available
+ * other than the two write-back engines; with two bits, copies of 2 MiB or more are split). Replaces the copy stream and slot events of AsyncBlockStreamer
  * (memory.py:109-119) and TrainableBlockStreamer (trainable_offload.py:128-179). */
 int mo_streamer_create(int device, uint32_t slots, uint32_t h2d_engine, mo_streamer** out);
 int mo_streamer_destroy(mo_streamer* streamer);
@@ -288,7 +291,8 @@ typedef struct mo_gradacc_stats {
 } mo_gradacc_stats;
 
 /* An accumulator on `device`: `slots` device staging slots of `slot_bytes` (a multiple of 4096)
- * each with a pinned host twin, an SDMA D2H link on engine `d2h_engine`, and `host_threads`
+ * each with a pinned host twin, an SDMA D2H link on engines `d2h_engine` (bits, 0 = the two
+ * lowest available; copies of 2 MiB or more are split across two), and `host_threads`
  * threads for the host additions. Replaces the blocking pinned copy of
  * FusedAdafactor._stash_gradient_on_host (fused_adafactor.py:337-346). */
 int mo_gradacc_create(int device, uint32_t slots, uint64_t slot_bytes, uint32_t host_threads, uint32_t d2h_engine,

@@ -31,6 +31,11 @@ int64_t now_ns() {
 
 constexpr int64_t kWaitLimitNs = 300ll * 1000000000ll;  // a copy that takes longer is reported as failed
 
+// H2D copies enqueued and not finished per device, over every SDMA link of the process
+// (engine, streamer).
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_h2d_inflight[kMaxDevices];
+
 // Short polling sleep. The default 50 us timer slack of a Linux thread would dominate a 5 us
 // sleep, so each polling thread lowers its own slack once.
 void short_sleep() {
@@ -66,6 +71,9 @@ struct SdmaCopy : CopyState {
   bool to_host = true;
   uint64_t bytes = 0;
   int64_t issue_ns = 0;
+  int parts_left = 0;        // halves still in flight (worker thread only)
+  bool counted_h2d = false;  // counted in g_h2d_inflight until finished
+  bool part_failed = false;  // a half failed or timed out (worker thread only)
   bool done() const override { return finished.load(std::memory_order_acquire); }
   bool failed() const override { return fail.load(std::memory_order_acquire); }
 };
@@ -159,8 +167,10 @@ class SdmaLink : public Link {
       err = "no SDMA engine available between host and device";
       return MO_E_STATE;
     }
-    e_d2h_ = pick(d2h_mask, d2h_engine, 0);
-    e_h2d_ = pick(h2d_mask, h2d_engine, e_d2h_);
+    n_d2h_ = pick(d2h_mask, d2h_engine, 0, 2, e_d2h_);
+    uint32_t taken = 0;
+    for (int i = 0; i < n_d2h_; ++i) taken |= e_d2h_[i];
+    n_h2d_ = pick(h2d_mask, h2d_engine, taken, 1, e_h2d_);
     worker_ = std::thread([this] { run(); });
     return 0;
   }
@@ -191,6 +201,8 @@ class SdmaLink : public Link {
 
   int h2d(void* dst, const void* src, uint64_t bytes, const CopyRef& after, int gate, CopyRef* out) override {
     auto copy = make_copy(false, bytes);
+    h2d_inflight().fetch_add(1, std::memory_order_relaxed);
+    copy->counted_h2d = true;
     Job job;
     job.copy = copy;
     job.dst = dst;
@@ -285,12 +297,33 @@ class SdmaLink : public Link {
   }
 
  private:
-  static uint32_t pick(uint32_t mask, uint32_t want, uint32_t avoid) {
-    if (want && (mask & want)) return want & (~want + 1);
-    for (int i = 0; i < 32; ++i)
-      if ((mask & (1u << i)) && (1u << i) != avoid) return 1u << i;
-    return mask & (~mask + 1);
+  // Engines of one direction, as bits: the available bits of `want` (at most two), else the
+  // `automatic` lowest available bits outside `avoid`, else the lowest available ones. Returns
+  // how many. Automatic choice: two for D2H, one for H2D. A second H2D engine gains nothing
+  // (H2D writes HBM and holds 55-57 GB/s under load), and while both directions run it takes
+  // the host link from D2H (block microbench: D2H 53 -> 34 GB/s).
+  static int pick(uint32_t mask, uint32_t want, uint32_t avoid, int automatic, uint32_t out[2]) {
+    int n = 0, limit = 2;
+    auto take = [&](uint32_t bits) {
+      for (int i = 0; i < 32 && n < limit; ++i)
+        if (bits & (1u << i)) out[n++] = 1u << i;
+    };
+    if (want) take(want & mask);
+    limit = n ? limit : automatic;
+    if (!n) take(mask & ~avoid);
+    if (!n) take(mask);
+    return n;
   }
+
+  // A copy of at least kSplitBytes with two engines in its direction goes out as two halves,
+  // one per engine. One SDMA engine keeps too few reads in flight to cover HBM latency while
+  // HBM-bound kernels run (28 MB D2H: 41.6 GB/s alone, 56-57 GB/s as two halves). A D2H is
+  // split only while no H2D is pending on the device (enqueued, even if still waiting for its
+  // dependencies): with both directions busy the host link is the limit, and a split D2H takes
+  // it from the H2D (block microbench: D2H 53 -> 55, H2D 57 -> 53 GB/s, iteration 43.7 ->
+  // 45.5 ms).
+  static constexpr uint64_t kSplitBytes = 2ull << 20;
+  std::atomic<int>& h2d_inflight() { return g_h2d_inflight[device_ < kMaxDevices && device_ >= 0 ? device_ : 0]; }
 
   SdmaRef make_copy(bool to_host, uint64_t bytes) {
     auto c = std::make_shared<SdmaCopy>();
@@ -340,6 +373,10 @@ class SdmaLink : public Link {
 
   void finish(const SdmaRef& c, bool failed) {
     const int dir = c->to_host ? 0 : 1;
+    if (c->counted_h2d) {
+      c->counted_h2d = false;
+      h2d_inflight().fetch_sub(1, std::memory_order_relaxed);
+    }
     const int64_t t = now_ns();
     if (failed) {
       c->fail.store(true, std::memory_order_release);
@@ -381,24 +418,38 @@ class SdmaLink : public Link {
         return true;
       }
     }
-    hsa_signal_t sig{0};
-    if (!take_signal(&sig)) {
-      finish(job.copy, true);
-      return true;
-    }
     SdmaCopy& c = *job.copy;
+    const uint32_t* engines = c.to_host ? e_d2h_ : e_h2d_;
+    const bool quiet = !c.to_host || h2d_inflight().load(std::memory_order_relaxed) == 0;
+    const int parts = (c.to_host ? n_d2h_ : n_h2d_) > 1 && c.bytes >= kSplitBytes && quiet ? 2 : 1;
+    const uint64_t half = parts == 2 ? c.bytes / 2 / 4096 * 4096 : c.bytes;
+    c.parts_left = parts;
     c.issue_ns = now_ns();
-    const hsa_status_t st = hsa_amd_memory_async_copy_on_engine(
-        job.dst, c.to_host ? cpu_ : gpu_, job.src, c.to_host ? gpu_ : cpu_, c.bytes, 0, nullptr, sig,
-        (hsa_amd_sdma_engine_id_t)(c.to_host ? e_d2h_ : e_h2d_), true);
-    if (st != HSA_STATUS_SUCCESS) {
-      sig_pool_.push_back(sig);
-      finish(job.copy, true);
-      return true;
+    for (int k = 0; k < parts; ++k) {
+      const uint64_t off = k ? half : 0;
+      const uint64_t len = k ? c.bytes - half : half;
+      hsa_signal_t sig{0};
+      hsa_status_t st = HSA_STATUS_ERROR;
+      if (take_signal(&sig)) {
+        st = hsa_amd_memory_async_copy_on_engine(
+            (char*)job.dst + off, c.to_host ? cpu_ : gpu_, (const char*)job.src + off, c.to_host ? gpu_ : cpu_, len,
+            0, nullptr, sig, (hsa_amd_sdma_engine_id_t)engines[k], true);
+        if (st != HSA_STATUS_SUCCESS) sig_pool_.push_back(sig);
+      }
+      if (st != HSA_STATUS_SUCCESS) {
+        part_done(job.copy, true);  // the other half, if issued, still completes through its signal
+        continue;
+      }
+      inflight_.push_back(InFlight{job.copy, sig});
+      inflight_count_++;
     }
-    inflight_.push_back(InFlight{job.copy, sig});
-    inflight_count_++;
     return true;
+  }
+
+  // One half (or the whole) of a copy ended; the copy finishes with its last part.
+  void part_done(const SdmaRef& c, bool failed) {
+    if (failed) c->part_failed = true;
+    if (--c->parts_left == 0) finish(c, c->part_failed);
   }
 
   // Completed copies leave the in-flight list (in issue order per engine, but checked all).
@@ -407,14 +458,14 @@ class SdmaLink : public Link {
     for (auto it = inflight_.begin(); it != inflight_.end();) {
       const hsa_signal_value_t v = hsa_signal_load_scacquire(it->sig);
       if (v < 1) {
-        finish(it->copy, v < 0);
+        part_done(it->copy, v < 0);
         sig_pool_.push_back(it->sig);
         it = inflight_.erase(it);
         inflight_count_--;
         progress = true;
       } else if (now_ns() - it->copy->issue_ns > kWaitLimitNs) {
         // Give up on a copy the engine never completed: report it, keep the signal alive.
-        finish(it->copy, true);
+        part_done(it->copy, true);
         it = inflight_.erase(it);
         inflight_count_--;
         progress = true;
@@ -485,7 +536,8 @@ class SdmaLink : public Link {
   int device_ = 0;
   bool hsa_inited_ = false;
   hsa_agent_t gpu_{0}, cpu_{0};
-  uint32_t e_d2h_ = 0, e_h2d_ = 0;
+  uint32_t e_d2h_[2] = {0, 0}, e_h2d_[2] = {0, 0};  // engine bits per direction
+  int n_d2h_ = 0, n_h2d_ = 0;
   std::vector<GateState> gates_;  // API threads only (engine mutex)
   uint64_t d2h_bytes_ = 0, h2d_bytes_ = 0, host_blocks_ = 0, host_block_ns_ = 0;  // API threads only
 
