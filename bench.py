@@ -486,7 +486,7 @@ def calibration_copy(device, stream: int, repeats: int = 3) -> None:
 
 
 def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: int, restore_slots: int,
-          batch_packs: bool = True):
+          batch_packs: bool = True, d2h_engine: int = 0, h2d_engine: int = 0):
     """one regime-B block's saved set through pack -> D2H -> H2D -> unpack.
 
     Every iteration packs the block's tensors into one group (staging ring + SDMA D2H), commits
@@ -501,7 +501,8 @@ def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: 
 
     engine = OffloadEngine(device, EngineConfig(
         stage_slot_bytes=slot_mib << 20, stage_slots=stage_slots, restore_slots=restore_slots,
-        timing=True, kernel_timing=True, staged_restore=False, prefetch=False, batch_packs=batch_packs))
+        timing=True, kernel_timing=True, staged_restore=False, prefetch=False, batch_packs=batch_packs,
+        d2h_engine=d2h_engine, h2d_engine=h2d_engine))
     stream = torch.cuda.current_stream(device).cuda_stream
     payload = sum(t.numel() * t.element_size() for t in tensors)
     storages = {}
@@ -785,6 +786,7 @@ def run(args) -> dict:
         kernel_copy=args.kernel_copy,
         batch_packs=not args.eager_pack,
         d2h_engine=args.d2h_engine,
+        h2d_engine=args.h2d_engine,
     )
     model = build_model(device, args.layers)
     inputs = make_inputs(device)
@@ -811,7 +813,8 @@ def run(args) -> dict:
         payload = sum(t.numel() * t.element_size() for t in tensors)
         log(f"micro: one regime-B block, {len(tensors)} unique saves, {payload / 1e6:.1f} MB")
         result["micro"] = micro(device, tensors, args.micro_iters, args.micro_warmup, args.slot_mib,
-                                args.stage_slots, args.restore_slots, batch_packs=not args.eager_pack)
+                                args.stage_slots, args.restore_slots, batch_packs=not args.eager_pack,
+                                d2h_engine=args.d2h_engine, h2d_engine=args.h2d_engine)
         m = result["micro"]
         log(f"micro: {m['s_per_iter'] * 1e3:.2f} ms/iter, D2H {m['d2h_gbps']:.1f} GB/s, H2D {m['h2d_gbps']:.1f} GB/s, "
             f"pack {m['pack_hbm_gbps']:.0f} GB/s ({m['pack_avg_launch_us']:.1f} us/launch), unpack "
@@ -1047,6 +1050,8 @@ def main() -> int:
     parser.add_argument("--no-staged-restore", action="store_true")
     parser.add_argument("--d2h-engine", type=lambda v: int(v, 0), default=0,
                         help="SDMA engine bits for D2H (0: two engines, copies split in halves)")
+    parser.add_argument("--h2d-engine", type=lambda v: int(v, 0), default=0,
+                        help="SDMA engine bits for H2D (0: one engine, the lowest not used by D2H)")
     parser.add_argument("--eager-pack", action="store_true",
                         help="one gather launch per save instead of one per staging segment")
     parser.add_argument("--kernel-copy", action="store_true", help="copy kernel on HIP streams instead of SDMA")
