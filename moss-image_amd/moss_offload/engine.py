@@ -134,8 +134,6 @@ class OffloadEngine:
         with self._lock:
             _native.describe(source, self._desc[0])
             _native.check("mo_pack", self._lib.mo_pack(self._handle, self._desc, 1, stream, self._ref))
-            if self.config.batch_packs:
-                self._hold(source)
             gid, idx = int(self._ref[0].group), int(self._ref[0].entry)
             group = self._groups.get(gid)
             if group is None:
@@ -148,6 +146,8 @@ class OffloadEngine:
             entry.refs = 1
             group.entries.append(entry)
             group.live += 1
+            if self.config.batch_packs:
+                self._hold(source)  # after the bookkeeping: it may raise for an earlier save
             return gid, idx
 
     def commit(self, stream: int) -> int | None:
@@ -193,9 +193,11 @@ class OffloadEngine:
                     del self._live[pos]
                 _native.check("mo_release", self._lib.mo_release(self._handle, gid))
                 if self._held:
-                    self._hold()
+                    # releasing the open group drops its pending gathers: their sources were
+                    # never read, so a later in-place change to them is no error
+                    self._hold(check=False)
 
-    def _hold(self, source: torch.Tensor | None = None) -> None:
+    def _hold(self, source: torch.Tensor | None = None, check: bool = True) -> None:
         """Keep ``source`` (of the pack call just made) alive while its gather is pending, and
         let go of the sources whose gathers the engine has launched. Launched kernels are
         stream-ordered before anything that later reuses their memory.
@@ -214,7 +216,7 @@ class OffloadEngine:
         launched = self._launched.value
         while self._held and self._held[0][0] <= launched:
             _, tensor, version = self._held.popleft()
-            if tensor._version != version:
+            if check and tensor._version != version:
                 raise RuntimeError(
                     "a tensor saved for backward was modified in place before the offload engine "
                     "gathered it (autograd would reject this without offloading); "

@@ -230,6 +230,7 @@ def test_release_of_the_open_group_drops_pending_gathers() -> None:
     small = [torch.randn(1000 + k, device=device) for k in range(5)]
     handles = [engine.pack(t, stream) for t in small]
     assert len(engine._held) == 5
+    small[0].add_(1.0)  # a dropped graph's source modified afterwards: its gather never runs
     for gid, idx in handles:
         engine.drop(gid, idx)
     assert not engine._held and engine.live_groups() == 0
