@@ -399,13 +399,13 @@ def capture_block_saves(model, inputs):
 
     import torch
     from moss_offload import dit
-    from moss_offload.activation_offload import _offload_view, _storage_key
+    from moss_offload.activation_offload import _bf16_exact, _offload_view, _storage_key
 
     configure_mode(model, "none", "B")
     resident = {_storage_key(t) for t in (*model.parameters(), *model.buffers())}
     layer = model.layers[len(model.layers) // 2]
     state = {"on": False}
-    saved, seen = [], set()
+    saved, seen, narrow = [], set(), []
 
     def pack(t):
         if state["on"] and t.device.type == "cuda" and _storage_key(t) not in resident and _offload_view(t) is not None:
@@ -413,8 +413,10 @@ def capture_block_saves(model, inputs):
             if key not in seen:
                 seen.add(key)
                 # detached: a saved tensor's grad_fn would keep the whole graph (and every
-                # activation up to this block) alive after the forward is dropped
+                # activation up to this block) alive after the forward is dropped; whether the
+                # hook would narrow it is decided now, while the graph is there
                 saved.append(t.detach())
+                narrow.append(_bf16_exact(t, _offload_view(t)[0]))
         # detached alias: returning `t` itself would tie outputs saved by their own node into
         # a reference cycle through the graph that the collector cannot break
         return t.detach()
@@ -431,7 +433,7 @@ def capture_block_saves(model, inputs):
         for h in handles:
             h.remove()
     del error
-    return saved
+    return saved, narrow
 
 
 def _same_bits(a, b) -> bool:
@@ -486,7 +488,7 @@ def calibration_copy(device, stream: int, repeats: int = 3) -> None:
 
 
 def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: int, restore_slots: int,
-          batch_packs: bool = True, d2h_engine: int = 0, h2d_engine: int = 0):
+          batch_packs: bool = True, d2h_engine: int = 0, h2d_engine: int = 0, narrow=None):
     """one regime-B block's saved set through pack -> D2H -> H2D -> unpack.
 
     Every iteration packs the block's tensors into one group (staging ring + SDMA D2H), commits
@@ -509,12 +511,17 @@ def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: 
     for t in tensors:
         storages.setdefault(t.untyped_storage().data_ptr(), t)
 
+    narrow = list(narrow) if narrow is not None else [False] * len(tensors)
+
     def refill():
         for t in storages.values():
             torch.empty(0, dtype=torch.uint8, device=device).set_(t.untyped_storage()).random_(0, 256)
+        for t, nr in zip(tensors, narrow):
+            if nr:  # keep the float32 casts of bfloat16 values exact bfloat16, as the hook found them
+                t.view(torch.int32).bitwise_and_(-65536)
 
     def one(keep: bool):
-        refs = [engine.pack(t, stream) for t in tensors]
+        refs = [engine.pack(t, stream, narrow=nr) for t, nr in zip(tensors, narrow)]
         engine.commit(stream)
         outs = [engine.restore(g, i, stream) for g, i in refs]
         for g, i in refs:
@@ -556,12 +563,13 @@ def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: 
         "d2h_gbps": st["timed_d2h_bytes"] / max(st["d2h_ms"], 1e-9) / 1e6,
         "h2d_gbps": st["timed_h2d_bytes"] / max(st["h2d_ms"], 1e-9) / 1e6,
         "pipeline_gbps": 2 * payload / seconds / 1e9,
-        "pack_hbm_gbps": 2 * st["timed_pack_bytes"] / max(st["pack_ms"], 1e-9) / 1e6,
-        "unpack_hbm_gbps": 2 * st["timed_unpack_bytes"] / max(st["unpack_ms"], 1e-9) / 1e6,
+        "pack_hbm_gbps": st["timed_pack_hbm_bytes"] / max(st["pack_ms"], 1e-9) / 1e6,
+        "unpack_hbm_gbps": st["timed_unpack_hbm_bytes"] / max(st["unpack_ms"], 1e-9) / 1e6,
         "pack_avg_launch_us": st["pack_ms"] * 1e3 / max(st["timed_pack_launches"], 1),
         "unpack_avg_launch_us": st["unpack_ms"] * 1e3 / max(st["timed_unpack_launches"], 1),
         "pack_bytes_per_launch": st["timed_pack_bytes"] / max(st["timed_pack_launches"], 1),
         "unpack_bytes_per_launch": st["timed_unpack_bytes"] / max(st["timed_unpack_launches"], 1),
+        "pack_hbm_bytes_per_launch": st["timed_pack_hbm_bytes"] / max(st["timed_pack_launches"], 1),
         "pack_launches_per_iter": st["timed_pack_launches"] / iters,
         "unpack_launches_per_iter": st["timed_unpack_launches"] / iters,
         "host_blocks_per_iter": st["host_blocks"] / iters,
@@ -787,6 +795,7 @@ def run(args) -> dict:
         batch_packs=not args.eager_pack,
         d2h_engine=args.d2h_engine,
         h2d_engine=args.h2d_engine,
+        narrow_bf16_casts=not args.no_narrow,
     )
     model = build_model(device, args.layers)
     inputs = make_inputs(device)
@@ -808,13 +817,18 @@ def run(args) -> dict:
         log(f"parity: {result['parity']}")
 
     if "M" in args.regimes:
-        tensors = capture_block_saves(model, inputs)
+        tensors, narrow = capture_block_saves(model, inputs)
+        if args.no_narrow:
+            narrow = [False] * len(tensors)
         torch.cuda.synchronize()
         payload = sum(t.numel() * t.element_size() for t in tensors)
-        log(f"micro: one regime-B block, {len(tensors)} unique saves, {payload / 1e6:.1f} MB")
+        moved = sum(t.numel() * (2 if nr else t.element_size()) for t, nr in zip(tensors, narrow))
+        log(f"micro: one regime-B block, {len(tensors)} unique saves, {payload / 1e6:.1f} MB "
+            f"({sum(narrow)} bf16 casts narrowed: {moved / 1e6:.1f} MB over the link)")
         result["micro"] = micro(device, tensors, args.micro_iters, args.micro_warmup, args.slot_mib,
                                 args.stage_slots, args.restore_slots, batch_packs=not args.eager_pack,
-                                d2h_engine=args.d2h_engine, h2d_engine=args.h2d_engine)
+                                d2h_engine=args.d2h_engine, h2d_engine=args.h2d_engine, narrow=narrow)
+        result["micro"].update(narrowed_tensors=sum(narrow), link_bytes_per_iter=moved)
         m = result["micro"]
         log(f"micro: {m['s_per_iter'] * 1e3:.2f} ms/iter, D2H {m['d2h_gbps']:.1f} GB/s, H2D {m['h2d_gbps']:.1f} GB/s, "
             f"pack {m['pack_hbm_gbps']:.0f} GB/s ({m['pack_avg_launch_us']:.1f} us/launch), unpack "
@@ -992,11 +1006,12 @@ def run(args) -> dict:
                     h2d_s_per_step=st["h2d_ms"] / 1e3 / n,
                     d2h_gbps=st["timed_d2h_bytes"] / max(st["d2h_ms"], 1e-9) / 1e6,
                     h2d_gbps=st["timed_h2d_bytes"] / max(st["h2d_ms"], 1e-9) / 1e6,
-                    pack_hbm_gbps=2 * st["timed_pack_bytes"] / max(st["pack_ms"], 1e-9) / 1e6,
-                    unpack_hbm_gbps=2 * st["timed_unpack_bytes"] / max(st["unpack_ms"], 1e-9) / 1e6,
+                    pack_hbm_gbps=st["timed_pack_hbm_bytes"] / max(st["pack_ms"], 1e-9) / 1e6,
+                    unpack_hbm_gbps=st["timed_unpack_hbm_bytes"] / max(st["unpack_ms"], 1e-9) / 1e6,
                     pack_avg_launch_us=st["pack_ms"] * 1e3 / max(st["timed_pack_launches"], 1),
                     unpack_avg_launch_us=st["unpack_ms"] * 1e3 / max(st["timed_unpack_launches"], 1),
                     pack_bytes_per_launch=st["timed_pack_bytes"] / max(st["timed_pack_launches"], 1),
+                    pack_hbm_bytes_per_launch=st["timed_pack_hbm_bytes"] / max(st["timed_pack_launches"], 1),
                     unpack_bytes_per_launch=st["timed_unpack_bytes"] / max(st["timed_unpack_launches"], 1),
                     host_blocks=st["host_blocks"],
                     host_block_ms=st["host_block_ms"],
@@ -1052,6 +1067,8 @@ def main() -> int:
                         help="SDMA engine bits for D2H (0: two engines, copies split in halves)")
     parser.add_argument("--h2d-engine", type=lambda v: int(v, 0), default=0,
                         help="SDMA engine bits for H2D (0: one engine, the lowest not used by D2H)")
+    parser.add_argument("--no-narrow", action="store_true",
+                        help="offload float32 casts of bfloat16 tensors whole instead of as their high halves")
     parser.add_argument("--eager-pack", action="store_true",
                         help="one gather launch per save instead of one per staging segment")
     parser.add_argument("--kernel-copy", action="store_true", help="copy kernel on HIP streams instead of SDMA")
@@ -1109,8 +1126,9 @@ def main() -> int:
     # dominant engine kernel of the headline regime
     # Dominant engine kernel: the pack kernel (mo_pack_kernel). Measured on the config-2 block
     # microbench when it ran (one regime-B block's saves, the bulk of all offload traffic),
-    # else on the headline regime's steps. achieved = 2 x payload bytes per launch (read the
-    # source, write the staging slot) / average dispatch duration (HIP events of the launch).
+    # else on the headline regime's steps. achieved = device-memory bytes per launch (read the
+    # source, write the staging slot: 2 x payload, or 3 x for a narrowed float32 piece, which
+    # reads 4 bytes per 2 it writes) / average dispatch duration (HIP events of the launch).
     src = result.get("micro") or eng
     pack_bound = {
         "bound": "hbm",
@@ -1122,7 +1140,7 @@ def main() -> int:
         "frac": round(src.get("pack_hbm_gbps", 0.0) / HBM_PEAK_GBPS, 4),
         "traffic": profiled_traffic() if "micro" in result else None,
         "traffic_source": PACK_PROFILE.name if "micro" in result else None,
-        "algorithmic_bytes_per_launch": 2 * src.get("pack_bytes_per_launch", 0.0),
+        "algorithmic_bytes_per_launch": src.get("pack_hbm_bytes_per_launch", 0.0),
         "avg_launch_us": src.get("pack_avg_launch_us"),
     }
     line = {

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 6
+#define MO_ABI_VERSION 7
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -64,7 +64,17 @@ typedef struct mo_tensor {
   uint32_t ndim;       /* 0..MO_MAX_DIMS */
   int64_t size[MO_MAX_DIMS];
   int64_t stride[MO_MAX_DIMS];
+  uint32_t flags;      /* MO_TENSOR_*                                                    */
+  uint32_t reserved;   /* 0                                                              */
 } mo_tensor;
+
+/* Flags for mo_tensor.flags.
+ * MO_TENSOR_BF16_HIGH: a contiguous float32 tensor whose values are exactly bfloat16 (the low
+ * 16 bits of every element are zero, as for the output of a bfloat16 -> float32 cast). Its
+ * payload keeps the high 16 bits of each element (numel x 2 bytes), and restoring it writes
+ * them back with the low bits zero: the same float32 bits, over half the bytes. No reference
+ * counterpart: the reference copies the float32 tensor as it is. */
+#define MO_TENSOR_BF16_HIGH 0x1
 
 /* Engine configuration (mo_create). Zero fields take the defaults in brackets. */
 typedef struct mo_config {
@@ -110,6 +120,8 @@ typedef struct mo_stats {
   double pack_ms, unpack_ms;   /* summed kernel durations (MO_FLAG_KERNEL_TIMING)         */
   uint64_t timed_pack_bytes, timed_unpack_bytes; /* payload bytes of those launches      */
   uint64_t timed_pack_launches, timed_unpack_launches;
+  uint64_t timed_pack_hbm_bytes, timed_unpack_hbm_bytes; /* device-memory bytes read + written
+                                                            by those launches                */
 } mo_stats;
 
 typedef struct mo_engine mo_engine;

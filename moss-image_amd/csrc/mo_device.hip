@@ -14,6 +14,10 @@
 //           dimension): elements are gathered one by one into LDS and the tile is written
 //           to the payload with 128-bit stores (pack), or read from the payload with 128-bit
 //           loads into LDS and scattered from there (unpack).
+//   NARROW  a contiguous float32 tensor whose values are exactly bfloat16: the payload holds
+//           the high 16 bits of each element (pack reads 32 B and writes 16 B a chunk; unpack
+//           writes the halves back with zero low bits), so the same bits cross the host link
+//           in half the bytes.
 //
 // Grid: one 256-lane workgroup per 16 KiB tile of payload; tiles of all pieces of the
 // launch are numbered consecutively and a workgroup finds its piece with a scalar search.
@@ -57,6 +61,7 @@ enum Space { kG, kL };
 // 16-byte values move as a native vector: uint4 is a class whose copy constructor takes a
 // generic reference, which would turn the access back into a flat one.
 typedef unsigned int mo_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int mo_u32x2 __attribute__((ext_vector_type(2)));
 
 template <Space S, typename T>
 __device__ __forceinline__ T ld(const char* p) {
@@ -114,6 +119,29 @@ __device__ __forceinline__ void st16_out(char* p, uint4 v) {
   else st16(p, v);
 }
 
+// NARROW: 8 float32 elements (two 16-byte words a, b) <-> their 8 high halves (one 16-byte word;
+// element j's bits at payload bytes 2j, 2j+1, little-endian).
+__device__ __forceinline__ uint4 high_halves(uint4 a, uint4 b) {
+  return make_uint4((a.x >> 16) | (a.y & 0xffff0000u), (a.z >> 16) | (a.w & 0xffff0000u),
+                    (b.x >> 16) | (b.y & 0xffff0000u), (b.z >> 16) | (b.w & 0xffff0000u));
+}
+__device__ __forceinline__ void widen(uint4 v, uint4& a, uint4& b) {
+  a = make_uint4(v.x << 16, v.x & 0xffff0000u, v.y << 16, v.y & 0xffff0000u);
+  b = make_uint4(v.z << 16, v.z & 0xffff0000u, v.w << 16, v.w & 0xffff0000u);
+}
+template <bool kPack>
+__device__ __forceinline__ void narrow_chunk(char* payload16, char* tensor32) {
+  if (kPack) {
+    const uint4 a = ld16(tensor32), b = ld16(tensor32 + 16);
+    st16_stream(payload16, high_halves(a, b));
+  } else {
+    uint4 a, b;
+    widen(ld16(payload16), a, b);
+    st16(tensor32, a);
+    st16(tensor32 + 16, b);
+  }
+}
+
 // One 16 KiB tile (`tile`, numbered within the launch) of piece `d`.
 template <bool kPack>
 __device__ __forceinline__ void copy_tile(const KDesc& d, uint32_t tile) {
@@ -140,6 +168,45 @@ __device__ __forceinline__ void copy_tile(const KDesc& d, uint32_t tile) {
       const uint32_t nvec = tile_bytes / 16;
       for (uint32_t c = tid; c < nvec; c += kThreads) st16_out<kPack>(dst + (size_t)c * 16, ld16(src + (size_t)c * 16));
       for (uint32_t b = nvec * 16 + tid * eb; b < tile_bytes; b += kThreads * eb) copy_elem<kG, kG>(dst + b, src + b, eb);
+    }
+    return;
+  }
+
+  if (d.path == kPathNarrow) {
+    // payload offsets count bfloat16 bits; the float32 tensor side is twice as far in. A full
+    // tile, measured both ways on the block microbench: pack keeps 16-byte streaming stores (a
+    // lane reads the 32 tensor bytes of one payload chunk); unpack moves 8 contiguous payload
+    // bytes <-> 16 contiguous tensor bytes a lane, so each instruction covers one span.
+    char* const t = tensor + 2 * (d.first + tile_off);
+    if (tile_bytes == kTileBytes) {
+      constexpr int kRounds = 2 * kUnroll;
+      if (kPack) {
+        uint4 a[kUnroll], b[kUnroll];
+#pragma unroll
+        for (int k = 0; k < kUnroll; ++k) {
+          a[k] = ld16(t + (size_t)(k * kThreads + tid) * 32);
+          b[k] = ld16(t + (size_t)(k * kThreads + tid) * 32 + 16);
+        }
+#pragma unroll
+        for (int k = 0; k < kUnroll; ++k) st16_stream(payload + (size_t)(k * kThreads + tid) * 16, high_halves(a[k], b[k]));
+      } else {
+        mo_u32x2 v[kRounds];
+#pragma unroll
+        for (int k = 0; k < kRounds; ++k) v[k] = *(const MO_GLOBAL mo_u32x2*)(payload + (size_t)(k * kThreads + tid) * 8);
+#pragma unroll
+        for (int k = 0; k < kRounds; ++k)
+          st16(t + (size_t)(k * kThreads + tid) * 16,
+               make_uint4(v[k].x << 16, v[k].x & 0xffff0000u, v[k].y << 16, v[k].y & 0xffff0000u));
+      }
+    } else {
+      const uint32_t nvec = tile_bytes / 16;
+      for (uint32_t c = tid; c < nvec; c += kThreads) narrow_chunk<kPack>(payload + (size_t)c * 16, t + (size_t)c * 32);
+      for (uint32_t b = nvec * 16 + tid * 2; b < tile_bytes; b += kThreads * 2) {
+        if (kPack)
+          st<kG>(payload + b, (uint16_t)(ld<kG, uint32_t>(t + (size_t)b * 2) >> 16));
+        else
+          st<kG>(t + (size_t)b * 2, (uint32_t)ld<kG, uint16_t>(payload + b) << 16);
+      }
     }
     return;
   }

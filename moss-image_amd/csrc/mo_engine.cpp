@@ -274,6 +274,7 @@ struct PendingFree {
 struct Timing {
   hipEvent_t start, end;
   uint64_t bytes;
+  uint64_t hbm;
   bool pack;
 };
 
@@ -307,7 +308,7 @@ struct Engine {
     Timing cur{};
     KernelTimer(Engine* engine, bool p) : e(engine), pack(p) {}
     int events(hipEvent_t* start, hipEvent_t* stop) override {
-      cur = Timing{nullptr, nullptr, 0, pack};
+      cur = Timing{nullptr, nullptr, 0, 0, pack};
       if (!(e->cfg.flags & MO_FLAG_KERNEL_TIMING)) return 0;
       for (hipEvent_t* ev : {&cur.start, &cur.end}) {
         if (!e->timing_pool.empty()) {
@@ -322,10 +323,11 @@ struct Engine {
       *stop = cur.end;
       return 0;
     }
-    void launched(uint64_t bytes) override {
+    void launched(uint64_t bytes, uint64_t hbm) override {
       cur.bytes = bytes;
+      cur.hbm = hbm;
       e->timings.push_back(cur);
-      cur = Timing{nullptr, nullptr, 0, pack};
+      cur = Timing{nullptr, nullptr, 0, 0, pack};
     }
   };
 
@@ -377,10 +379,12 @@ struct Engine {
         if (t.pack) {
           st.pack_ms += ms;
           st.timed_pack_bytes += t.bytes;
+          st.timed_pack_hbm_bytes += t.hbm;
           st.timed_pack_launches++;
         } else {
           st.unpack_ms += ms;
           st.timed_unpack_bytes += t.bytes;
+          st.timed_unpack_hbm_bytes += t.hbm;
           st.timed_unpack_launches++;
         }
       }

@@ -22,7 +22,8 @@ class LaunchTimer {
   virtual ~LaunchTimer() = default;
   // *start/*stop stay null when the next launch is not timed.
   virtual int events(hipEvent_t* start, hipEvent_t* stop) = 0;
-  virtual void launched(uint64_t bytes) = 0;
+  // bytes: payload bytes of the launch; hbm: device-memory bytes it reads and writes
+  virtual void launched(uint64_t bytes, uint64_t hbm) = 0;
 };
 
 // Accumulates pieces and launches the pack (or unpack) kernel in batches of kMaxDesc.
@@ -46,6 +47,7 @@ class Launcher {
   uint64_t launches_ = 0;
   uint64_t bytes_ = 0;          // all bytes added
   uint64_t pending_bytes_ = 0;  // bytes of the batch not launched yet
+  uint64_t pending_hbm_ = 0;    // device-memory bytes the batch reads and writes
 };
 
 int launch_link_copy(void* dst, const void* src, uint64_t bytes, uint32_t blocks, hipStream_t stream);

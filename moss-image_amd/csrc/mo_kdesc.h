@@ -16,7 +16,9 @@ constexpr int kMaxDesc = 16;                  // pieces per launch (kernel-argum
 constexpr uint32_t kMaxTilesPerLaunch = 1u << 22;
 constexpr int kLinkUnroll = 8;                // 16-byte transfers in flight per lane (link copy)
 
-enum : uint8_t { kPathContig = 0, kPathRuns = 1, kPathElem = 2 };
+// NARROW: contiguous float32 on the tensor side, its high halves (bfloat16 bits) as the
+// payload; `first` and `nbytes` count payload bytes, the tensor side is twice that.
+enum : uint8_t { kPathContig = 0, kPathRuns = 1, kPathElem = 2, kPathNarrow = 3 };
 
 struct KFastDiv {
   uint32_t d, m, s;

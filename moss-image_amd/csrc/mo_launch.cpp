@@ -106,6 +106,16 @@ int make_kdesc(const Canon& c, uint64_t tensor_base, uint64_t first, uint64_t nb
   const bool inner_contig = nd == 0 || (uint64_t)c.stride[nd - 1] == c.eb;
   const uint64_t run_bytes = nd == 0 ? c.eb : (inner_contig ? (uint64_t)c.size[nd - 1] * c.eb : c.eb);
   const int nouter = inner_contig ? (nd > 0 ? nd - 1 : 0) : nd;  // dims outside the run
+  if (c.bf16_high) {
+    // canonicalize admits only contiguous tensors with this flag
+    if (nouter != 0 || tensor_base % 16 != 0) {
+      err = "a bf16-high tensor must be contiguous and 16-byte aligned";
+      return MO_E_INVALID;
+    }
+    kd.path = kPathNarrow;
+    kd.first = first;
+    return 0;
+  }
   if (nouter == 0 && tensor_base % 16 == 0) {
     kd.path = kPathContig;
     kd.first = first;
@@ -177,6 +187,7 @@ void Launcher::add(const KDesc& kd) {
   tiles_ += (uint32_t)t;
   bytes_ += kd.nbytes;
   pending_bytes_ += kd.nbytes;
+  pending_hbm_ += kd.nbytes * (kd.path == kPathNarrow ? 3 : 2);  // narrow: 2 B tensor-side per payload B
   args_.ndesc++;
   if (tiles_ > kMaxTilesPerLaunch) flush();
 }
@@ -201,11 +212,12 @@ int Launcher::flush() {
                             : hipModuleLaunchKernel(fn, tiles_, 1, 1, kThreads, 1, 1, 0, stream_, params, nullptr);
     if (e != hipSuccess) status_ = (int)e;
     launches_++;
-    if (e == hipSuccess && t0) timer_->launched(pending_bytes_);
+    if (e == hipSuccess && t0) timer_->launched(pending_bytes_, pending_hbm_);
   }
   args_.ndesc = 0;
   tiles_ = 0;
   pending_bytes_ = 0;
+  pending_hbm_ = 0;
   return status_;
 }
 

@@ -30,7 +30,8 @@ struct Canon {
   int64_t size[MO_MAX_DIMS] = {};
   int64_t stride[MO_MAX_DIMS] = {};  // bytes
   uint64_t numel = 0;
-  uint64_t nbytes = 0;   // numel * eb
+  uint64_t nbytes = 0;   // payload bytes: numel * eb, or numel * 2 for a bf16-high tensor
+  bool bf16_high = false;  // MO_TENSOR_BF16_HIGH: payload = the high halves of float32 elements
 };
 
 // Returns 0 or an MO_E_* code with a message in `err`.
@@ -61,6 +62,18 @@ inline int canonicalize(const mo_tensor& t, Canon& c, std::string& err) {
   }
   c.numel = numel;
   c.nbytes = numel * eb;
+  if (t.flags & ~(uint32_t)MO_TENSOR_BF16_HIGH) {
+    err = "unknown tensor flags";
+    return MO_E_INVALID;
+  }
+  if (t.flags & MO_TENSOR_BF16_HIGH) {
+    if (eb != 4) {
+      err = "MO_TENSOR_BF16_HIGH needs 4-byte (float32) elements";
+      return MO_E_INVALID;
+    }
+    c.bf16_high = true;
+    c.nbytes = numel * 2;
+  }
   if (numel == 0) return 0;
   if (t.ptr % eb != 0) {
     err = "tensor address is not aligned to its element size";
@@ -102,6 +115,10 @@ inline int canonicalize(const mo_tensor& t, Canon& c, std::string& err) {
   for (int i = 0; i < nm; ++i) {  // outermost first
     c.size[i] = merged[nm - 1 - i].size;
     c.stride[i] = merged[nm - 1 - i].stride * (int64_t)eb;
+  }
+  if (c.bf16_high && !(nm == 0 || (nm == 1 && merged[0].stride == 1))) {
+    err = "MO_TENSOR_BF16_HIGH needs a contiguous tensor";
+    return MO_E_LAYOUT;
   }
   return 0;
 }

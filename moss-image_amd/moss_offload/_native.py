@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 6
+MO_ABI_VERSION = 7
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -28,6 +28,7 @@ MO_FLAG_KERNEL_COPY = 0x2
 MO_FLAG_KERNEL_TIMING = 0x4
 MO_FLAG_NO_STAGED_RESTORE = 0x8
 MO_FLAG_EAGER_PACK = 0x10
+MO_TENSOR_BF16_HIGH = 0x1
 
 NO_GROUP = (1 << 64) - 1
 
@@ -39,6 +40,8 @@ class MoTensor(ctypes.Structure):
         ("ndim", ctypes.c_uint32),
         ("size", ctypes.c_int64 * MO_MAX_DIMS),
         ("stride", ctypes.c_int64 * MO_MAX_DIMS),
+        ("flags", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
     ]
 
 
@@ -102,6 +105,8 @@ class MoStats(ctypes.Structure):
         ("timed_unpack_bytes", ctypes.c_uint64),
         ("timed_pack_launches", ctypes.c_uint64),
         ("timed_unpack_launches", ctypes.c_uint64),
+        ("timed_pack_hbm_bytes", ctypes.c_uint64),
+        ("timed_unpack_hbm_bytes", ctypes.c_uint64),
     ]
 
     def as_dict(self) -> dict:
@@ -245,8 +250,8 @@ def check(call: str, status: int) -> None:
         raise EngineError(call, status, message)
 
 
-def describe(tensor: torch.Tensor, out: MoTensor, ptr: int | None = None) -> MoTensor:
-    """Fill ``out`` with the view ``tensor`` (address, element size, sizes, strides)."""
+def describe(tensor: torch.Tensor, out: MoTensor, ptr: int | None = None, flags: int = 0) -> MoTensor:
+    """Fill ``out`` with the view ``tensor`` (address, element size, sizes, strides, flags)."""
 
     shape = tensor.shape
     stride = tensor.stride()
@@ -256,6 +261,8 @@ def describe(tensor: torch.Tensor, out: MoTensor, ptr: int | None = None) -> MoT
     out.ptr = tensor.data_ptr() if ptr is None else ptr
     out.elem_bytes = tensor.element_size()
     out.ndim = ndim
+    out.flags = flags
+    out.reserved = 0
     for i in range(ndim):
         out.size[i] = shape[i]
         out.stride[i] = stride[i]

@@ -98,6 +98,31 @@ def _payload_key(source: torch.Tensor) -> tuple[int, tuple[tuple[int, int], ...]
     return source.storage_offset() * es, tuple(merged), es
 
 
+def _bf16_exact(tensor: torch.Tensor, source: torch.Tensor) -> bool:
+    """True when ``tensor`` is the untouched output of a bfloat16 -> float32 cast, so that the low
+    16 bits of every element are zero and its high halves alone restore it bit for bit.
+
+    Read from the autograd graph: the tensor's node is ``ToCopyBackward0`` and the gradient
+    its input receives is bfloat16 (the cast's source dtype). ``_version == 0``: nothing,
+    autograd-visible or under ``no_grad``, has written it since the cast. The payload must also
+    be dense in storage order and 16-byte aligned (the engine's narrowing path).
+    """
+
+    if tensor.dtype != torch.float32 or source is not tensor or tensor._version != 0:
+        return False
+    fn = tensor.grad_fn
+    if fn is None or type(fn).__name__ != "ToCopyBackward0" or tensor.data_ptr() % 16:
+        return False
+    try:
+        node, nr = fn.next_functions[0]
+        if node is None or node._input_metadata[nr].dtype != torch.bfloat16:
+            return False
+    except (AttributeError, IndexError, RuntimeError):  # private autograd API absent or changed
+        return False
+    dims = _payload_key(source)[1]
+    return len(dims) <= 1 and (not dims or dims[0][1] == 4)
+
+
 def _restore_layout(
     payload: torch.Tensor,
     device: torch.device,
@@ -166,6 +191,7 @@ class _ActivationOffload:
             if tensor.device.type == "cuda" and tensor.untyped_storage().nbytes()
         }
         self.dedupe = self.engine.config.dedupe and StorageWeakRef is not None
+        self.narrow = self.engine.config.narrow_bf16_casts
         self._seen: dict[tuple, tuple] = {}
         self._shared: set[int] = set()  # groups holding saves made more than once
         self._hooks = torch.autograd.graph.saved_tensors_hooks(self.pack, self.unpack)
@@ -254,7 +280,7 @@ class _ActivationOffload:
                     self._shared.add(gid)
                     return _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
         stream = torch.cuda.current_stream(device).cuda_stream
-        gid, idx = self.engine.pack(source, stream)
+        gid, idx = self.engine.pack(source, stream, narrow=self.narrow and _bf16_exact(tensor, source))
         if key is not None:
             self._seen[key] = (StorageWeakRef(tensor.untyped_storage()), tensor._version, gid, idx)
         return _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)

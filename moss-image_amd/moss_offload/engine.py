@@ -52,6 +52,10 @@ class EngineConfig:
     # nearer the HBM copy rate. The engine keeps each save's source tensor alive until its
     # kernel is launched (at most one staging slot of saves). False: launch at every save.
     batch_packs: bool = True
+    # A float32 save that is the untouched output of a bfloat16 -> float32 cast (every element's
+    # low 16 bits are zero) crosses the link as its high halves: the same bits in half the bytes
+    # (MO_TENSOR_BF16_HIGH). The hook decides from the autograd graph; False copies it whole.
+    narrow_bf16_casts: bool = True
     # Saves made inside the last `keep_last_blocks` blocks of `model.layers` stay on the device
     # (0: offload every block, as the reference does). Backward needs them first, so offloading
     # them only sends them out and straight back; keeping them trades device memory for link
@@ -128,11 +132,14 @@ class OffloadEngine:
         self._launched = ctypes.c_uint64()
 
     # ------------------------------------------------------------------ forward
-    def pack(self, source: torch.Tensor, stream: int) -> tuple[int, int]:
-        """Gather ``source`` into the open group; return ``(group, entry)`` with one reference."""
+    def pack(self, source: torch.Tensor, stream: int, narrow: bool = False) -> tuple[int, int]:
+        """Gather ``source`` into the open group; return ``(group, entry)`` with one reference.
+
+        ``narrow``: ``source`` is float32 with exact bfloat16 values; only its high halves are
+        kept (MO_TENSOR_BF16_HIGH), and the restore writes them back with zero low halves."""
 
         with self._lock:
-            _native.describe(source, self._desc[0])
+            _native.describe(source, self._desc[0], flags=_native.MO_TENSOR_BF16_HIGH if narrow else 0)
             _native.check("mo_pack", self._lib.mo_pack(self._handle, self._desc, 1, stream, self._ref))
             gid, idx = int(self._ref[0].group), int(self._ref[0].entry)
             group = self._groups.get(gid)
@@ -142,7 +149,7 @@ class OffloadEngine:
             if idx != len(group.entries):
                 raise RuntimeError(f"engine entry index {idx} out of sync with group {gid}")
             entry = _EntryState(source.dtype, tuple(source.shape), tuple(source.stride()),
-                                source.numel() * source.element_size())
+                                source.numel() * (2 if narrow else source.element_size()))
             entry.refs = 1
             group.entries.append(entry)
             group.live += 1

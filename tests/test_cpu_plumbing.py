@@ -12,6 +12,8 @@
 - The dedupe key of the engine's hook (``_payload_key``): equal for every view of the same
   bytes (transposed, reshaped, expanded), different for a shifted, strided, partial or
   same-size view of other bytes; the manifest counts aliasing views once.
+- The narrowing test of the hook (``_bf16_exact``): only the untouched float32 output of a
+  bfloat16 -> float32 cast qualifies.
 - The manifest probe lets the graph go when the forward is dropped (regression: a pack hook
   that returns its argument ties outputs saved by their own node into an uncollectable cycle).
 """
@@ -26,7 +28,7 @@ import torch
 
 import moss_offload
 from moss_offload import dit, engine
-from moss_offload.activation_offload import _offload_view, _payload_key
+from moss_offload.activation_offload import _bf16_exact, _offload_view, _payload_key
 from moss_offload.manifest import ManifestRecorder
 from oracle import reference_hooks
 
@@ -174,6 +176,31 @@ def test_manifest_counts_aliasing_views_once() -> None:
     assert len(offloaded) == 4
     assert [r.dup_of for r in offloaded] == [None, offloaded[0].index, offloaded[0].index, None]
     assert probe.payload_bytes(unique=True) == (x.numel() + x[:, 1:].numel()) * 4
+
+
+def test_bf16_exact_reads_the_cast_from_the_graph() -> None:
+    def ok(t):
+        return _bf16_exact(t, _offload_view(t)[0])
+
+    x = torch.randn(64, 32, dtype=torch.bfloat16, requires_grad=True)
+    assert ok((x * 2).float())  # cast of an op's bf16 output
+    assert ok(x.to(torch.float32))  # cast of a bf16 leaf
+    assert torch.equal(x.float().to(torch.bfloat16).float(), x.float())
+    h = torch.randn(64, 32, dtype=torch.float16, requires_grad=True)
+    assert not ok((h * 2).float())  # float16 source
+    f = torch.randn(64, 32, requires_grad=True)
+    assert not ok((f * 2).float())  # float32 -> float32 is no cast
+    y = (x * 2).float()
+    assert not ok(y.view(32, 64))  # a view: its own node
+    assert not ok((x * 2).float()[:, :16])
+    with torch.no_grad():
+        z = (x * 2).float()
+    assert not ok(z)  # no graph, no proof
+    w = (x * 2).float()
+    with torch.no_grad():
+        w.mul_(1.5)  # the node still reads ToCopyBackward0, the version does not
+    assert not ok(w)
+    assert not ok((x * 2).float() * 1.0)
 
 
 def _live_tensor_ids():

@@ -276,3 +276,35 @@ def test_save_modified_in_place_before_its_gather(batch) -> None:
     engine.drop(gid2, idx2)
     engine.synchronize()
     engine.close()
+
+
+def test_narrowed_float32_pieces_across_slots() -> None:
+    """bf16-exact float32 tensors packed narrowed (MO_TENSOR_BF16_HIGH), larger than a 2 MiB
+    slot so that their pieces split across slots (the tensor side of a later piece starts at
+    twice its payload offset), between plain tensors; every restore is bitwise."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(21)
+    handles, expected_bytes = [], 0
+    for k in range(6):
+        if k % 2 == 0:
+            n = 700_000 + 4099 * k  # 1.4 MB payload, 2.8 MB float32
+            bits = torch.randint(0, 1 << 16, (n,), generator=g, dtype=torch.int32) << 16
+            t = bits.view(torch.float32).to(device)
+            handles.append((t, *engine.pack(t, stream, narrow=True)))
+            expected_bytes += n * 2
+        else:
+            t = torch.randn(300_001, generator=g).to(device)
+            handles.append((t, *engine.pack(t, stream)))
+            expected_bytes += t.numel() * 4
+    engine.commit(stream)
+    for t, gid, idx in reversed(handles):
+        assert_bitwise(engine.restore(gid, idx, stream), t)
+    engine.synchronize()
+    assert engine.stats()["bytes_packed"] == expected_bytes
+    for _, gid, idx in handles:
+        engine.drop(gid, idx)
+    engine.synchronize()
+    engine.close()

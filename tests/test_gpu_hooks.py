@@ -333,3 +333,32 @@ def test_views_of_the_same_bytes_cross_the_link_once() -> None:
     y.sum().backward()
     assert _Recording.checked == 4
     torch.testing.assert_close(x.grad, torch.full_like(x, 2.0), rtol=0, atol=0)
+
+
+def test_bf16_casts_cross_narrowed_and_restore_bit_exact() -> None:
+    """Under bf16 autocast the harness's RMSNorm saves float32 casts of bfloat16 tokens. Those
+    cross the link as their high halves (MO_TENSOR_BF16_HIGH): fewer bytes packed, every
+    restored tensor still bitwise the save, and the step matches the run without offloading."""
+
+    device = torch.device("cuda", 0)
+    torch.manual_seed(914)
+    base = _tiny(layers=2, checkpointing=False, lora=True, dim=64, ffn=128).to(device).train()
+    latents, contexts = _inputs(device, seed=915, shapes=((4, 8, 8),), text=(12,))
+    expected = _run(copy.deepcopy(base), moss_offload.activation_cpu_offload, False, latents, contexts, autocast=True)
+    engine = moss_offload.get_engine(device)
+    packed = {}
+    try:
+        for narrow in (False, True):
+            engine.config.narrow_bf16_casts = narrow
+            engine.synchronize()
+            engine.reset_stats()
+            _Recording.log, _Recording.checked = {}, 0
+            actual = _run(copy.deepcopy(base), _recording_context, True, latents, contexts, autocast=True)
+            engine.synchronize()
+            packed[narrow] = engine.stats()["bytes_packed"]
+            assert _Recording.checked > 0  # every restore compared bitwise with its save
+            _compare(actual, expected, rtol=1e-3, atol=1e-5)
+    finally:
+        engine.config.narrow_bf16_casts = True
+    # two float32 casts per RMSNorm (square and scale), each crossing at half size
+    assert packed[True] < packed[False]

@@ -135,3 +135,48 @@ def test_empty_and_scalar() -> None:
     device = torch.device("cuda", 0)
     views = [torch.empty(0, 5, device=device), torch.tensor(3.5, device=device), torch.ones(1, 1, device=device)]
     _round_trip(views, device)
+
+
+def _bf16_exact_f32(n: int, device, seed: int) -> torch.Tensor:
+    """float32 values that are exactly bfloat16: every finite class plus NaNs with payloads."""
+
+    g = torch.Generator().manual_seed(seed)
+    bits = torch.randint(0, 1 << 16, (n,), generator=g, dtype=torch.int32)
+    special = torch.tensor([0x0000, 0x8000, 0x7F80, 0xFF80, 0x7FC0, 0x7F81, 0xFFFF, 0x0001, 0x807F, 0x3F80],
+                           dtype=torch.int32)  # +-0, +-inf, NaNs (quiet, signalling payloads), subnormals, 1.0
+    bits[: min(n, special.numel())] = special[: min(n, special.numel())]
+    return (bits << 16).view(torch.float32).to(device)
+
+
+@pytest.mark.parametrize("numel", [1, 7, 8, 1000, 8192, 8193, 3 * 8192 + 5, 1 << 20])
+def test_bf16_high_gather_keeps_the_high_halves_and_scatter_restores_the_bits(numel) -> None:
+    """MO_TENSOR_BF16_HIGH: the payload is the high 16 bits of each float32 element (the
+    oracle is the CPU's own bit shift), and the scatter restores every bit, NaN payloads,
+    infinities, signed zeros and subnormals included. Sizes cover partial chunks, the
+    element tail and several tiles."""
+
+    device = torch.device("cuda", 0)
+    lib = _native.load()
+    t = _bf16_exact_f32(numel, device, seed=numel)
+    plain = torch.randn(777, device=device)  # a normal piece in the same launch
+    views = [t, plain]
+    arr = (_native.MoTensor * 2)()
+    _native.describe(t, arr[0], flags=_native.MO_TENSOR_BF16_HIGH)
+    _native.describe(plain, arr[1])
+    offsets, total = _layout(lib, arr, 2)
+    assert offsets[1] - offsets[0] >= numel * 2 and total == offsets[1] + 777 * 4
+    payload = torch.full((total,), 0xC3, dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    _native.check("mo_gather", lib.mo_gather(arr, 2, payload.data_ptr(), None, stream))
+    host = payload.cpu()
+    expected = (t.cpu().view(torch.int32) >> 16).to(torch.int16).view(torch.uint8)
+    assert torch.equal(host[offsets[0] : offsets[0] + numel * 2], expected)
+    assert torch.equal(host[offsets[1] : offsets[1] + 777 * 4], plain.cpu().view(torch.uint8))
+    out = torch.full_like(t, float("nan"))
+    out_plain = torch.zeros_like(plain)
+    back = (_native.MoTensor * 2)()
+    _native.describe(out, back[0], flags=_native.MO_TENSOR_BF16_HIGH)
+    _native.describe(out_plain, back[1])
+    _native.check("mo_scatter", lib.mo_scatter(back, 2, payload.data_ptr(), None, stream))
+    assert_bitwise(out, t)
+    assert_bitwise(out_plain, plain)

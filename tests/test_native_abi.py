@@ -42,7 +42,7 @@ def _c_layouts(tmp_path: Path) -> dict[str, int]:
     """sizeof / offsetof of the ABI structs as the C compiler sees them."""
 
     fields = {
-        "mo_tensor": ["ptr", "elem_bytes", "ndim", "size", "stride"],
+        "mo_tensor": ["ptr", "elem_bytes", "ndim", "size", "stride", "flags", "reserved"],
         "mo_config": [f for f, _ in _native.MoConfig._fields_],
         "mo_ref": [f for f, _ in _native.MoRef._fields_],
         "mo_stats": [f for f, _ in _native.MoStats._fields_],
@@ -105,6 +105,39 @@ def test_payload_layout_offsets_and_errors() -> None:
     assert lib.mo_payload_layout(odd, 1, offsets, ctypes.byref(total)) == _native.MO_E_INVALID
     expanded = _descs([torch.zeros(5).expand(3, 5)])
     assert lib.mo_payload_layout(expanded, 1, offsets, ctypes.byref(total)) == _native.MO_E_LAYOUT
+
+
+def test_bf16_high_payload_is_half_size_and_only_for_contiguous_float32() -> None:
+    """MO_TENSOR_BF16_HIGH: the payload of a contiguous float32 tensor whose values are exact
+    bfloat16 keeps the high half of each element, numel x 2 bytes."""
+
+    lib = _native.load()
+    views = [torch.zeros(3, 5), torch.zeros(1000), torch.zeros(2, 8, 4)]
+    arr = _descs(views)
+    arr[1].flags = _native.MO_TENSOR_BF16_HIGH
+    arr[2].flags = _native.MO_TENSOR_BF16_HIGH
+    offsets = (ctypes.c_uint64 * 3)()
+    total = ctypes.c_uint64()
+    _native.check("mo_payload_layout", lib.mo_payload_layout(arr, 3, offsets, ctypes.byref(total)))
+    assert list(offsets) == [0, 256, 256 + 2048] and total.value == 256 + 2048 + 2 * 64
+    rejected = [
+        (torch.zeros(8, dtype=torch.bfloat16), _native.MO_E_INVALID),  # not float32
+        (torch.zeros(4, 8)[:, :6], _native.MO_E_LAYOUT),  # gaps between rows
+        (torch.zeros(16)[::2], _native.MO_E_LAYOUT),
+    ]
+    # a transposed view of a dense tensor is dense in storage order: accepted
+    dense_t = _descs([torch.zeros(4, 6).t()])
+    dense_t[0].flags = _native.MO_TENSOR_BF16_HIGH
+    _native.check("mo_payload_layout", lib.mo_payload_layout(dense_t, 1, offsets, ctypes.byref(total)))
+    assert total.value == 48
+    for view, code in rejected:
+        bad = _descs([view])
+        bad[0].flags = _native.MO_TENSOR_BF16_HIGH
+        assert lib.mo_payload_layout(bad, 1, offsets, ctypes.byref(total)) == code
+    unknown = _descs([torch.zeros(4)])
+    unknown[0].flags = 0x80
+    assert lib.mo_payload_layout(unknown, 1, offsets, ctypes.byref(total)) == _native.MO_E_INVALID
+    assert b"unknown tensor flags" in lib.mo_last_error()
 
 
 DRIVER = r"""
