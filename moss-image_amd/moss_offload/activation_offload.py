@@ -21,6 +21,7 @@ strides. Block boundaries come from forward hooks on ``model.layers``.
 
 from __future__ import annotations
 
+import weakref
 from contextlib import nullcontext
 from typing import ContextManager
 
@@ -177,6 +178,36 @@ class _OffloadedTensor:
                 pass
 
 
+class _DerivedTensor:
+    """Handle for a save that is recomputed on unpack instead of offloaded.
+
+    The save is an elementwise product of saves this context already holds (``torch.mul`` of two
+    tensors of one shape and dtype, or of a tensor and a Python number), or a dense view of
+    such a product. Unpack restores the inputs and replays the same ``torch.mul`` call: a
+    deterministic elementwise kernel on the same bits, so the result is the saved tensor bit
+    for bit, with no bytes over the host link. ``inputs`` are handles of this context
+    (offloaded, derived or resident tensors) that each hold their own reference.
+    """
+
+    __slots__ = ("inputs", "scalar", "shape", "stride")
+
+    def __init__(self, inputs, scalar, shape, stride):
+        self.inputs = inputs
+        self.scalar = scalar
+        self.shape = shape
+        self.stride = stride
+
+
+_VIEW_NODES = ("ViewBackward0", "UnsafeViewBackward0", "ReshapeAliasBackward0")
+
+
+def _numel(shape) -> int:
+    n = 1
+    for size in shape:
+        n *= size
+    return n
+
+
 class _ActivationOffload:
     """The context returned for an enabled offload: hooks + block boundaries + dedupe."""
 
@@ -192,6 +223,10 @@ class _ActivationOffload:
         }
         self.dedupe = self.engine.config.dedupe and StorageWeakRef is not None
         self.narrow = self.engine.config.narrow_bf16_casts
+        self.recompute = self.engine.config.recompute_products
+        # (autograd node, output index) -> (handle, weak ref, version at the save) of every save
+        # packed so far: the inputs a later product can be recomputed from
+        self._made: dict[tuple, tuple] = {}
         self._seen: dict[tuple, tuple] = {}
         self._shared: set[int] = set()  # groups holding saves made more than once
         self._hooks = torch.autograd.graph.saved_tensors_hooks(self.pack, self.unpack)
@@ -223,6 +258,7 @@ class _ActivationOffload:
                 handle.remove()
             self._block_handles.clear()
             self._seen.clear()
+            self._made.clear()
         stream = torch.cuda.current_stream(self.device).cuda_stream
         last = self.engine.commit(stream)
         if self.engine.config.prefetch and exc[0] is None:
@@ -268,6 +304,11 @@ class _ActivationOffload:
         device = tensor.device
         if source.numel() == 0:
             return _OffloadedTensor(None, None, 0, device, tensor.dtype, shape, stride, payload_shape)
+        if self.recompute:
+            derived = self._derive(tensor)
+            if derived is not None:
+                self._remember(tensor, derived)
+                return derived
         key = None
         if self.dedupe:
             # by payload bytes, not by view: any view of the same bytes in the same storage order
@@ -278,16 +319,113 @@ class _ActivationOffload:
                 ref, version, gid, idx = hit
                 if not ref.expired() and version == tensor._version and self.engine.acquire(gid, idx):
                     self._shared.add(gid)
-                    return _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
+                    handle = _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
+                    self._remember(tensor, handle)
+                    return handle
         stream = torch.cuda.current_stream(device).cuda_stream
         gid, idx = self.engine.pack(source, stream, narrow=self.narrow and _bf16_exact(tensor, source))
         if key is not None:
             self._seen[key] = (StorageWeakRef(tensor.untyped_storage()), tensor._version, gid, idx)
-        return _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
+        handle = _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
+        self._remember(tensor, handle)
+        return handle
+
+    # ------------------------------------------------------------------ recomputed products
+    def _remember(self, tensor: torch.Tensor, handle) -> None:
+        if self.recompute and tensor.grad_fn is not None:
+            meta = (tensor.dtype, tuple(tensor.shape), tensor.is_contiguous())
+            self._made[(tensor.grad_fn, tensor.output_nr)] = (handle, weakref.ref(tensor), tensor._version, meta)
+
+    def _held_input(self, edge):
+        """The handle and (dtype, shape, contiguous) of a product's input, if this context saved
+        it and, while the tensor lives, it is unchanged since (its version counter).
+
+        A freed input cannot change any more. Between its save and its death it could only have
+        been written in place, which autograd rejects in backward without offloading (the node
+        that saved it needs the saved value), so a step valid without offloading never does it;
+        the reference model's products (SiTU-GLU temporaries) are consumed at once."""
+
+        node, nr = edge
+        if node is None:
+            return None
+        rec = self._made.get((node, nr))
+        if rec is None:
+            return None
+        handle, ref, version, meta = rec
+        tensor = ref()
+        if tensor is not None and tensor._version != version:
+            return None
+        return handle, meta
+
+    def _own(self, handle):
+        """A reference of the derived handle's own to an input handle."""
+
+        if isinstance(handle, _OffloadedTensor) and handle.group is not None:
+            if not self.engine.acquire(handle.group, handle.entry):
+                return None
+            return _OffloadedTensor(handle.engine, handle.group, handle.entry, handle.device, handle.dtype,
+                                    handle.shape, handle.stride, handle.payload_shape)
+        return handle  # a derived handle (owns its inputs) or a resident tensor
+
+    def _derive(self, tensor: torch.Tensor) -> _DerivedTensor | None:
+        """A ``_DerivedTensor`` for ``tensor`` if it is the untouched output of a ``torch.mul``
+        (or a dense view of one) whose inputs this context saved unchanged, else None."""
+
+        fn = tensor.grad_fn
+        if fn is None or tensor._version != 0 or not tensor.is_contiguous():
+            return None
+        name = type(fn).__name__
+        if name in _VIEW_NODES:
+            # a view that covers its whole storage densely: the product it views, reshaped
+            if tensor.storage_offset() != 0 or tensor.numel() * tensor.element_size() != tensor.untyped_storage().nbytes():
+                return None
+            fn = fn.next_functions[0][0]
+            if fn is None or type(fn).__name__ != "MulBackward0":
+                return None
+        elif name != "MulBackward0":
+            return None
+        try:
+            edges = fn.next_functions
+            a = self._held_input(edges[0])
+            if a is None:
+                return None
+            if edges[1][0] is None:
+                # a Python number is saved as a 0-dim CPU tensor without the hooks; a tensor that
+                # went through them would be unpacked by reading it, so it is left alone
+                if fn._raw_saved_other.unpack_hook is not None:
+                    return None
+                other = fn._saved_other
+                if not (isinstance(other, torch.Tensor) and other.dim() == 0 and other.device.type == "cpu"):
+                    return None
+                scalar, inputs = other.item(), [a]
+            else:
+                b = self._held_input(edges[1])
+                if b is None:
+                    return None
+                scalar, inputs = None, [a, b]
+        except (AttributeError, IndexError, RuntimeError):  # private autograd API absent or changed
+            return None
+        numel = tensor.numel()
+        for _, (dtype, shape, contiguous) in inputs:
+            if dtype != tensor.dtype or not contiguous or _numel(shape) != numel:
+                return None
+        if len(inputs) == 2 and inputs[0][1][1] != inputs[1][1][1]:
+            return None
+        owned = []
+        for handle, _ in inputs:
+            mine = self._own(handle)
+            if mine is None:
+                return None
+            owned.append(mine)
+        return _DerivedTensor(tuple(owned), scalar, tuple(tensor.shape), tuple(tensor.stride()))
 
     def unpack(self, saved):
         if isinstance(saved, torch.Tensor):
             return saved
+        if isinstance(saved, _DerivedTensor):
+            args = [self.unpack(h) for h in saved.inputs]
+            product = torch.mul(args[0], saved.scalar if saved.scalar is not None else args[1])
+            return product.as_strided(saved.shape, saved.stride)
         if saved.group is None:
             restored = torch.empty_strided(saved.payload_shape, saved.stride, dtype=saved.dtype, device=saved.device)
         else:

@@ -56,6 +56,10 @@ class EngineConfig:
     # low 16 bits are zero) crosses the link as its high halves: the same bits in half the bytes
     # (MO_TENSOR_BF16_HIGH). The hook decides from the autograd graph; False copies it whole.
     narrow_bf16_casts: bool = True
+    # A save that is the output of torch.mul over saves already held (two tensors of one shape,
+    # or a tensor and a Python number), or a dense view of one, is recomputed on unpack by the
+    # same torch.mul instead of crossing the link. False offloads it like any other save.
+    recompute_products: bool = True
     # Saves made inside the last `keep_last_blocks` blocks of `model.layers` stay on the device
     # (0: offload every block, as the reference does). Backward needs them first, so offloading
     # them only sends them out and straight back; keeping them trades device memory for link

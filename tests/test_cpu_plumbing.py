@@ -232,3 +232,98 @@ def test_manifest_probe_leaves_gradients_unchanged() -> None:
     actual = _step(probed, latent, context, ManifestRecorder(probed, device_type="cpu"))
     for name in expected[2]:
         assert reference_hooks.bitwise_equal(actual[2][name], expected[2][name]), name
+
+
+class _StubEngine:
+    class config:
+        dedupe = True
+        narrow_bf16_casts = True
+        recompute_products = True
+        keep_last_blocks = 0
+
+    def acquire(self, gid, idx):
+        return True
+
+    def drop(self, gid, idx):
+        pass
+
+
+def _derive_context():
+    from moss_offload.activation_offload import _ActivationOffload
+
+    ctx = _ActivationOffload.__new__(_ActivationOffload)
+    ctx.engine = _StubEngine()
+    ctx.recompute = True
+    ctx._made = {}
+    return ctx
+
+
+def test_recomputed_products_are_found_from_the_graph() -> None:
+    """The rule of ``_ActivationOffload._derive``: a save is recomputed only when it is the
+    untouched output of ``torch.mul`` over saves already held (tensor x tensor of one shape, or
+    tensor x Python number), or a dense view of one. The activation is the reference's SiTU-GLU
+    (training/model.py:38)."""
+
+    from moss_offload.activation_offload import _DerivedTensor, _OffloadedTensor
+
+    ctx = _derive_context()
+
+    def held(t, gid):
+        h = _OffloadedTensor(None, gid, 0, t.device, t.dtype, tuple(t.shape), tuple(t.stride()), tuple(t.shape))
+        ctx._remember(t, h)
+        return h
+
+    gate = torch.randn(6, 16, dtype=torch.bfloat16, requires_grad=True) * 1.0
+    hidden = torch.randn(6, 16, dtype=torch.bfloat16, requires_grad=True) * 1.0
+    t1 = torch.tanh(gate / 4.0)
+    s = torch.sigmoid(gate)
+    t2 = torch.tanh(hidden / 25.0)
+    held(t1, 1), held(s, 2), held(t2, 3)
+    a4 = 4.0 * t1
+    d4 = ctx._derive(a4)
+    assert isinstance(d4, _DerivedTensor) and d4.scalar == 4.0 and len(d4.inputs) == 1
+    ctx._remember(a4, d4)
+    p = a4 * s
+    dp = ctx._derive(p)
+    assert isinstance(dp, _DerivedTensor) and dp.scalar is None and len(dp.inputs) == 2
+    ctx._remember(p, dp)
+    b25 = 25.0 * t2
+    d25 = ctx._derive(b25)
+    assert d25 is not None and d25.scalar == 25.0
+    ctx._remember(b25, d25)
+    y = p * b25  # not saved itself: only a view of it is
+    view = y.view(96)
+    dv = ctx._derive(view)
+    assert isinstance(dv, _DerivedTensor) and dv.shape == (96,)
+    # replaying the recorded muls gives the same bits
+    assert torch.equal((4.0 * t1.detach()).view(torch.int16), a4.detach().view(torch.int16))
+    # rejected: an input never saved; a product of a tensor not saved through the context
+    assert ctx._derive(torch.tanh(gate) * 3.0) is None
+    u = torch.randn(6, 16, dtype=torch.bfloat16, requires_grad=True) * 1.0
+    assert ctx._derive(t1 * u) is None
+    # rejected: a constant tensor operand (saved through the hooks in a real context)
+    c = torch.randn(6, 16, dtype=torch.bfloat16)
+    assert ctx._derive(t1 * c) is None
+    # rejected: broadcasting, a changed input, a written output, a partial view, non-mul ops
+    assert ctx._derive(t1 * s[:1]) is None
+    assert ctx._derive(t1 + s) is None
+    w = 2.0 * t2
+    with torch.no_grad():
+        w.add_(1.0)
+    assert ctx._derive(w) is None
+    assert ctx._derive(y[:3]) is None
+    with torch.no_grad():
+        t2.mul_(1.0)  # t2 changed after its save: products of it are no longer recomputable
+    assert ctx._derive(25.0 * t2) is None
+    # a freed input (a temporary, as in the reference's activation) still counts: only a handle
+    # of it is held
+    import weakref
+
+    t3 = torch.tanh(hidden)
+    held(t3, 4)
+    b3 = 3.0 * t3
+    key = (t3.grad_fn, t3.output_nr)
+    handle, _, version, meta = ctx._made[key]
+    ctx._made[key] = (handle, weakref.ref(torch.zeros(1)), version, meta)  # the referent is gone
+    assert ctx._made[key][1]() is None
+    assert ctx._derive(b3) is not None

@@ -18,7 +18,7 @@ import torch
 
 import moss_offload
 from moss_offload import dit
-from moss_offload.activation_offload import _ActivationOffload, _OffloadedTensor
+from moss_offload.activation_offload import _ActivationOffload, _DerivedTensor, _OffloadedTensor
 from oracle import reference_hooks
 
 from gpu_util import assert_bitwise, requires_gpu
@@ -34,13 +34,15 @@ class _Recording(_ActivationOffload):
 
     def pack(self, tensor):
         handle = super().pack(tensor)
-        if isinstance(handle, _OffloadedTensor):
+        if isinstance(handle, (_OffloadedTensor, _DerivedTensor)):
             _Recording.log[id(handle)] = tensor.detach().clone()
         return handle
 
     def unpack(self, saved):
         restored = super().unpack(saved)
-        if isinstance(saved, _OffloadedTensor):
+        # a derived save restores its inputs through handles of its own, which pack never
+        # returned: those are checked through the derived result
+        if isinstance(saved, (_OffloadedTensor, _DerivedTensor)) and id(saved) in _Recording.log:
             expected = _Recording.log[id(saved)]
             assert restored.shape == expected.shape and restored.stride() == saved.stride
             assert_bitwise(restored, expected)
@@ -362,3 +364,54 @@ def test_bf16_casts_cross_narrowed_and_restore_bit_exact() -> None:
         engine.config.narrow_bf16_casts = True
     # two float32 casts per RMSNorm (square and scale), each crossing at half size
     assert packed[True] < packed[False]
+
+
+def test_products_are_recomputed_not_offloaded_and_restore_bit_exact() -> None:
+    """The SiTU-GLU activation (reference training/model.py:38) saves 4 tanh(g/4), 25 tanh(h/25),
+    their product chain and a view of the result: products of saves already held. Those are
+    recomputed on unpack by the same torch.mul (no bytes over the link), every restore is bitwise
+    the save, and the step matches the run without offloading, in fp32 and under bf16 autocast."""
+
+    device = torch.device("cuda", 0)
+    torch.manual_seed(916)
+    base = _tiny(layers=2, checkpointing=False, lora=True, dim=64, ffn=128).to(device).train()
+    latents, contexts = _inputs(device, seed=917, shapes=((4, 8, 8),), text=(12,))
+    engine = moss_offload.get_engine(device)
+    for autocast in (False, True):
+        expected = _run(copy.deepcopy(base), moss_offload.activation_cpu_offload, False, latents, contexts,
+                        autocast=autocast)
+        packed, derived = {}, {}
+        try:
+            for recompute in (False, True):
+                engine.config.recompute_products = recompute
+                engine.synchronize()
+                engine.reset_stats()
+                _Recording.log, _Recording.checked = {}, 0
+                _derived_ids.clear()
+                actual = _run(copy.deepcopy(base), _recording_context, True, latents, contexts, autocast=autocast)
+                engine.synchronize()
+                packed[recompute] = engine.stats()["bytes_packed"]
+                assert _Recording.checked > 0
+                derived[recompute] = sum(1 for k in _Recording.log if k in _derived_ids)
+                if autocast:
+                    _compare(actual, expected, rtol=1e-3, atol=1e-5)
+                else:
+                    _compare(actual, expected, rtol=5e-5, atol=5e-6)
+        finally:
+            engine.config.recompute_products = True
+        assert packed[True] < packed[False]
+        assert derived[True] > 0 and derived[False] == 0
+
+
+_derived_ids: set = set()
+_base_pack = _Recording.pack
+
+
+def _pack_noting_derived(self, tensor):
+    handle = _base_pack(self, tensor)
+    if isinstance(handle, _DerivedTensor):
+        _derived_ids.add(id(handle))
+    return handle
+
+
+_Recording.pack = _pack_noting_derived
