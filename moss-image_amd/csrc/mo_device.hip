@@ -286,6 +286,40 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_unpack1_kernel(con
   mo::copy_tile<false>(d, blockIdx.x);
 }
 
+// Byte equality of two ranges (both 16-byte aligned), one 16 KiB tile per workgroup. Lanes
+// that see a difference write 1 to *flag (pinned host memory the host cleared before the
+// launch); equal ranges write nothing. The host reads the flag once an event recorded after
+// the launch has completed.
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_equal_kernel(const char* a, const char* b,
+                                                                            uint64_t nbytes, uint32_t* flag) {
+  using namespace mo;
+  const uint32_t tid = threadIdx.x;
+  const uint64_t tile_off = (uint64_t)blockIdx.x * kTileBytes;
+  const uint64_t left = nbytes - tile_off;
+  const char* const x = a + tile_off;
+  const char* const y = b + tile_off;
+  uint32_t diff = 0;
+  if (left >= kTileBytes) {
+    uint4 u[kUnroll], v[kUnroll];
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+      u[k] = ld16(x + (size_t)(k * kThreads + tid) * 16);
+      v[k] = ld16(y + (size_t)(k * kThreads + tid) * 16);
+    }
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) diff |= (u[k].x ^ v[k].x) | (u[k].y ^ v[k].y) | (u[k].z ^ v[k].z) | (u[k].w ^ v[k].w);
+  } else {
+    const uint32_t nvec = (uint32_t)(left / 16);
+    for (uint32_t c = tid; c < nvec; c += kThreads) {
+      const uint4 u = ld16(x + (size_t)c * 16), v = ld16(y + (size_t)c * 16);
+      diff |= (u.x ^ v.x) | (u.y ^ v.y) | (u.z ^ v.z) | (u.w ^ v.w);
+    }
+    for (uint32_t i = nvec * 16 + tid; i < (uint32_t)left; i += kThreads)
+      diff |= (uint32_t)(ld<kG, uint8_t>(x + i) ^ ld<kG, uint8_t>(y + i));
+  }
+  if (diff) st<kG>((char*)flag, 1u);
+}
+
 // Device <-> pinned-host copy through the shader engines instead of a DMA engine.
 // Each lane keeps kLinkUnroll 16-byte transfers in flight; the grid strides over the buffer.
 extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_link_copy_kernel(char* __restrict__ dst,

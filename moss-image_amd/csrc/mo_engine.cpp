@@ -301,6 +301,78 @@ struct Engine {
   std::deque<Timing> timings;
   mo_stats st{};
 
+  // ---- equality checks (mo_equal): a verdict word in pinned host memory + an event each ----
+  static constexpr uint32_t kEqualSlots = 64;
+  enum { kFree = 0, kRunning = 1, kAbandoned = 2 };
+  struct EqualSlot {
+    hipEvent_t ev = nullptr;
+    uint64_t gen = 0;
+    int state = kFree;
+  };
+  uint32_t* eq_flags = nullptr;  // kEqualSlots words, written by mo_equal_kernel
+  EqualSlot eq[kEqualSlots];
+  uint64_t eq_gen = 0;
+
+  int equal(uint64_t a, uint64_t b, uint64_t nbytes, hipStream_t stream, uint64_t* ticket) {
+    *ticket = 0;
+    if (a % 16 || b % 16) return fail(MO_E_INVALID, "mo_equal: addresses must be 16-byte aligned");
+    if (!eq_flags) {
+      void* p = nullptr;
+      MO_HIP(hipHostMalloc(&p, kEqualSlots * sizeof(uint32_t), hipHostMallocDefault));
+      eq_flags = (uint32_t*)p;
+    }
+    int slot = -1;
+    for (uint32_t i = 0; i < kEqualSlots && slot < 0; ++i) {
+      if (eq[i].state == kAbandoned && hipEventQuery(eq[i].ev) == hipSuccess) eq[i].state = kFree;
+      if (eq[i].state == kFree) slot = (int)i;
+    }
+    if (slot < 0) return 0;  // every slot waits for a verdict: no check, ticket 0
+    EqualSlot& q = eq[slot];
+    if (!q.ev) MO_HIP(hipEventCreateWithFlags(&q.ev, hipEventDisableTiming));
+    eq_flags[slot] = 0;
+    uint32_t* flag = nullptr;
+    MO_HIP(hipHostGetDevicePointer((void**)&flag, eq_flags, 0));
+    if (int rc = launch_equal((const void*)a, (const void*)b, nbytes, flag + slot, stream))
+      return hip_fail(rc, "equality kernel launch");
+    MO_HIP(hipEventRecord(q.ev, stream));
+    q.gen = ++eq_gen;
+    q.state = kRunning;
+    *ticket = (q.gen << 8) | (uint64_t)slot;
+    return 0;
+  }
+
+  EqualSlot* equal_slot(uint64_t ticket) {
+    const uint64_t slot = ticket & 0xff;
+    if (ticket == 0 || slot >= kEqualSlots || eq[slot].state != kRunning || eq[slot].gen != (ticket >> 8))
+      return nullptr;
+    return &eq[slot];
+  }
+
+  int equal_result(uint64_t ticket, int wait, int* state) {
+    EqualSlot* q = equal_slot(ticket);
+    if (!q) return fail(MO_E_INVALID, "mo_equal_result: unknown ticket " + std::to_string(ticket));
+    if (wait) {
+      MO_HIP(hipEventSynchronize(q->ev));
+    } else {
+      const hipError_t e = hipEventQuery(q->ev);
+      if (e == hipErrorNotReady) {
+        *state = 0;
+        return 0;
+      }
+      if (e != hipSuccess) return hip_fail((int)e, "hipEventQuery (equality check)");
+    }
+    *state = eq_flags[q - eq] ? 2 : 1;
+    q->state = kFree;
+    return 0;
+  }
+
+  int equal_discard(uint64_t ticket) {
+    EqualSlot* q = equal_slot(ticket);
+    if (!q) return fail(MO_E_INVALID, "mo_equal_discard: unknown ticket " + std::to_string(ticket));
+    q->state = kAbandoned;  // reused once its kernel has finished
+    return 0;
+  }
+
   // ---- pack/unpack kernel timing (MO_FLAG_KERNEL_TIMING) ----
   struct KernelTimer : LaunchTimer {
     Engine* e;
@@ -811,6 +883,12 @@ struct Engine {
     timings.clear();
     for (hipEvent_t e : timing_pool) (void)hipEventDestroy(e);
     timing_pool.clear();
+    for (auto& q : eq) {
+      if (q.ev) (void)hipEventDestroy(q.ev);
+      q = EqualSlot{};
+    }
+    if (eq_flags) (void)hipHostFree(eq_flags);
+    eq_flags = nullptr;
     for (auto& s : stage)
       if (s.dev) (void)hipFree(s.dev);
     for (auto& r : restore)
@@ -973,6 +1051,18 @@ int mo_pack_progress(mo_engine* engine, uint64_t* calls, uint64_t* launched) {
 }
 
 int mo_pack_flush(mo_engine* engine) { MO_ENGINE_CALL(engine, engine->e.flush_packs()); }
+
+int mo_equal(mo_engine* engine, uint64_t a, uint64_t b, uint64_t nbytes, uint64_t stream, uint64_t* ticket) {
+  if (!ticket) return mo::fail(MO_E_INVALID, "mo_equal: null output");
+  MO_ENGINE_CALL(engine, engine->e.equal(a, b, nbytes, (hipStream_t)stream, ticket));
+}
+
+int mo_equal_result(mo_engine* engine, uint64_t ticket, int wait, int* state) {
+  if (!state) return mo::fail(MO_E_INVALID, "mo_equal_result: null output");
+  MO_ENGINE_CALL(engine, engine->e.equal_result(ticket, wait, state));
+}
+
+int mo_equal_discard(mo_engine* engine, uint64_t ticket) { MO_ENGINE_CALL(engine, engine->e.equal_discard(ticket)); }
 
 int mo_commit(mo_engine* engine, uint64_t stream, uint64_t* group) {
   if (!group) return mo::fail(MO_E_INVALID, "mo_commit: null output");

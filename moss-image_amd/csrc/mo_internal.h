@@ -52,4 +52,7 @@ class Launcher {
 
 int launch_link_copy(void* dst, const void* src, uint64_t bytes, uint32_t blocks, hipStream_t stream);
 
+// mo_equal_kernel over nbytes at a and b (16-byte aligned); writes 1 to *flag on a difference.
+int launch_equal(const void* a, const void* b, uint64_t nbytes, uint32_t* flag, hipStream_t stream);
+
 }  // namespace mo

@@ -35,6 +35,7 @@ struct DeviceModule {
   hipModule_t module = nullptr;
   hipFunction_t pack = nullptr, unpack = nullptr, link = nullptr;
   hipFunction_t pack1 = nullptr, unpack1 = nullptr;  // single-piece launches
+  hipFunction_t equal = nullptr;
 };
 
 std::mutex g_modules_mu;
@@ -48,6 +49,7 @@ int load_functions(DeviceModule& m) {
   if ((e = hipModuleGetFunction(&m.link, m.module, "mo_link_copy_kernel")) != hipSuccess) return (int)e;
   if ((e = hipModuleGetFunction(&m.pack1, m.module, "mo_pack1_kernel")) != hipSuccess) return (int)e;
   if ((e = hipModuleGetFunction(&m.unpack1, m.module, "mo_unpack1_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.equal, m.module, "mo_equal_kernel")) != hipSuccess) return (int)e;
   return 0;
 }
 
@@ -233,6 +235,20 @@ int launch_link_copy(void* dst, const void* src, uint64_t bytes, uint32_t blocks
   uint64_t n = bytes;
   void* params[] = {&d, &s, &n};
   return (int)hipModuleLaunchKernel(fn, blocks, 1, 1, kThreads, 1, 1, 0, stream, params, nullptr);
+}
+
+int launch_equal(const void* a, const void* b, uint64_t nbytes, uint32_t* flag, hipStream_t stream) {
+  if (nbytes == 0) return 0;
+  const uint64_t tiles = (nbytes + kTileBytes - 1) / kTileBytes;
+  if (tiles * kThreads > UINT32_MAX) return (int)hipErrorInvalidValue;
+  DeviceModule m;
+  if (int rc = module_of_device(&m)) return rc;
+  const void* x = a;
+  const void* y = b;
+  uint64_t n = nbytes;
+  uint32_t* f = flag;
+  void* params[] = {&x, &y, &n, &f};
+  return (int)hipModuleLaunchKernel(m.equal, (uint32_t)tiles, 1, 1, kThreads, 1, 1, 0, stream, params, nullptr);
 }
 
 }  // namespace mo

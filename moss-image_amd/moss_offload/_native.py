@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 7
+MO_ABI_VERSION = 8
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -175,6 +175,9 @@ SIGNATURES: dict[str, tuple] = {
     "mo_pack": (ctypes.c_int, [ctypes.c_void_p, _P(MoTensor), ctypes.c_int, _u64, _P(MoRef)]),
     "mo_pack_progress": (ctypes.c_int, [ctypes.c_void_p, _P(_u64), _P(_u64)]),
     "mo_pack_flush": (ctypes.c_int, [ctypes.c_void_p]),
+    "mo_equal": (ctypes.c_int, [ctypes.c_void_p, _u64, _u64, _u64, _u64, _P(_u64)]),
+    "mo_equal_result": (ctypes.c_int, [ctypes.c_void_p, _u64, ctypes.c_int, _P(ctypes.c_int)]),
+    "mo_equal_discard": (ctypes.c_int, [ctypes.c_void_p, _u64]),
     "mo_commit": (ctypes.c_int, [ctypes.c_void_p, _u64, _P(_u64)]),
     "mo_prefetch": (ctypes.c_int, [ctypes.c_void_p, _u64, _u64]),
     "mo_unpack": (ctypes.c_int, [ctypes.c_void_p, _u64, _P(_u64), ctypes.c_uint32, _u64]),

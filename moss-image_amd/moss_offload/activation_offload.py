@@ -21,6 +21,7 @@ strides. Block boundaries come from forward hooks on ``model.layers``.
 
 from __future__ import annotations
 
+import threading
 import weakref
 from contextlib import nullcontext
 from typing import ContextManager
@@ -198,6 +199,64 @@ class _DerivedTensor:
         self.stride = stride
 
 
+_SETTLE_LOCK = threading.Lock()
+_ALIAS_MIN_BYTES = 1 << 20  # smaller casts are offloaded: the check would cost more than the copy
+
+
+class _CheckedAlias:
+    """Handle for a save compared, on the device, with an earlier save of this context that has
+    the same origin: a second cast of the same autograd output (the two ``tokens.float()`` of
+    RMSNorm, ``training/model.py:171``). The graph cannot prove such casts equal (the source may
+    have been written under ``no_grad`` in between), so the engine compares the bytes
+    (``mo_equal``) while this handle keeps the save alive. Equal: ``target`` (a reference to
+    the earlier save's entry) restores it and the save is let go. Different: the save stays on
+    the device as saved, like a layout the reference keeps resident."""
+
+    __slots__ = ("engine", "ticket", "target", "tensor")
+
+    def __init__(self, engine, ticket, target, tensor):
+        self.engine = engine
+        self.ticket = ticket
+        self.target = target
+        self.tensor = tensor
+
+    def settle(self, wait: bool) -> bool:
+        """Take the verdict if it is known (or ``wait``); True once settled."""
+
+        with _SETTLE_LOCK:  # forward polls on the caller's thread, unpack on autograd's
+            if self.ticket:
+                state = self.engine.equal_result(self.ticket, wait)
+                if state == 0:
+                    return False
+                self.ticket = 0
+                if state == 1:
+                    self.tensor = None
+                else:
+                    self.target = None
+            return True
+
+    def __del__(self):
+        if self.ticket:
+            try:
+                self.engine.equal_discard(self.ticket)
+            except Exception:  # interpreter shutdown or engine already closed
+                pass
+
+
+def _cast_origin(tensor: torch.Tensor):
+    """``(autograd node, output index)`` of the tensor a cast was made from, if ``tensor`` is
+    the untouched output of a dtype cast (``ToCopyBackward0``) of a tensor that requires grad."""
+
+    fn = tensor.grad_fn
+    if fn is None or tensor._version != 0 or type(fn).__name__ != "ToCopyBackward0":
+        return None
+    try:
+        edge = fn.next_functions[0]
+    except (AttributeError, IndexError, RuntimeError):  # private autograd API absent or changed
+        return None
+    return edge if edge[0] is not None else None
+
+
 _VIEW_NODES = ("ViewBackward0", "UnsafeViewBackward0", "ReshapeAliasBackward0")
 
 
@@ -224,6 +283,11 @@ class _ActivationOffload:
         self.dedupe = self.engine.config.dedupe and StorageWeakRef is not None
         self.narrow = self.engine.config.narrow_bf16_casts
         self.recompute = self.engine.config.recompute_products
+        self.alias = getattr(self.engine.config, "alias_equal_casts", False)
+        # cast origin (autograd node, output index) -> (handle, weak ref, version, stream) of an
+        # offloaded cast, and the aliases whose device comparison has no verdict yet
+        self._casts: dict[tuple, tuple] = {}
+        self._pending: list[_CheckedAlias] = []
         # (autograd node, output index) -> (handle, weak ref, version at the save) of every save
         # packed so far: the inputs a later product can be recomputed from
         self._made: dict[tuple, tuple] = {}
@@ -259,6 +323,8 @@ class _ActivationOffload:
             self._block_handles.clear()
             self._seen.clear()
             self._made.clear()
+            self._casts.clear()
+            self._poll()
         stream = torch.cuda.current_stream(self.device).cuda_stream
         last = self.engine.commit(stream)
         if self.engine.config.prefetch and exc[0] is None:
@@ -304,11 +370,20 @@ class _ActivationOffload:
         device = tensor.device
         if source.numel() == 0:
             return _OffloadedTensor(None, None, 0, device, tensor.dtype, shape, stride, payload_shape)
+        if self._pending:
+            self._poll()
         if self.recompute:
             derived = self._derive(tensor)
             if derived is not None:
                 self._remember(tensor, derived)
                 return derived
+        stream = torch.cuda.current_stream(device).cuda_stream
+        origin = _cast_origin(tensor) if self.alias else None
+        if origin is not None:
+            alias = self._alias(tensor, origin, stream)
+            if alias is not None:
+                self._remember(tensor, alias)
+                return alias
         key = None
         if self.dedupe:
             # by payload bytes, not by view: any view of the same bytes in the same storage order
@@ -322,13 +397,49 @@ class _ActivationOffload:
                     handle = _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
                     self._remember(tensor, handle)
                     return handle
-        stream = torch.cuda.current_stream(device).cuda_stream
         gid, idx = self.engine.pack(source, stream, narrow=self.narrow and _bf16_exact(tensor, source))
         if key is not None:
             self._seen[key] = (StorageWeakRef(tensor.untyped_storage()), tensor._version, gid, idx)
         handle = _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
         self._remember(tensor, handle)
+        if origin is not None:
+            self._casts[origin] = (handle, weakref.ref(tensor), tensor._version, stream)
         return handle
+
+    # ------------------------------------------------------------------ equal casts
+    def _alias(self, tensor: torch.Tensor, origin, stream: int) -> _CheckedAlias | None:
+        """A ``_CheckedAlias`` of an earlier offloaded cast of the same origin, with the device
+        comparison of the two started, if that cast is still alive, unchanged and laid out
+        the same; else None."""
+
+        rec = self._casts.get(origin)
+        if rec is None:
+            return None
+        handle, ref, version, rec_stream = rec
+        earlier = ref()
+        if earlier is None or earlier._version != version or earlier is tensor:
+            return None
+        if tensor.numel() * tensor.element_size() < _ALIAS_MIN_BYTES:
+            return None
+        if (earlier.dtype != tensor.dtype or earlier.shape != tensor.shape or not tensor.is_contiguous()
+                or not earlier.is_contiguous() or tensor.data_ptr() % 16 or earlier.data_ptr() % 16):
+            return None
+        # the comparison runs on the stream the earlier cast was offloaded from, which orders it
+        # before any reuse of that cast's memory once the engine lets go of it
+        if stream != rec_stream:
+            return None
+        target = self._own(handle)
+        if target is None:
+            return None
+        ticket = self.engine.equal(earlier, tensor, stream)
+        if not ticket:
+            return None
+        alias = _CheckedAlias(self.engine, ticket, target, tensor)
+        self._pending.append(alias)
+        return alias
+
+    def _poll(self) -> None:
+        self._pending = [alias for alias in self._pending if not alias.settle(False)]
 
     # ------------------------------------------------------------------ recomputed products
     def _remember(self, tensor: torch.Tensor, handle) -> None:
@@ -426,6 +537,9 @@ class _ActivationOffload:
             args = [self.unpack(h) for h in saved.inputs]
             product = torch.mul(args[0], saved.scalar if saved.scalar is not None else args[1])
             return product.as_strided(saved.shape, saved.stride)
+        if isinstance(saved, _CheckedAlias):
+            saved.settle(True)
+            return saved.tensor if saved.tensor is not None else self.unpack(saved.target)
         if saved.group is None:
             restored = torch.empty_strided(saved.payload_shape, saved.stride, dtype=saved.dtype, device=saved.device)
         else:

@@ -60,6 +60,11 @@ class EngineConfig:
     # or a tensor and a Python number), or a dense view of one, is recomputed on unpack by the
     # same torch.mul instead of crossing the link. False offloads it like any other save.
     recompute_products: bool = True
+    # A save that is a cast of the same autograd output as a cast already offloaded (RMSNorm's
+    # two tokens.float(), say) is compared with it on the device (mo_equal); if the bytes are
+    # equal it restores from the earlier save's payload, else it stays on the device as saved.
+    # False offloads it like any other save.
+    alias_equal_casts: bool = True
     # Saves made inside the last `keep_last_blocks` blocks of `model.layers` stay on the device
     # (0: offload every block, as the reference does). Backward needs them first, so offloading
     # them only sends them out and straight back; keeping them trades device memory for link
@@ -240,6 +245,32 @@ class OffloadEngine:
             _native.check("mo_pack_flush", self._lib.mo_pack_flush(self._handle))
             if self._held:
                 self._hold()
+
+    # ------------------------------------------------------------------ equality checks
+    def equal(self, a: torch.Tensor, b: torch.Tensor, stream: int) -> int:
+        """Start a device-side byte comparison of two dense tensors of one size on ``stream``;
+        returns its ticket, or 0 when no check could be started. Both must stay unchanged
+        until the verdict is known."""
+
+        ticket = _native._u64(0)
+        with self._lock:
+            _native.check("mo_equal", self._lib.mo_equal(
+                self._handle, a.data_ptr(), b.data_ptr(), a.numel() * a.element_size(), stream,
+                ctypes.byref(ticket)))
+        return ticket.value
+
+    def equal_result(self, ticket: int, wait: bool) -> int:
+        """0 while the check runs (``wait`` False), 1 equal, 2 different; 1 and 2 free the ticket."""
+
+        state = ctypes.c_int(0)
+        with self._lock:
+            _native.check("mo_equal_result", self._lib.mo_equal_result(
+                self._handle, ticket, 1 if wait else 0, ctypes.byref(state)))
+        return state.value
+
+    def equal_discard(self, ticket: int) -> None:
+        with self._lock:
+            _native.check("mo_equal_discard", self._lib.mo_equal_discard(self._handle, ticket))
 
     # ------------------------------------------------------------------ backward
     def restore(self, gid: int, idx: int, stream: int) -> torch.Tensor:

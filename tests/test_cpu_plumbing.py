@@ -21,6 +21,7 @@
 from __future__ import annotations
 
 import copy
+import weakref
 import gc
 from contextlib import nullcontext
 
@@ -235,17 +236,36 @@ def test_manifest_probe_leaves_gradients_unchanged() -> None:
 
 
 class _StubEngine:
+    """Bookkeeping of the device engine, with the byte comparison done at once on the CPU."""
+
     class config:
         dedupe = True
         narrow_bf16_casts = True
         recompute_products = True
+        alias_equal_casts = True
         keep_last_blocks = 0
+
+    def __init__(self):
+        self.verdicts = {}
+        self.discarded = []
 
     def acquire(self, gid, idx):
         return True
 
     def drop(self, gid, idx):
         pass
+
+    def equal(self, a, b, stream):
+        ticket = len(self.verdicts) + len(self.discarded) + 1
+        same = a.numel() == b.numel() and torch.equal(a.reshape(-1).view(torch.uint8), b.reshape(-1).view(torch.uint8))
+        self.verdicts[ticket] = 1 if same else 2
+        return ticket
+
+    def equal_result(self, ticket, wait):
+        return self.verdicts.pop(ticket)
+
+    def equal_discard(self, ticket):
+        self.discarded.append(self.verdicts.pop(ticket))
 
 
 def _derive_context():
@@ -254,7 +274,10 @@ def _derive_context():
     ctx = _ActivationOffload.__new__(_ActivationOffload)
     ctx.engine = _StubEngine()
     ctx.recompute = True
+    ctx.alias = True
     ctx._made = {}
+    ctx._casts = {}
+    ctx._pending = []
     return ctx
 
 
@@ -327,3 +350,62 @@ def test_recomputed_products_are_found_from_the_graph() -> None:
     ctx._made[key] = (handle, weakref.ref(torch.zeros(1)), version, meta)  # the referent is gone
     assert ctx._made[key][1]() is None
     assert ctx._derive(b3) is not None
+
+
+def test_equal_casts_are_aliased_only_after_the_bytes_compare_equal() -> None:
+    """The rule of ``_ActivationOffload._alias``: a second cast of the same autograd output as
+    an offloaded cast (RMSNorm's two ``tokens.float()``, training/model.py:171) is compared with
+    it on the device; equal bytes restore from the first cast's entry, different bytes keep the
+    save itself. The graph alone cannot tell: a write under ``no_grad`` between the casts
+    leaves both casts' nodes pointing at the same output."""
+
+    from moss_offload.activation_offload import _CheckedAlias, _OffloadedTensor, _cast_origin
+
+    def offloaded(ctx, t, gid):
+        h = _OffloadedTensor(None, gid, 0, t.device, t.dtype, tuple(t.shape), tuple(t.stride()), tuple(t.shape))
+        ctx._casts[_cast_origin(t)] = (h, weakref.ref(t), t._version, 0)
+        return h
+
+    tokens = torch.randn(512, 1024, dtype=torch.bfloat16, requires_grad=True) * 1.0
+    ctx = _derive_context()
+    second = tokens.float()  # saved first (by square's node in RMSNorm)
+    h = offloaded(ctx, second, 7)
+    first = tokens.float()
+    assert _cast_origin(first) == _cast_origin(second)
+    alias = ctx._alias(first, _cast_origin(first), 0)
+    assert isinstance(alias, _CheckedAlias) and alias.tensor is first and ctx._pending == [alias]
+    assert alias.settle(False) and alias.tensor is None and alias.target.group == h.group
+    # a write between the casts that autograd does not see: the bytes differ, the save stays
+    ctx = _derive_context()
+    second = tokens.float()
+    offloaded(ctx, second, 8)
+    with torch.no_grad():
+        tokens.add_(1.0)
+    first = tokens.float()
+    alias = ctx._alias(first, _cast_origin(first), 0)
+    assert alias is not None and alias.settle(True) and alias.target is None and alias.tensor is first
+    # rejected: the earlier cast freed or written, another stream, another shape, a small cast
+    ctx = _derive_context()
+    offloaded(ctx, tokens.float(), 9)  # freed at once
+    assert ctx._alias(tokens.float(), _cast_origin(tokens.float()), 0) is None
+    second = tokens.float()
+    offloaded(ctx, second, 10)
+    assert ctx._alias(tokens.float(), _cast_origin(second), 1) is None
+    with torch.no_grad():
+        second.mul_(1.0)
+    assert ctx._alias(tokens.float(), _cast_origin(second), 0) is None
+    part = tokens[:256].float()
+    offloaded(ctx, tokens[:256].float(), 11)
+    assert ctx._alias(tokens.float(), _cast_origin(part), 0) is None
+    small = torch.randn(64, 64, dtype=torch.bfloat16, requires_grad=True) * 1.0
+    kept = small.float()
+    offloaded(ctx, kept, 12)
+    assert ctx._alias(small.float(), _cast_origin(kept), 0) is None
+    # an alias dropped before its verdict gives its ticket back
+    ctx = _derive_context()
+    second = tokens.float()
+    offloaded(ctx, second, 13)
+    alias = ctx._alias(tokens.float(), _cast_origin(second), 0)
+    ctx._pending.clear()
+    del alias
+    assert ctx.engine.discarded == [1]

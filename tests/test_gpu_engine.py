@@ -308,3 +308,59 @@ def test_narrowed_float32_pieces_across_slots() -> None:
         engine.drop(gid, idx)
     engine.synchronize()
     engine.close()
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 + 5, 16 * 1024, 16 * 1024 + 48, 3 * MiB + 7, 54 * MiB])
+def test_equal_reports_equal_and_any_single_byte_difference(nbytes) -> None:
+    """mo_equal: equal ranges report 1; one flipped byte at the start, in the middle or in the
+    last (tail) byte reports 2. Buffers are exactly nbytes long (plus nothing), so a read past
+    the range would show up as a fault, not a verdict."""
+
+    engine = _engine()
+    device = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device=device).manual_seed(nbytes)
+    a = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=device, generator=g)
+    try:
+        for where in (None, 0, nbytes // 2, nbytes - 1):
+            b = a.clone()
+            if where is not None:
+                b[where] ^= 0x10
+            ticket = engine.equal(a, b, stream)
+            assert ticket != 0
+            assert engine.equal_result(ticket, wait=True) == (1 if where is None else 2), where
+        # polling: 0 until known, then the verdict once
+        ticket = engine.equal(a, a.clone(), stream)
+        torch.cuda.synchronize()
+        assert engine.equal_result(ticket, wait=False) == 1
+        with pytest.raises(RuntimeError):
+            engine.equal_result(ticket, wait=False)
+    finally:
+        engine.close()
+
+
+def test_equal_tickets_run_out_and_come_back() -> None:
+    """64 verdict slots: a 65th check starts nothing (ticket 0); a discarded ticket's slot and a
+    reported one's are reused."""
+
+    engine = _engine()
+    device = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    a = torch.arange(4096, dtype=torch.int32, device=device)
+    b = a.clone()
+    try:
+        tickets = [engine.equal(a, b, stream) for _ in range(64)]
+        assert all(tickets) and len(set(tickets)) == 64
+        assert engine.equal(a, b, stream) == 0
+        engine.equal_discard(tickets[0])
+        torch.cuda.synchronize()
+        again = engine.equal(a, b, stream)
+        assert again != 0 and again not in tickets
+        for t in tickets[1:] + [again]:
+            assert engine.equal_result(t, wait=True) == 1
+        with pytest.raises(RuntimeError):
+            engine.equal_discard(tickets[0])
+        with pytest.raises(RuntimeError):
+            engine.equal(a[1:], b, stream)  # 4-byte offset: not 16-byte aligned
+    finally:
+        engine.close()

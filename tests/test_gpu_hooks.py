@@ -18,7 +18,12 @@ import torch
 
 import moss_offload
 from moss_offload import dit
-from moss_offload.activation_offload import _ActivationOffload, _DerivedTensor, _OffloadedTensor
+from moss_offload.activation_offload import (
+    _ActivationOffload,
+    _CheckedAlias,
+    _DerivedTensor,
+    _OffloadedTensor,
+)
 from oracle import reference_hooks
 
 from gpu_util import assert_bitwise, requires_gpu
@@ -32,9 +37,11 @@ class _Recording(_ActivationOffload):
     log: dict = {}
     checked = 0
 
+    kinds = (_OffloadedTensor, _DerivedTensor, _CheckedAlias)
+
     def pack(self, tensor):
         handle = super().pack(tensor)
-        if isinstance(handle, (_OffloadedTensor, _DerivedTensor)):
+        if isinstance(handle, _Recording.kinds):
             _Recording.log[id(handle)] = tensor.detach().clone()
         return handle
 
@@ -42,9 +49,11 @@ class _Recording(_ActivationOffload):
         restored = super().unpack(saved)
         # a derived save restores its inputs through handles of its own, which pack never
         # returned: those are checked through the derived result
-        if isinstance(saved, (_OffloadedTensor, _DerivedTensor)) and id(saved) in _Recording.log:
+        if isinstance(saved, _Recording.kinds) and id(saved) in _Recording.log:
             expected = _Recording.log[id(saved)]
-            assert restored.shape == expected.shape and restored.stride() == saved.stride
+            # an alias stands for a dense cast: its save's strides are the clone's
+            stride = saved.stride if hasattr(saved, "stride") else expected.stride()
+            assert restored.shape == expected.shape and restored.stride() == stride
             assert_bitwise(restored, expected)
             _Recording.checked += 1
         return restored
@@ -407,11 +416,90 @@ _derived_ids: set = set()
 _base_pack = _Recording.pack
 
 
+_made_handles: list = []  # aliases returned by pack, in order
+
+
 def _pack_noting_derived(self, tensor):
     handle = _base_pack(self, tensor)
     if isinstance(handle, _DerivedTensor):
         _derived_ids.add(id(handle))
+    if isinstance(handle, _CheckedAlias):
+        _made_handles.append(handle)
     return handle
 
 
 _Recording.pack = _pack_noting_derived
+
+
+def test_equal_casts_restore_bit_exact() -> None:
+    """Under bf16 autocast each RMSNorm of the harness block saves two float32 casts of the same
+    bfloat16 tokens (reference training/model.py:171). The second restores from the first one's
+    entry once the device has found the bytes equal: fewer bytes packed, every restore bitwise
+    the save, and the step matches the run without offloading."""
+
+    device = torch.device("cuda", 0)
+    torch.manual_seed(918)
+    # dim 512 and 640 joint tokens: a float32 cast of [T, D] is 1.3 MB, above the aliasing floor
+    # of 1 MiB (the text adapter's 64-token casts stay below it)
+    base = _tiny(layers=2, checkpointing=False, lora=True, dim=512, ffn=1024, heads=8).to(device).train()
+    latents, contexts = _inputs(device, seed=919, shapes=((4, 24, 24),), text=(64,))
+    expected = _run(copy.deepcopy(base), moss_offload.activation_cpu_offload, False, latents, contexts, autocast=True)
+    engine = moss_offload.get_engine(device)
+    packed, made = {}, {}
+    try:
+        for on in (False, True):
+            engine.config.alias_equal_casts = on
+            engine.synchronize()
+            engine.reset_stats()
+            _Recording.log, _Recording.checked = {}, 0
+            _made_handles.clear()
+            actual = _run(copy.deepcopy(base), _recording_context, True, latents, contexts, autocast=True)
+            engine.synchronize()
+            packed[on] = engine.stats()["bytes_packed"]
+            made[on] = len(_made_handles)
+            # every alias settles as equal: the casts it stands for were never written
+            assert all(h.settle(True) and h.tensor is None and h.target is not None for h in _made_handles)
+            assert _Recording.checked > 0
+            _compare(actual, expected, rtol=1e-3, atol=1e-5)
+    finally:
+        _made_handles.clear()
+        engine.config.alias_equal_casts = True
+    # at least the q- and k-norms of both blocks (bfloat16 inputs); one cast of each pair moves
+    assert made[False] == 0 and made[True] >= 4, made
+    assert packed[True] < packed[False]
+
+
+def test_cast_written_between_casts_stays_resident_and_matches() -> None:
+    """Two casts of one tensor with a ``no_grad`` write in between share an autograd origin but
+    not their bytes: the device comparison finds the difference, the second cast stays on the
+    device as saved, and the gradients are bitwise those of the run without hooks."""
+
+    device = torch.device("cuda", 0)
+    model = _tiny().to(device)
+    g = torch.Generator(device=device).manual_seed(920)
+    x0 = torch.randn(512, 1024, device=device, generator=g).to(torch.bfloat16)
+
+    def step(context):
+        x = x0.clone().requires_grad_(True)
+        t = x * 1.0
+        with context:
+            b = t.float()
+            y1 = b.square()  # saves b, offloaded
+            with torch.no_grad():
+                t.add_(1.0)  # not seen by either cast's node
+            a = t.float()
+            y2 = a.square()  # saves a: same origin as b, other bytes
+        (y1.sum() + y2.sum()).backward()
+        return x.grad
+
+    expected = step(torch.enable_grad())
+    _Recording.log, _Recording.checked = {}, 0
+    _made_handles.clear()
+    got = step(_Recording(model, device))
+    aliases = [h for h in _made_handles if isinstance(h, _CheckedAlias)]
+    _made_handles.clear()
+    assert len(aliases) == 1
+    alias = aliases[0]
+    assert alias.ticket == 0 and alias.target is None and alias.tensor is not None
+    assert _Recording.checked == 2
+    assert_bitwise(got, expected)
