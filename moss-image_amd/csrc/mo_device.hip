@@ -20,7 +20,8 @@
 //           in half the bytes.
 //
 // Grid: one 256-lane workgroup per 16 KiB tile of payload; tiles of all pieces of the
-// launch are numbered consecutively and a workgroup finds its piece with a scalar search.
+// launch are numbered consecutively and a workgroup finds its piece from the launch's array
+// of piece start tiles.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -256,12 +257,14 @@ __device__ __forceinline__ void copy_tile(const KDesc& d, uint32_t tile) {
   }
 }
 
-// Several pieces: the workgroup finds its piece with a scalar search over the descriptors.
+// Several pieces: the workgroup's piece is the last one starting at or before its tile. The
+// starts are one contiguous array (unused entries UINT32_MAX), compared without branches.
 template <bool kPack>
 __device__ __forceinline__ void copy_body(const LaunchArgs& args) {
   const uint32_t tile = blockIdx.x;
   uint32_t i = 0;
-  while (i + 1 < args.ndesc && args.d[i + 1].tile0 <= tile) ++i;
+#pragma unroll
+  for (int k = 1; k < kMaxDesc; ++k) i += args.tile0[k] <= tile ? 1u : 0u;
   copy_tile<kPack>(args.d[i], tile);
 }
 

@@ -44,6 +44,9 @@ struct KDesc {
 struct LaunchArgs {
   uint32_t ndesc;
   uint32_t pad;
+  // d[i].tile0 for i < ndesc, UINT32_MAX after: contiguous, so a workgroup finds its piece with
+  // one 64-byte scalar load instead of a chain of dependent loads over the descriptors
+  uint32_t tile0[kMaxDesc];
   KDesc d[kMaxDesc];
 };
 static_assert(sizeof(LaunchArgs) <= 4096, "kernel arguments must fit in 4 KiB");

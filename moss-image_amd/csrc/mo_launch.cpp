@@ -177,6 +177,7 @@ int make_kdesc(const Canon& c, uint64_t tensor_base, uint64_t first, uint64_t nb
 Launcher::Launcher(bool pack, hipStream_t stream, LaunchTimer* timer) : pack_(pack), stream_(stream), timer_(timer) {
   args_.ndesc = 0;
   args_.pad = 0;
+  for (auto& t : args_.tile0) t = UINT32_MAX;
 }
 
 void Launcher::add(const KDesc& kd) {
@@ -185,6 +186,7 @@ void Launcher::add(const KDesc& kd) {
   KDesc& slot = args_.d[args_.ndesc];
   slot = kd;
   slot.tile0 = tiles_;
+  args_.tile0[args_.ndesc] = tiles_;
   const uint64_t t = (kd.nbytes + kTileBytes - 1) / kTileBytes;
   tiles_ += (uint32_t)t;
   bytes_ += kd.nbytes;
@@ -216,6 +218,7 @@ int Launcher::flush() {
     launches_++;
     if (e == hipSuccess && t0) timer_->launched(pending_bytes_, pending_hbm_);
   }
+  for (uint32_t k = 0; k < args_.ndesc; ++k) args_.tile0[k] = UINT32_MAX;
   args_.ndesc = 0;
   tiles_ = 0;
   pending_bytes_ = 0;
