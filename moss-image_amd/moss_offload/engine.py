@@ -252,11 +252,13 @@ class OffloadEngine:
         returns its ticket, or 0 when no check could be started. Both must stay unchanged
         until the verdict is known."""
 
+        nbytes = a.numel() * a.element_size()
+        if nbytes != b.numel() * b.element_size() or not (a.is_contiguous() and b.is_contiguous()):
+            raise ValueError("equal() compares two contiguous tensors of the same byte size")
         ticket = _native._u64(0)
         with self._lock:
             _native.check("mo_equal", self._lib.mo_equal(
-                self._handle, a.data_ptr(), b.data_ptr(), a.numel() * a.element_size(), stream,
-                ctypes.byref(ticket)))
+                self._handle, a.data_ptr(), b.data_ptr(), nbytes, stream, ctypes.byref(ticket)))
         return ticket.value
 
     def equal_result(self, ticket: int, wait: bool) -> int:

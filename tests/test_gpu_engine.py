@@ -361,6 +361,8 @@ def test_equal_tickets_run_out_and_come_back() -> None:
         with pytest.raises(RuntimeError):
             engine.equal_discard(tickets[0])
         with pytest.raises(RuntimeError):
-            engine.equal(a[1:], b, stream)  # 4-byte offset: not 16-byte aligned
+            engine.equal(a[1:], b[:-1], stream)  # 4-byte offset: not 16-byte aligned
+        with pytest.raises(ValueError):
+            engine.equal(a[1:], b, stream)  # sizes differ
     finally:
         engine.close()
