@@ -43,7 +43,8 @@ extern "C" {
 #define MO_E_STATE 1004     /* call not valid in the engine's current state */
 
 /* Flags for mo_config.flags. */
-#define MO_FLAG_TIMING 0x1         /* KERNEL_COPY link: time every copy with HIP events   */
+#define MO_FLAG_TIMING 0x1         /* time every copy: HIP events (KERNEL_COPY link), or the
+                                      SDMA engines' own start/end stamps (SDMA link)      */
 #define MO_FLAG_KERNEL_COPY 0x2    /* move D2H/H2D with a copy kernel on HIP streams instead
                                       of the SDMA engines (comparison; contends for CUs)   */
 #define MO_FLAG_KERNEL_TIMING 0x4  /* time every pack/unpack launch with HIP events       */

@@ -853,6 +853,7 @@ struct Engine {
       link = make_sdma_link(device, cfg.d2h_engine, cfg.h2d_engine, err, &status);
     }
     if (!link) return fail(status ? status : MO_E_STATE, "creating the host link failed: " + err);
+    if (cfg.flags & MO_FLAG_TIMING) (void)link->use_dma_timestamps();
     stage.resize(cfg.stage_slots);
     for (auto& s : stage) {
       MO_HIP(hipMalloc(&s.dev, cfg.stage_slot_bytes));

@@ -75,6 +75,9 @@ struct SdmaCopy : CopyState {
   bool counted_h2d = false;  // counted in g_h2d_inflight until finished
   bool counted_d2h = false;  // counted in d2h_inflight_ until finished (worker thread only)
   bool part_failed = false;  // a half failed or timed out (worker thread only)
+  // DMA-engine stamps over the copy's parts, HSA system clock (worker thread only)
+  uint64_t dma_start = UINT64_MAX, dma_end = 0;
+  bool dma_stamped = true;  // every part completed with stamps
   bool done() const override { return finished.load(std::memory_order_acquire); }
   bool failed() const override { return fail.load(std::memory_order_acquire); }
 };
@@ -282,6 +285,20 @@ class SdmaLink : public Link {
     return 0;
   }
 
+  bool use_dma_timestamps() override {
+    // Async-copy profiling is a process-wide switch of the HSA runtime; the stamps land in each
+    // copy's completion signal.
+    static std::once_flag once;
+    static bool enabled = false;
+    std::call_once(once, [] { enabled = hsa_amd_profiling_async_copy_enable(true) == HSA_STATUS_SUCCESS; });
+    uint64_t hz = 0;
+    if (!enabled || hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP_FREQUENCY, &hz) != HSA_STATUS_SUCCESS || !hz)
+      return false;
+    ns_per_tick_ = 1e9 / (double)hz;
+    dma_time_.store(true, std::memory_order_release);
+    return true;
+  }
+
   void stats(LinkStats* out) override {
     out->d2h_bytes = d2h_bytes_;
     out->h2d_bytes = h2d_bytes_;
@@ -400,10 +417,18 @@ class SdmaLink : public Link {
       c->fail.store(true, std::memory_order_release);
       failures_++;
     } else {
-      // Engine-busy time: copies on one engine run back to back, so a copy starts at the later
-      // of its issue and the previous completion in its direction.
-      const int64_t start = c->issue_ns > last_done_ns_[dir] ? c->issue_ns : last_done_ns_[dir];
-      busy_ns_[dir] += t > start ? (uint64_t)(t - start) : 0;
+      if (dma_time_.load(std::memory_order_acquire) && c->dma_stamped && c->dma_end > c->dma_start) {
+        // Engine-busy time from the engines' own stamps: the part of [start, end] not already
+        // counted for the direction (copies of one direction may overlap on two engines).
+        const uint64_t s = std::max(c->dma_start, last_dma_end_[dir]);
+        busy_ns_[dir] += c->dma_end > s ? (uint64_t)((double)(c->dma_end - s) * ns_per_tick_) : 0;
+        last_dma_end_[dir] = std::max(last_dma_end_[dir], c->dma_end);
+      } else {
+        // Host clock: copies on one engine run back to back, so a copy starts at the later of
+        // its issue and the previous completion in its direction.
+        const int64_t start = c->issue_ns > last_done_ns_[dir] ? c->issue_ns : last_done_ns_[dir];
+        busy_ns_[dir] += t > start ? (uint64_t)(t - start) : 0;
+      }
       done_bytes_[dir] += c->bytes;
       last_done_ns_[dir] = t;
     }
@@ -480,6 +505,18 @@ class SdmaLink : public Link {
     for (auto it = inflight_.begin(); it != inflight_.end();) {
       const hsa_signal_value_t v = hsa_signal_load_scacquire(it->sig);
       if (v < 1) {
+        if (v == 0 && dma_time_.load(std::memory_order_acquire)) {
+          // read before the signal is reused: it holds the stamps of its last copy
+          SdmaCopy& c = *it->copy;
+          hsa_amd_profiling_async_copy_time_t tm{};
+          if (hsa_amd_profiling_get_async_copy_time(it->sig, &tm) == HSA_STATUS_SUCCESS && tm.start &&
+              tm.end >= tm.start) {
+            c.dma_start = std::min<uint64_t>(c.dma_start, tm.start);
+            c.dma_end = std::max<uint64_t>(c.dma_end, tm.end);
+          } else {
+            c.dma_stamped = false;
+          }
+        }
         part_done(it->copy, v < 0);
         sig_pool_.push_back(it->sig);
         it = inflight_.erase(it);
@@ -584,6 +621,9 @@ class SdmaLink : public Link {
   std::vector<InFlight> inflight_;
   std::vector<hsa_signal_t> sig_pool_;
   int64_t last_done_ns_[2] = {0, 0};
+  std::atomic<bool> dma_time_{false};
+  double ns_per_tick_ = 1.0;
+  uint64_t last_dma_end_[2] = {0, 0};
 
   std::atomic<int> inflight_count_{0};
   std::atomic<uint64_t> failures_{0};

@@ -66,6 +66,9 @@ class Link {
   virtual int consumed(int gate, hipStream_t compute) = 0;
   // Block until every copy issued so far finished.
   virtual int synchronize() = 0;
+  // Time copies by the DMA engine's own start and end stamps instead of the host clock at
+  // issue and completion. False if the transport cannot (it keeps the host clock).
+  virtual bool use_dma_timestamps() { return false; }
   virtual void stats(LinkStats* out) = 0;
   virtual void reset_stats() = 0;
   virtual const char* name() const = 0;
