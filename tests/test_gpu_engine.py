@@ -366,3 +366,33 @@ def test_equal_tickets_run_out_and_come_back() -> None:
             engine.equal(a[1:], b, stream)  # sizes differ
     finally:
         engine.close()
+
+
+def test_timed_link_rate_is_bounded_by_the_host_clock() -> None:
+    """With timing on, the SDMA link times copies by the DMA engines' own stamps. Their busy time
+    can be no longer than the host's view of the same copies (issue to observed completion) and
+    must give a rate a PCIe x16 link can carry: between 10 and 70 GB/s for the 2 MiB segment
+    copies of this small-slot engine."""
+
+    import time
+
+    engine = _engine(timing=True)
+    device = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    src = torch.randint(0, 256, (32 * MiB,), dtype=torch.uint8, device=device)
+    try:
+        engine.synchronize()
+        engine.reset_stats()
+        t0 = time.perf_counter()
+        for _ in range(8):
+            engine.pack(src, stream)
+            engine.commit(stream)
+        engine.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3
+        st = engine.stats()
+        assert st["timed_d2h_bytes"] == 8 * 32 * MiB
+        assert 0 < st["d2h_ms"] <= wall_ms
+        rate = st["timed_d2h_bytes"] / st["d2h_ms"] / 1e6
+        assert 10 < rate < 70, rate
+    finally:
+        engine.close()
