@@ -178,17 +178,17 @@ int mo_pack_flush(mo_engine* engine);
 
 /* Byte equality of nbytes at device addresses a and b (both 16-byte aligned), checked by a
  * kernel on `stream` after the work already queued there; nothing blocks. *ticket receives a
- * handle for the verdict, or 0 when all 64 verdict slots are taken (no check was started).
- * The caller keeps both ranges unchanged until the verdict is known.
+ * handle for the result, or 0 when all 64 result slots are taken (no check was started).
+ * The caller keeps both ranges unchanged until the result is known.
  * No reference counterpart: the hooks use it to store a saved tensor that equals an earlier
  * save (two casts of one tensor, for instance) once, where the reference copies both. */
 int mo_equal(mo_engine* engine, uint64_t a, uint64_t b, uint64_t nbytes, uint64_t stream, uint64_t* ticket);
 
 /* *state = 0 while the check runs (wait == 0), 1 if the ranges were equal, 2 if they differed.
- * wait != 0 blocks until the verdict is known. A ticket reports 1 or 2 once and is then freed. */
+ * wait != 0 blocks until the result is known. A ticket reports 1 or 2 once and is then freed. */
 int mo_equal_result(mo_engine* engine, uint64_t ticket, int wait, int* state);
 
-/* Give up a ticket whose verdict is no longer wanted; its slot is reused once the check ends. */
+/* Give up a ticket whose result is no longer wanted; its slot is reused once the check ends. */
 int mo_equal_discard(mo_engine* engine, uint64_t ticket);
 
 /* Close the open group: the compute stream records an event, the D2H stream waits for it and

@@ -301,7 +301,7 @@ struct Engine {
   std::deque<Timing> timings;
   mo_stats st{};
 
-  // ---- equality checks (mo_equal): a verdict word in pinned host memory + an event each ----
+  // ---- equality checks (mo_equal): a result word in pinned host memory + an event each ----
   static constexpr uint32_t kEqualSlots = 64;
   enum { kFree = 0, kRunning = 1, kAbandoned = 2 };
   struct EqualSlot {
@@ -326,7 +326,7 @@ struct Engine {
       if (eq[i].state == kAbandoned && hipEventQuery(eq[i].ev) == hipSuccess) eq[i].state = kFree;
       if (eq[i].state == kFree) slot = (int)i;
     }
-    if (slot < 0) return 0;  // every slot waits for a verdict: no check, ticket 0
+    if (slot < 0) return 0;  // every slot waits for a result: no check, ticket 0
     EqualSlot& q = eq[slot];
     if (!q.ev) MO_HIP(hipEventCreateWithFlags(&q.ev, hipEventDisableTiming));
     eq_flags[slot] = 0;

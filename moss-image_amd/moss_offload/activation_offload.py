@@ -221,7 +221,7 @@ class _CheckedAlias:
         self.tensor = tensor
 
     def settle(self, wait: bool) -> bool:
-        """Take the verdict if it is known (or ``wait``); True once settled."""
+        """Take the result if it is known (or ``wait``); True once settled."""
 
         with _SETTLE_LOCK:  # forward polls on the caller's thread, unpack on autograd's
             if self.ticket:
@@ -285,7 +285,7 @@ class _ActivationOffload:
         self.recompute = self.engine.config.recompute_products
         self.alias = getattr(self.engine.config, "alias_equal_casts", False)
         # cast origin (autograd node, output index) -> (handle, weak ref, version, stream) of an
-        # offloaded cast, and the aliases whose device comparison has no verdict yet
+        # offloaded cast, and the aliases whose device comparison has no result yet
         self._casts: dict[tuple, tuple] = {}
         self._pending: list[_CheckedAlias] = []
         # (autograd node, output index) -> (handle, weak ref, version at the save) of every save

@@ -250,7 +250,7 @@ class OffloadEngine:
     def equal(self, a: torch.Tensor, b: torch.Tensor, stream: int) -> int:
         """Start a device-side byte comparison of two dense tensors of one size on ``stream``;
         returns its ticket, or 0 when no check could be started. Both must stay unchanged
-        until the verdict is known."""
+        until the result is known."""
 
         nbytes = a.numel() * a.element_size()
         if nbytes != b.numel() * b.element_size() or not (a.is_contiguous() and b.is_contiguous()):

@@ -246,7 +246,7 @@ class _StubEngine:
         keep_last_blocks = 0
 
     def __init__(self):
-        self.verdicts = {}
+        self.results = {}
         self.discarded = []
 
     def acquire(self, gid, idx):
@@ -256,16 +256,16 @@ class _StubEngine:
         pass
 
     def equal(self, a, b, stream):
-        ticket = len(self.verdicts) + len(self.discarded) + 1
+        ticket = len(self.results) + len(self.discarded) + 1
         same = a.numel() == b.numel() and torch.equal(a.reshape(-1).view(torch.uint8), b.reshape(-1).view(torch.uint8))
-        self.verdicts[ticket] = 1 if same else 2
+        self.results[ticket] = 1 if same else 2
         return ticket
 
     def equal_result(self, ticket, wait):
-        return self.verdicts.pop(ticket)
+        return self.results.pop(ticket)
 
     def equal_discard(self, ticket):
-        self.discarded.append(self.verdicts.pop(ticket))
+        self.discarded.append(self.results.pop(ticket))
 
 
 def _derive_context():
@@ -401,7 +401,7 @@ def test_equal_casts_are_aliased_only_after_the_bytes_compare_equal() -> None:
     kept = small.float()
     offloaded(ctx, kept, 12)
     assert ctx._alias(small.float(), _cast_origin(kept), 0) is None
-    # an alias dropped before its verdict gives its ticket back
+    # an alias dropped before its result gives its ticket back
     ctx = _derive_context()
     second = tokens.float()
     offloaded(ctx, second, 13)

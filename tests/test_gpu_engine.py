@@ -313,8 +313,8 @@ def test_narrowed_float32_pieces_across_slots() -> None:
 @pytest.mark.parametrize("nbytes", [16, 4096 + 5, 16 * 1024, 16 * 1024 + 48, 3 * MiB + 7, 54 * MiB])
 def test_equal_reports_equal_and_any_single_byte_difference(nbytes) -> None:
     """mo_equal: equal ranges report 1; one flipped byte at the start, in the middle or in the
-    last (tail) byte reports 2. Buffers are exactly nbytes long (plus nothing), so a read past
-    the range would show up as a fault, not a verdict."""
+    last (tail) byte reports 2. Buffers are exactly nbytes long, so the kernel's tail handling
+    is exercised at every size, full tiles, partial tiles and a trailing partial 16-byte word."""
 
     engine = _engine()
     device = torch.device("cuda", 0)
@@ -329,7 +329,7 @@ def test_equal_reports_equal_and_any_single_byte_difference(nbytes) -> None:
             ticket = engine.equal(a, b, stream)
             assert ticket != 0
             assert engine.equal_result(ticket, wait=True) == (1 if where is None else 2), where
-        # polling: 0 until known, then the verdict once
+        # polling: 0 until known, then the result once
         ticket = engine.equal(a, a.clone(), stream)
         torch.cuda.synchronize()
         assert engine.equal_result(ticket, wait=False) == 1
@@ -340,7 +340,7 @@ def test_equal_reports_equal_and_any_single_byte_difference(nbytes) -> None:
 
 
 def test_equal_tickets_run_out_and_come_back() -> None:
-    """64 verdict slots: a 65th check starts nothing (ticket 0); a discarded ticket's slot and a
+    """64 result slots: a 65th check starts nothing (ticket 0); a discarded ticket's slot and a
     reported one's are reused."""
 
     engine = _engine()
