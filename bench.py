@@ -612,7 +612,7 @@ def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
         return start.elapsed_time(stop) / 1e3 / iters
 
     shapes = {}
-    block = {"hip": 0.0, "eager": 0.0}
+    block = {"hip": 0.0, "fused": 0.0, "eager": 0.0}
     block_flop = 0.0
     for name, ((out_f, in_f), count) in C5_GEMMS.items():
         x = torch.randn(rows, in_f, device=device, generator=g).to(torch.bfloat16)
@@ -624,6 +624,8 @@ def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
         t = {
             "hip_fwd": timed(lambda: qk.int8_linear_forward(x, w, s)),
             "hip_bwd": timed(lambda: qk.int8_linear_backward(dy, w, s, x.shape)),
+            "fused_fwd": timed(lambda: qk.int8_linear_forward(x, w, s, path="fused")),
+            "fused_bwd": timed(lambda: qk.int8_linear_backward(dy, w, s, x.shape, path="fused")),
             "eager_fwd": timed(lambda: F.linear(x, qk.decode(w, s, torch.bfloat16))),
             "eager_bwd": timed(lambda: dy.matmul(qk.decode(w, s, torch.bfloat16))),
         }
@@ -639,17 +641,23 @@ def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
         rec["bwd_vs_eager_max_rel_diff"] = ((gh - ge).abs().max() / ge.abs().max()).item()
         shapes[name] = rec
         block["hip"] += count * (t["hip_fwd"] + t["hip_bwd"])
+        block["fused"] += count * (t["fused_fwd"] + t["fused_bwd"])
         block["eager"] += count * (t["eager_fwd"] + t["eager_bwd"])
         block_flop += count * 2 * flop
         log(f"int8 GEMM {name} ({out_f}x{in_f}, {rows} rows): hip fwd {rec['hip_fwd_tflops']} bwd "
-            f"{rec['hip_bwd_tflops']} | eager fwd {rec['eager_fwd_tflops']} bwd {rec['eager_bwd_tflops']} TFLOP/s")
+            f"{rec['hip_bwd_tflops']} | fused fwd {rec['fused_fwd_tflops']} bwd {rec['fused_bwd_tflops']} | "
+            f"eager fwd {rec['eager_fwd_tflops']} bwd {rec['eager_bwd_tflops']} TFLOP/s")
         del x, dy, w, s, wd, yh, ye, gh, ge
     achieved = block_flop / block["hip"] / 1e12
     return {
         "shapes": shapes,
         "block_ms": {k: round(v * 1e3, 3) for k, v in block.items()},
         "block_speedup_vs_eager": round(block["eager"] / block["hip"], 4),
-        "roofline": {"bound": "mfma", "kernels": "mo_int8_linear_{fwd,bwd}_{large,small}",
+        "fused_block_speedup_vs_eager": round(block["eager"] / block["fused"], 4),
+        "library_rows": qk.LIBRARY_ROWS,
+        "roofline": {"bound": "mfma",
+                     "kernels": (f"mo_int8_decode_kernel + library GEMM (rows >= {qk.LIBRARY_ROWS}), "
+                                 "mo_int8_linear_{fwd,bwd}_{large,small} below"),
                      "workload": "one config-5 joint block: 4 x qkvo + ffn_up_gate + ffn_down, forward and "
                                  f"input gradient, {rows} rows",
                      "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",

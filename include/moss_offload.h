@@ -282,6 +282,14 @@ int mo_streamer_reset_stats(mo_streamer* streamer);
 
 /* ---- int8 weight-only linear (training/quant_kernels.py:100-228, quantization.py:27-65) ----- */
 
+/* The decoded weight bf16(q * bf16(scale)) of an int8 weight [out_features][in_features] (fp32
+ * per-row scale) written to `out` (bf16, same shape), on `stream`; in_features a multiple of 16,
+ * weight and out 16-byte aligned. This is one pass in place of the reference eager path's decode
+ * (quant_kernels.py:126-131, cast then scale). Calls with many rows take it and a library GEMM
+ * instead of the fused kernels below. */
+int mo_int8_decode(uint64_t w, uint64_t scale, uint64_t out, uint32_t out_features, uint32_t in_features,
+                   uint64_t stream);
+
 /* y[rows][out] = x[rows][in] . decode(w)^T (+ bias), on bf16 MFMA with fp32 accumulation, where
  * decode(w)[n][k] = bf16(w[n][k] * bf16(scale[n])), the decode of quant_kernels.py:126-131.
  * x, y, bias: bf16 (bias may be 0); w: int8 [out][in] row-major; scale: fp32 [out].

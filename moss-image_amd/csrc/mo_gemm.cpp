@@ -36,6 +36,7 @@ struct GemmModule {
   int cus = 0;
   // [backward][small][tail]
   Kernel k[2][2][2];
+  hipFunction_t decode = nullptr;  // mo_int8_decode_kernel
 };
 
 std::mutex g_mu;
@@ -64,6 +65,8 @@ int gemm_module(GemmModule* out) {
           k.tile = small ? kSmall : kLarge;
           k.threads = small ? 256 : (bwd ? 256 : 512);  // waves of each configuration x 64
         }
+    if ((e = hipModuleGetFunction(&m.decode, m.module, "mo_int8_decode_kernel")) != hipSuccess)
+      return mo::set_hip_error((int)e, "hipModuleGetFunction (int8 decode)");
     it = g_modules.emplace(device, m).first;
   }
   *out = it->second;
@@ -129,6 +132,27 @@ int launch(const Kernel& k, void** params, uint32_t rows, uint32_t cols, uint64_
 }  // namespace
 
 extern "C" {
+
+int mo_int8_decode(uint64_t w, uint64_t scale, uint64_t out, uint32_t out_features, uint32_t in_features,
+                   uint64_t stream) {
+  if (!w || !scale || !out) return mo::set_error(MO_E_INVALID, "null pointer");
+  if (out_features == 0 || in_features == 0) return mo::set_error(MO_E_INVALID, "empty weight");
+  if (in_features % 16) return mo::set_error(MO_E_INVALID, "in_features must be a multiple of 16");
+  if ((w | out) % 16 || scale % 4) return mo::set_error(MO_E_INVALID, "misaligned pointer");
+  if ((uint64_t)in_features * out_features >= (1ull << 31)) return mo::set_error(MO_E_INVALID, "weight too large");
+  GemmModule m;
+  if (int rc = gemm_module(&m)) return rc;
+  const uint64_t chunks = (uint64_t)out_features * (in_features / 16);
+  const void* q = (const void*)w;
+  const void* sc = (const void*)scale;
+  void* o = (void*)out;
+  uint32_t rows = out_features, cols = in_features;
+  void* params[] = {&q, &sc, &o, &rows, &cols};
+  const hipError_t e = hipModuleLaunchKernel(m.decode, (uint32_t)((chunks + 255) / 256), 1, 1, 256, 1, 1, 0,
+                                             (hipStream_t)stream, params, nullptr);
+  if (e != hipSuccess) return mo::set_hip_error((int)e, "int8 decode launch");
+  return 0;
+}
 
 int mo_int8_linear_forward(uint64_t x, uint64_t w, uint64_t scale, uint64_t bias, uint64_t y, uint32_t rows,
                            uint32_t in_features, uint32_t out_features, uint64_t stream) {

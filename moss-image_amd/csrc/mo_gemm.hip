@@ -407,3 +407,40 @@ MO_GEMM_BWD(mo_int8_linear_bwd_large, mo_gemm::BwdLarge, true, 6)
 MO_GEMM_BWD(mo_int8_linear_bwd_large_tail, mo_gemm::BwdLarge, false, 6)
 MO_GEMM_BWD(mo_int8_linear_bwd_small, mo_gemm::Small, true, 6)
 MO_GEMM_BWD(mo_int8_linear_bwd_small_tail, mo_gemm::Small, false, 6)
+
+// The decoded weight W' = bf16(q * bf16(scale)) written out whole, for calls with enough rows
+// that one decode per call costs less than the fused kernels' in-tile decode: a library GEMM
+// then takes W' as a plain bf16 operand. One lane per 16 weights of a row (cols % 16 == 0):
+// a 16-byte int8 load and two 16-byte bf16 stores; the same decode() as the fused kernels.
+extern "C" __global__ __launch_bounds__(256) void mo_int8_decode_kernel(const int8_t* q, const float* scale,
+                                                                        __bf16* out, uint32_t rows,
+                                                                        uint32_t cols) {
+  using u32x4 = unsigned int __attribute__((ext_vector_type(4)));
+  const uint32_t per_row = cols / 16;
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;  // chunk of 16 weights
+  if (i >= rows * per_row) return;
+  const uint32_t r = i / per_row;
+  const float s = (float)(__bf16)scale[r];
+  const u32x4 v = *(const u32x4*)(q + (size_t)i * 16);
+  u32x4 lo, hi;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t packed[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const unsigned short a = __builtin_bit_cast(unsigned short, mo_gemm::decode(v[w], 2 * h, s));
+      const unsigned short b = __builtin_bit_cast(unsigned short, mo_gemm::decode(v[w], 2 * h + 1, s));
+      packed[h] = (uint32_t)a | ((uint32_t)b << 16);
+    }
+    if (w < 2) {
+      lo[2 * w] = packed[0];
+      lo[2 * w + 1] = packed[1];
+    } else {
+      hi[2 * (w - 2)] = packed[0];
+      hi[2 * (w - 2) + 1] = packed[1];
+    }
+  }
+  u32x4* dst = (u32x4*)(out + (size_t)i * 16);
+  dst[0] = lo;
+  dst[1] = hi;
+}

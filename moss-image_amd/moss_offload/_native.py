@@ -210,6 +210,7 @@ SIGNATURES: dict[str, tuple] = {
     "mo_gradacc_wait": (ctypes.c_int, [ctypes.c_void_p, _u64]),
     "mo_gradacc_get_stats": (ctypes.c_int, [ctypes.c_void_p, _P(MoGradaccStats)]),
     "mo_gradacc_reset_stats": (ctypes.c_int, [ctypes.c_void_p]),
+    "mo_int8_decode": (ctypes.c_int, [_u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32, _u64]),
     "mo_int8_linear_forward": (ctypes.c_int, [_u64, _u64, _u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32,
                                               ctypes.c_uint32, _u64]),
     "mo_int8_linear_backward": (ctypes.c_int, [_u64, _u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32,

@@ -3,7 +3,9 @@
 
 The GEMMs are hand-written gfx950 kernels in ``csrc/mo_gemm.hip`` (bf16 MFMA, int8 tiles
 decoded to bf16 on their way into LDS), reached through ``mo_int8_linear_forward`` and
-``mo_int8_linear_backward``. Backend selection mirrors the reference's ``auto | eager | triton``
+``mo_int8_linear_backward``. From ``LIBRARY_ROWS`` rows up, a call instead decodes the weight
+in one HIP pass (``mo_int8_decode``) and runs the same library GEMM as the eager path, bit for
+bit equal to it and faster by the decode. Backend selection mirrors the reference's ``auto | eager | triton``
 with ``hip`` in place of ``triton``: ``auto`` takes the HIP kernels whenever the call is
 supported (bf16 activations and weight dtype on a HIP device, int8 weights, fp32 scales,
 feature sizes multiples of 16, contiguous operands) and the eager path otherwise; an explicit
@@ -76,6 +78,35 @@ def decode(weight: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> tor
     return weight.to(dtype) * scale.to(dtype)[:, None]
 
 
+# From this many rows up, a call decodes the weight once (mo_int8_decode) and runs the library
+# GEMM on it; below, the fused kernels decode the int8 tiles in LDS. The fused kernels decode each
+# weight tile again for every row tile, and their MFMA loop runs below the library's on these
+# shapes. At 17 792 rows (config 5), for one joint block, the decode-once path took 9.65 ms
+# against 10.77 ms fused and 9.79 ms for the eager path. The one-pass decode takes 7.9 / 35 /
+# 20 us for qkvo / up_gate / down, against 34 / 225 / 100 us for the eager cast-then-scale. At
+# 4096 rows the decode is still under a tenth of the GEMM; fewer rows keep the fused kernels,
+# which read the int8 weight only.
+LIBRARY_ROWS = 4096
+PATHS = ("auto", "fused", "library")
+
+
+def decode_hip(weight: torch.Tensor, scale: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``decode(weight, scale, bfloat16)`` in one HIP pass (``mo_int8_decode``), bit for bit."""
+
+    lib = _native.load()
+    out_features, in_features = weight.shape
+    out = _output(out, (out_features, in_features), weight.device, "decoded-weight")
+    _native.check("mo_int8_decode", lib.mo_int8_decode(weight.data_ptr(), scale.data_ptr(), out.data_ptr(),
+                                                       out_features, in_features, _stream(weight)))
+    return out
+
+
+def _library(rows: int, path: str) -> bool:
+    if path not in PATHS:
+        raise ValueError(f"path must be one of {PATHS}")
+    return path == "library" or (path == "auto" and rows >= LIBRARY_ROWS)
+
+
 def _stream(tensor: torch.Tensor) -> int:
     return torch.cuda.current_stream(tensor.device).cuda_stream
 
@@ -90,8 +121,11 @@ def _output(out: torch.Tensor | None, shape: tuple[int, int], device: torch.devi
 
 
 def int8_linear_forward(tokens: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
-                        bias: torch.Tensor | None = None, *, out: torch.Tensor | None = None) -> torch.Tensor:
-    """``tokens @ decode(weight).T (+ bias)`` on the HIP kernel; the call must be supported."""
+                        bias: torch.Tensor | None = None, *, out: torch.Tensor | None = None,
+                        path: str = "auto") -> torch.Tensor:
+    """``tokens @ decode(weight).T (+ bias)``; the call must be supported. ``path``: ``fused`` (the
+    MFMA kernels), ``library`` (``decode_hip``, then the same ``addmm``/``mm`` as the reference's
+    eager path, bit for bit), ``auto`` (library from ``LIBRARY_ROWS`` rows up)."""
 
     lib = _native.load()
     matrix = tokens.reshape(-1, tokens.shape[-1]).contiguous()
@@ -100,6 +134,13 @@ def int8_linear_forward(tokens: torch.Tensor, weight: torch.Tensor, scale: torch
     out = _output(out, (rows, out_features), tokens.device, "output")
     if bias is not None:
         bias = bias.to(torch.bfloat16).contiguous()
+    if _library(rows, path):
+        decoded = decode_hip(weight, scale)
+        if bias is None:
+            torch.mm(matrix, decoded.t(), out=out)
+        else:
+            torch.addmm(bias, matrix, decoded.t(), out=out)
+        return out.reshape(*tokens.shape[:-1], out_features)
     _native.check(
         "mo_int8_linear_forward",
         lib.mo_int8_linear_forward(matrix.data_ptr(), weight.data_ptr(), scale.data_ptr(),
@@ -110,14 +151,19 @@ def int8_linear_forward(tokens: torch.Tensor, weight: torch.Tensor, scale: torch
 
 
 def int8_linear_backward(gradient: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
-                         input_shape: torch.Size, *, out: torch.Tensor | None = None) -> torch.Tensor:
-    """``gradient @ decode(weight)``: the input gradient of the frozen int8 linear."""
+                         input_shape: torch.Size, *, out: torch.Tensor | None = None,
+                         path: str = "auto") -> torch.Tensor:
+    """``gradient @ decode(weight)``: the input gradient of the frozen int8 linear (``path`` as in
+    ``int8_linear_forward``)."""
 
     lib = _native.load()
     matrix = gradient.reshape(-1, gradient.shape[-1]).to(torch.bfloat16).contiguous()
     rows, out_features = matrix.shape
     in_features = weight.shape[1]
     out = _output(out, (rows, in_features), gradient.device, "input-gradient")
+    if _library(rows, path):
+        torch.mm(matrix, decode_hip(weight, scale), out=out)
+        return out.reshape(input_shape)
     _native.check(
         "mo_int8_linear_backward",
         lib.mo_int8_linear_backward(matrix.data_ptr(), weight.data_ptr(), scale.data_ptr(), out.data_ptr(), rows,

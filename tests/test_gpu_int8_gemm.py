@@ -17,6 +17,7 @@ import copy
 
 import pytest
 import torch
+import torch.nn.functional as F
 
 from moss_offload import dit, quant_kernels
 
@@ -100,7 +101,7 @@ PLAN_SHAPES = [(4096, 4096, 4096), (4096, 1040, 4096), (17792, 3072, 3072), (177
 @pytest.mark.parametrize("rows,in_f,out_f", PLAN_SHAPES)
 def test_forward_launch_plans_match_fp64_reference(rows, in_f, out_f) -> None:
     x, w, scale, b = _operands(rows, in_f, out_f, seed=rows + in_f + 3 * out_f, bias=True)
-    y = quant_kernels.int8_linear_forward(x, w, scale, b)
+    y = quant_kernels.int8_linear_forward(x, w, scale, b, path="fused")
     decoded = quant_kernels.decode(w, scale, torch.bfloat16).double()
     exact = x.double() @ decoded.t() + b.double()
     magnitude = x.double().abs() @ decoded.abs().t()
@@ -113,7 +114,7 @@ def test_backward_launch_plans_match_fp64_reference(rows, in_f, out_f) -> None:
     _, w, scale, _ = _operands(1, in_f, out_f, seed=rows + 5 * in_f + out_f)
     g = torch.Generator().manual_seed(rows + 1)
     dy = torch.randn(rows, out_f, generator=g).to(torch.bfloat16).to(DEV)
-    dx = quant_kernels.int8_linear_backward(dy, w, scale, torch.Size((rows, in_f)))
+    dx = quant_kernels.int8_linear_backward(dy, w, scale, torch.Size((rows, in_f)), path="fused")
     decoded = quant_kernels.decode(w, scale, torch.bfloat16).double()
     exact = dy.double() @ decoded
     magnitude = dy.double().abs() @ decoded.abs()
@@ -125,14 +126,15 @@ def test_tile_choice_does_not_change_results() -> None:
     # on small tiles only. Each output element has one reduction order in every plan.
     rows, in_f, out_f = 17792, 3072, 3072
     x, w, scale, b = _operands(rows, in_f, out_f, seed=77, bias=True)
-    full = quant_kernels.int8_linear_forward(x, w, scale, b)
-    assert torch.equal(quant_kernels.int8_linear_forward(x[:4096], w, scale, b).view(torch.int16),
+    fused = {"path": "fused"}
+    full = quant_kernels.int8_linear_forward(x, w, scale, b, **fused)
+    assert torch.equal(quant_kernels.int8_linear_forward(x[:4096], w, scale, b, **fused).view(torch.int16),
                        full[:4096].view(torch.int16))
-    assert torch.equal(quant_kernels.int8_linear_forward(x[16384:], w, scale, b).view(torch.int16),
+    assert torch.equal(quant_kernels.int8_linear_forward(x[16384:], w, scale, b, **fused).view(torch.int16),
                        full[16384:].view(torch.int16))
     dy = x[:, :out_f].contiguous()
-    dfull = quant_kernels.int8_linear_backward(dy, w, scale, torch.Size((rows, in_f)))
-    part = quant_kernels.int8_linear_backward(dy[:4096], w, scale, torch.Size((4096, in_f)))
+    dfull = quant_kernels.int8_linear_backward(dy, w, scale, torch.Size((rows, in_f)), **fused)
+    part = quant_kernels.int8_linear_backward(dy[:4096], w, scale, torch.Size((4096, in_f)), **fused)
     assert torch.equal(part.view(torch.int16), dfull[:4096].view(torch.int16))
 
 
@@ -222,3 +224,45 @@ def test_int8_lora_model_hip_backend_matches_eager() -> None:
     assert eg.keys() == hg.keys() and eg
     for name in eg:
         torch.testing.assert_close(hg[name], eg[name], rtol=5e-2, atol=1e-3, msg=name)
+
+
+@pytest.mark.parametrize("out_f,in_f", [(16, 16), (48, 80), (3072, 1040), (4097, 16), (24576, 3072)])
+def test_decode_kernel_matches_the_reference_decode_bitwise(out_f, in_f) -> None:
+    """mo_int8_decode writes bf16(q * bf16(scale)) exactly as the reference's eager decode
+    (quant_kernels.py:126-131); scales span normal fp32 magnitudes and bf16 rounding ties."""
+
+    g = torch.Generator().manual_seed(out_f + in_f)
+    w = torch.randint(-128, 128, (out_f, in_f), dtype=torch.int8, generator=g).to(DEV)
+    scale = torch.empty(out_f).uniform_(1e-3, 2e-2, generator=g)
+    scale[::7] = torch.empty(scale[::7].shape).uniform_(-3.0, 3.0, generator=g)
+    scale[::11] = 1.0 + 2.0**-8  # halfway between two bf16 values
+    scale = scale.to(DEV)
+    got = quant_kernels.decode_hip(w, scale)
+    want = quant_kernels.decode(w, scale, torch.bfloat16)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", [(4096, 1040, 3072), (4100, 3072, 1040)])
+def test_library_path_is_the_eager_path_bit_for_bit(rows, in_f, out_f) -> None:
+    """From LIBRARY_ROWS rows up, ``auto`` decodes once and runs the library GEMM: the result is the
+    reference eager path's (decode, then F.linear / matmul) bit for bit, with and without bias,
+    and within the fp64 accumulation bound like the fused kernels."""
+
+    assert rows >= quant_kernels.LIBRARY_ROWS
+    x, w, scale, b = _operands(rows, in_f, out_f, seed=rows + in_f, bias=True)
+    decoded = quant_kernels.decode(w, scale, torch.bfloat16)
+    for bias in (None, b):
+        y = quant_kernels.int8_linear_forward(x, w, scale, bias)
+        assert torch.equal(y.view(torch.int16), F.linear(x, decoded, bias).view(torch.int16))
+    g = torch.Generator().manual_seed(rows)
+    dy = torch.randn(rows, out_f, generator=g).to(torch.bfloat16).to(DEV)
+    dx = quant_kernels.int8_linear_backward(dy, w, scale, torch.Size((rows, in_f)))
+    assert torch.equal(dx.view(torch.int16), dy.matmul(decoded).view(torch.int16))
+    exact = x.double() @ decoded.double().t() + b.double()
+    _within_accumulation_bound(y, exact, x.double().abs() @ decoded.double().abs().t(), in_f)
+    # below the threshold auto is the fused kernel
+    small = x[: quant_kernels.LIBRARY_ROWS - 1]
+    assert torch.equal(quant_kernels.int8_linear_forward(small, w, scale, b).view(torch.int16),
+                       quant_kernels.int8_linear_forward(small, w, scale, b, path="fused").view(torch.int16))
+    with pytest.raises(ValueError):
+        quant_kernels.int8_linear_forward(x, w, scale, b, path="triton")
