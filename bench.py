@@ -655,9 +655,11 @@ def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
         "block_speedup_vs_eager": round(block["eager"] / block["hip"], 4),
         "fused_block_speedup_vs_eager": round(block["eager"] / block["fused"], 4),
         "library_rows": qk.LIBRARY_ROWS,
+        "library_weight_elements": qk.LIBRARY_WEIGHT,
         "roofline": {"bound": "mfma",
-                     "kernels": (f"mo_int8_decode_kernel + library GEMM (rows >= {qk.LIBRARY_ROWS}), "
-                                 "mo_int8_linear_{fwd,bwd}_{large,small} below"),
+                     "kernels": (f"mo_int8_decode_kernel + library GEMM (rows >= {qk.LIBRARY_ROWS} or weight >= "
+                                 f"{qk.LIBRARY_WEIGHT} elements), mo_int8_linear_{{fwd,bwd}}_{{large,small}} "
+                                 "otherwise"),
                      "workload": "one config-5 joint block: 4 x qkvo + ffn_up_gate + ffn_down, forward and "
                                  f"input gradient, {rows} rows",
                      "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",

@@ -3,8 +3,8 @@
 
 The GEMMs are hand-written gfx950 kernels in ``csrc/mo_gemm.hip`` (bf16 MFMA, int8 tiles
 decoded to bf16 on their way into LDS), reached through ``mo_int8_linear_forward`` and
-``mo_int8_linear_backward``. From ``LIBRARY_ROWS`` rows up, a call instead decodes the weight
-in one HIP pass (``mo_int8_decode``) and runs the same library GEMM as the eager path, bit for
+``mo_int8_linear_backward``. From ``LIBRARY_ROWS`` rows or ``LIBRARY_WEIGHT`` weight elements
+up, a call instead decodes the weight in one HIP pass (``mo_int8_decode``) and runs the same library GEMM as the eager path, bit for
 bit equal to it and faster by the decode. Backend selection mirrors the reference's ``auto | eager | triton``
 with ``hip`` in place of ``triton``: ``auto`` takes the HIP kernels whenever the call is
 supported (bf16 activations and weight dtype on a HIP device, int8 weights, fp32 scales,
@@ -78,15 +78,19 @@ def decode(weight: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> tor
     return weight.to(dtype) * scale.to(dtype)[:, None]
 
 
-# From this many rows up, a call decodes the weight once (mo_int8_decode) and runs the library
-# GEMM on it; below, the fused kernels decode the int8 tiles in LDS. The fused kernels decode each
-# weight tile again for every row tile, and their MFMA loop runs below the library's on these
-# shapes. At 17 792 rows (config 5), for one joint block, the decode-once path took 9.65 ms
-# against 10.77 ms fused and 9.79 ms for the eager path. The one-pass decode takes 7.9 / 35 /
-# 20 us for qkvo / up_gate / down, against 34 / 225 / 100 us for the eager cast-then-scale. At
-# 4096 rows the decode is still under a tenth of the GEMM; fewer rows keep the fused kernels,
-# which read the int8 weight only.
-LIBRARY_ROWS = 4096
+# A call with at least LIBRARY_ROWS rows, or a weight of at least LIBRARY_WEIGHT elements,
+# decodes the weight once (mo_int8_decode) and runs the library GEMM on it. Any other call
+# runs the fused kernels, which decode the int8 tiles in LDS. Measured on MI355X, forward plus
+# input gradient, library time / fused time:
+#   qkvo 3072x3072:     1.14 / 1.06 / 1.15 / 0.94 / 0.80 / 0.83 at 256 / 512 / 1024 / 2048 / 4096 / 8192 rows
+#   up_gate 24576x3072: 0.77 / 0.99 / 0.99 / 1.01 / 0.78 / 0.76
+#   down 3072x12288:    0.77 / 0.86 / 0.90 / 0.83 / 0.79 / 0.83
+# The fused kernels decode each weight tile again for every row tile, and their MFMA loop runs
+# below the library's on these shapes. They keep small weights at few rows, where the one
+# decode pass is a large share of the call. The one-pass decode takes 7.9 / 35 / 20 us for
+# qkvo / up_gate / down, against 34 / 225 / 100 us for the eager cast-then-scale.
+LIBRARY_ROWS = 2048
+LIBRARY_WEIGHT = 16 << 20
 PATHS = ("auto", "fused", "library")
 
 
@@ -101,10 +105,10 @@ def decode_hip(weight: torch.Tensor, scale: torch.Tensor, *, out: torch.Tensor |
     return out
 
 
-def _library(rows: int, path: str) -> bool:
+def _library(rows: int, weight: torch.Tensor, path: str) -> bool:
     if path not in PATHS:
         raise ValueError(f"path must be one of {PATHS}")
-    return path == "library" or (path == "auto" and rows >= LIBRARY_ROWS)
+    return path == "library" or (path == "auto" and (rows >= LIBRARY_ROWS or weight.numel() >= LIBRARY_WEIGHT))
 
 
 def _stream(tensor: torch.Tensor) -> int:
@@ -125,7 +129,8 @@ def int8_linear_forward(tokens: torch.Tensor, weight: torch.Tensor, scale: torch
                         path: str = "auto") -> torch.Tensor:
     """``tokens @ decode(weight).T (+ bias)``; the call must be supported. ``path``: ``fused`` (the
     MFMA kernels), ``library`` (``decode_hip``, then the same ``addmm``/``mm`` as the reference's
-    eager path, bit for bit), ``auto`` (library from ``LIBRARY_ROWS`` rows up)."""
+    eager path, bit for bit), ``auto`` (library from ``LIBRARY_ROWS`` rows or ``LIBRARY_WEIGHT``
+    weight elements up)."""
 
     lib = _native.load()
     matrix = tokens.reshape(-1, tokens.shape[-1]).contiguous()
@@ -134,7 +139,7 @@ def int8_linear_forward(tokens: torch.Tensor, weight: torch.Tensor, scale: torch
     out = _output(out, (rows, out_features), tokens.device, "output")
     if bias is not None:
         bias = bias.to(torch.bfloat16).contiguous()
-    if _library(rows, path):
+    if _library(rows, weight, path):
         decoded = decode_hip(weight, scale)
         if bias is None:
             torch.mm(matrix, decoded.t(), out=out)
@@ -161,7 +166,7 @@ def int8_linear_backward(gradient: torch.Tensor, weight: torch.Tensor, scale: to
     rows, out_features = matrix.shape
     in_features = weight.shape[1]
     out = _output(out, (rows, in_features), gradient.device, "input-gradient")
-    if _library(rows, path):
+    if _library(rows, weight, path):
         torch.mm(matrix, decode_hip(weight, scale), out=out)
         return out.reshape(input_shape)
     _native.check(
