@@ -802,6 +802,7 @@ def run(args) -> dict:
         stage_slot_bytes=args.slot_mib << 20,
         staged_restore=not args.no_staged_restore,
         kernel_copy=args.kernel_copy,
+        link=args.link,
         batch_packs=not args.eager_pack,
         d2h_engine=args.d2h_engine,
         h2d_engine=args.h2d_engine,
@@ -1082,6 +1083,9 @@ def main() -> int:
     parser.add_argument("--eager-pack", action="store_true",
                         help="one gather launch per save instead of one per staging segment")
     parser.add_argument("--kernel-copy", action="store_true", help="copy kernel on HIP streams instead of SDMA")
+    parser.add_argument("--link", default="sdma", choices=("sdma", "hipdma"),
+                        help="host-link transport: SDMA through HSA with host-side ordering, or the same DMA "
+                             "copies on HIP streams ordered by hipStreamWaitEvent")
     parser.add_argument("--cpu-threads", type=int, default=16)
     parser.add_argument("--gradacc-threads", type=int, default=12, help="host threads of the G leg's accumulator")
     parser.add_argument("--keep-last-blocks", type=int, default=16,

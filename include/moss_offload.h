@@ -52,6 +52,12 @@ extern "C" {
                                          still intact in its staging slot                  */
 #define MO_FLAG_EAGER_PACK 0x10    /* launch each mo_pack call's gather kernels before it
                                       returns instead of batching them per segment        */
+#define MO_FLAG_HIP_DMA 0x20       /* move D2H/H2D with hipMemcpyAsync on dedicated HIP copy
+                                      streams (the runtime runs them on the SDMA engines),
+                                      ordered by hipStreamWaitEvent only: an unpack enqueues
+                                      a stream wait and never blocks the host. D2H copies of
+                                      2 MiB or more are split over two copy streams while no
+                                      H2D is pending, unless d2h_engine has exactly one bit */
 
 /*
  * A strided tensor view on the device. `ptr` is the address of logical element (0,...,0),

@@ -849,6 +849,9 @@ struct Engine {
     if (cfg.flags & MO_FLAG_KERNEL_COPY) {
       link = make_stream_link(device, cfg.copy_kernel_blocks, (cfg.flags & MO_FLAG_TIMING) != 0, host_alias, &pool,
                               err, &status);
+    } else if (cfg.flags & MO_FLAG_HIP_DMA) {
+      const bool split = __builtin_popcount(cfg.d2h_engine) != 1;
+      link = make_hip_dma_link(device, split, (cfg.flags & MO_FLAG_TIMING) != 0, err, &status);
     } else {
       link = make_sdma_link(device, cfg.d2h_engine, cfg.h2d_engine, err, &status);
     }

@@ -18,6 +18,7 @@
 #include <thread>
 #include <vector>
 
+#include "mo_gate_order.h"
 #include "mo_internal.h"
 
 namespace mo {
@@ -35,6 +36,40 @@ constexpr int64_t kWaitLimitNs = 300ll * 1000000000ll;  // a copy that takes lon
 // (engine, streamer).
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_h2d_inflight[kMaxDevices];
+
+// The HSA runtime is shared with HIP (and with a profiler's interception layer when one is
+// loaded). The library takes one reference on it, the first time a link is made, and never
+// gives it back: an hsa_shut_down from a library's teardown can run while HIP and the
+// profiler still use the runtime (at interpreter exit, for instance), and the runtime ends
+// with the process anyway.
+bool hsa_reference() {
+  static const bool ok = hsa_init() == HSA_STATUS_SUCCESS;
+  return ok;
+}
+
+// Process-wide pool of copy-completion signals. A signal handed to the runtime as a copy's
+// completion signal is never destroyed: a profiler that intercepts the copy API may wrap it and
+// still touch it after the copy is reported complete, or in its own exit handlers. Links
+// return their signals here and later links reuse them; the process end reclaims them.
+std::mutex g_signal_mu;
+std::vector<hsa_signal_t> g_signals;
+
+bool signal_pool_take(hsa_signal_t* sig) {
+  {
+    std::lock_guard<std::mutex> lock(g_signal_mu);
+    if (!g_signals.empty()) {
+      *sig = g_signals.back();
+      g_signals.pop_back();
+      return true;
+    }
+  }
+  return hsa_signal_create(1, 0, nullptr, sig) == HSA_STATUS_SUCCESS;
+}
+
+void signal_pool_give(hsa_signal_t sig) {
+  std::lock_guard<std::mutex> lock(g_signal_mu);
+  g_signals.push_back(sig);
+}
 
 // Short polling sleep. The default 50 us timer slack of a Linux thread would dominate a 5 us
 // sleep, so each polling thread lowers its own slack once.
@@ -88,7 +123,8 @@ struct Job {
   void* dst = nullptr;
   const void* src = nullptr;
   EventRef wait;  // issue after this HIP event completed
-  SdmaRef after;  // and after this copy completed
+  SdmaRef after;  // and after this copy completed (the D2H that filled an H2D's source)
+  SdmaRef prev;   // and after this earlier copy through the same gate (GateOrder)
   // Polling of `wait` backs off while the compute stream is far behind (hipEventQuery is a
   // runtime call that competes with the application's own launches).
   int64_t next_query_ns = 0;
@@ -104,8 +140,8 @@ struct InFlight {
 };
 
 struct GateState {
-  SdmaRef last;      // the last copy through the gate
-  EventRef consumed;  // the slot's last consumer on a compute stream
+  GateOrder<SdmaRef> order;  // copy-to-copy ordering; order.last is the gate's last copy
+  EventRef consumed;         // the slot's last consumer on a compute stream
 };
 
 struct AgentSearch {
@@ -142,11 +178,10 @@ class SdmaLink : public Link {
 
   int init(int device, uint32_t d2h_engine, uint32_t h2d_engine, std::string& err) {
     device_ = device;
-    if (hsa_init() != HSA_STATUS_SUCCESS) {
+    if (!hsa_reference()) {
       err = "hsa_init failed";
       return MO_E_STATE;
     }
-    hsa_inited_ = true;
     // Match the HIP device to its HSA agent by PCI location (falls back to the ordinal).
     AgentSearch s;
     int v = 0;
@@ -209,8 +244,8 @@ class SdmaLink : public Link {
     job.dst = dst;
     job.src = src;
     job.wait = std::move(ev);
+    job.prev = gates_[gate].order.on_read(copy);
     enqueue(std::move(job));
-    gates_[gate].last = copy;
     d2h_bytes_ += bytes;
     *out = copy;
     return 0;
@@ -226,8 +261,8 @@ class SdmaLink : public Link {
     job.src = src;
     job.wait = gates_[gate].consumed;
     job.after = std::dynamic_pointer_cast<SdmaCopy>(after);
+    job.prev = gates_[gate].order.on_write(copy);
     enqueue(std::move(job));
-    gates_[gate].last = copy;
     h2d_bytes_ += bytes;
     *out = copy;
     return 0;
@@ -240,8 +275,8 @@ class SdmaLink : public Link {
     job.dst = dst;
     job.src = src;
     job.wait = gates_[gate].consumed;
+    job.prev = gates_[gate].order.on_read(copy);
     enqueue(std::move(job));
-    gates_[gate].last = copy;
     d2h_bytes_ += bytes;
     *out = copy;
     return 0;
@@ -251,7 +286,7 @@ class SdmaLink : public Link {
   // GPU work afterwards, so stream order does the rest.
   int wait(int gate, hipStream_t compute) override {
     (void)compute;
-    const SdmaRef& c = gates_[gate].last;
+    const SdmaRef& c = gates_[gate].order.last;
     if (!c || c->done()) return 0;
     const int64_t t0 = now_ns();
     while (!c->done()) {
@@ -391,15 +426,16 @@ class SdmaLink : public Link {
     cv_.notify_one();
   }
 
-  // Worker-owned signal pool: a signal goes back to the pool as soon as its copy finished.
+  // Worker-owned signal pool: a signal goes back to the pool as soon as its copy finished. The
+  // pool is filled from, and returned to, the process-wide pool (signal_pool_take/give).
   bool take_signal(hsa_signal_t* sig) {
+    if (sig_pool_.empty() && !signal_pool_take(sig)) return false;
     if (!sig_pool_.empty()) {
       *sig = sig_pool_.back();
       sig_pool_.pop_back();
-      hsa_signal_store_screlease(*sig, 1);
-      return true;
     }
-    return hsa_signal_create(1, 0, nullptr, sig) == HSA_STATUS_SUCCESS;
+    hsa_signal_store_screlease(*sig, 1);
+    return true;
   }
 
   void finish(const SdmaRef& c, bool failed) {
@@ -452,10 +488,11 @@ class SdmaLink : public Link {
         return true;
       }
     }
-    if (job.after) {
-      if (!job.after->done()) return false;
-      const bool bad = job.after->failed();
-      job.after.reset();
+    for (SdmaRef* dep : {&job.after, &job.prev}) {
+      if (!*dep) continue;
+      if (!(*dep)->done()) return false;
+      const bool bad = (*dep)->failed();
+      dep->reset();
       if (bad) {
         finish(job.copy, true);
         return true;
@@ -585,21 +622,18 @@ class SdmaLink : public Link {
       worker_.join();  // returns once the queue is drained and nothing is in flight
     }
     gates_.clear();
-    for (hsa_signal_t s : sig_pool_) hsa_signal_destroy(s);
+    for (hsa_signal_t s : sig_pool_) signal_pool_give(s);
     sig_pool_.clear();
     {
       std::lock_guard<std::mutex> lock(ev_mu_);
       for (hipEvent_t e : ev_pool_) (void)hipEventDestroy(e);
       ev_pool_.clear();
     }
-    if (hsa_inited_) {
-      hsa_shut_down();
-      hsa_inited_ = false;
-    }
+    // No hsa_shut_down: the HSA reference taken in init() is held until the process ends (see
+    // hsa_reference()).
   }
 
   int device_ = 0;
-  bool hsa_inited_ = false;
   hsa_agent_t gpu_{0}, cpu_{0};
   uint32_t e_d2h_[2] = {0, 0}, e_h2d_[2] = {0, 0};  // engine bits per direction
   int n_d2h_ = 0, n_h2d_ = 0;
@@ -636,58 +670,79 @@ EventHold::~EventHold() {
 }
 
 // ==========================================================================================
-// Stream link: copy kernel on dedicated HIP streams
+// Stream link: copies on dedicated HIP streams, ordered with HIP events only
+//
+// Two ways to move the bytes:
+//   kDma         hipMemcpyAsync(..., hipMemcpyDeviceToDeviceNoCU) between pinned host memory and
+//                device memory: the HIP runtime runs it on the SDMA engines (no compute unit).
+//   kCopyKernel  the engine's own copy kernel (a comparison point: it contends for CUs).
+// Every dependency is a hipStreamWaitEvent on a stream: compute -> copy (the copy stream waits
+// for an event recorded after the producing kernels), copy -> copy (GateOrder), and copy ->
+// compute (wait() makes the compute stream wait for the gate's last copy). The host never
+// waits for a copy on this path; it only enqueues.
 
 struct StreamCopy : CopyState {
-  hipEvent_t ev = nullptr;
+  hipEvent_t ev[2] = {nullptr, nullptr};  // one per part (a split D2H has two)
+  int parts = 0;
   std::vector<hipEvent_t>* pool = nullptr;
   std::mutex* pool_mu = nullptr;
   ~StreamCopy() override {
-    if (ev) {
-      std::lock_guard<std::mutex> lock(*pool_mu);
-      pool->push_back(ev);
-    }
+    std::lock_guard<std::mutex> lock(*pool_mu);
+    for (int k = 0; k < parts; ++k) pool->push_back(ev[k]);
   }
-  bool done() const override { return hipEventQuery(ev) == hipSuccess; }
+  bool done() const override {
+    for (int k = 0; k < parts; ++k)
+      if (hipEventQuery(ev[k]) != hipSuccess) return false;
+    return true;
+  }
   bool failed() const override { return false; }
 };
+using StreamRef = std::shared_ptr<StreamCopy>;
 
 class StreamLink : public Link {
  public:
+  enum Method { kCopyKernel, kDma };
+
   ~StreamLink() override {
     (void)synchronize();
     for (auto& g : gates_) {
-      if (g.ready) (void)hipEventDestroy(g.ready);
+      g.order.clear();
       if (g.consumed) (void)hipEventDestroy(g.consumed);
     }
+    last_h2d_.reset();
     for (auto& t : timings_) {
       (void)hipEventDestroy(t.start);
       (void)hipEventDestroy(t.end);
     }
     for (hipEvent_t e : pool_) (void)hipEventDestroy(e);
     if (tmp_) (void)hipEventDestroy(tmp_);
-    if (d2h_) (void)hipStreamDestroy(d2h_);
+    if (base_) (void)hipEventDestroy(base_);
+    for (hipStream_t s : d2h_)
+      if (s) (void)hipStreamDestroy(s);
     if (h2d_) (void)hipStreamDestroy(h2d_);
   }
 
-  int init(uint32_t blocks, bool timing, char* (*alias)(void*, char*), void* ctx) {
+  int init(Method method, uint32_t blocks, bool timing, bool split_d2h, char* (*alias)(void*, char*), void* ctx) {
+    method_ = method;
     blocks_ = blocks ? blocks : 16;
     timing_ = timing;
     alias_ = alias;
     alias_ctx_ = ctx;
+    n_d2h_ = split_d2h ? 2 : 1;
     hipError_t e;
-    if ((e = hipStreamCreateWithFlags(&d2h_, hipStreamNonBlocking)) != hipSuccess) return (int)e;
+    for (int k = 0; k < n_d2h_; ++k)
+      if ((e = hipStreamCreateWithFlags(&d2h_[k], hipStreamNonBlocking)) != hipSuccess) return (int)e;
     if ((e = hipStreamCreateWithFlags(&h2d_, hipStreamNonBlocking)) != hipSuccess) return (int)e;
     if ((e = hipEventCreateWithFlags(&tmp_, hipEventDisableTiming)) != hipSuccess) return (int)e;
+    if (timing_) {
+      if ((e = hipEventCreate(&base_)) != hipSuccess) return (int)e;
+      if ((e = hipEventRecord(base_, d2h_[0])) != hipSuccess) return (int)e;
+    }
     return 0;
   }
 
   int new_gate(int* gate) override {
-    Gate g;
-    hipError_t e;
-    if ((e = hipEventCreateWithFlags(&g.ready, hipEventDisableTiming)) != hipSuccess) return (int)e;
-    if ((e = hipEventCreateWithFlags(&g.consumed, hipEventDisableTiming)) != hipSuccess) return (int)e;
-    gates_.push_back(g);
+    gates_.emplace_back();
     *gate = (int)gates_.size() - 1;
     return 0;
   }
@@ -695,42 +750,69 @@ class StreamLink : public Link {
   int d2h(void* dst, const void* src, uint64_t bytes, hipStream_t compute, int gate, CopyRef* out) override {
     hipError_t e;
     if ((e = hipEventRecord(tmp_, compute)) != hipSuccess) return (int)e;
-    if ((e = hipStreamWaitEvent(d2h_, tmp_, 0)) != hipSuccess) return (int)e;
-    return copy(d2h_, alias_(alias_ctx_, (char*)dst), src, bytes, true, gate, out);
+    // Split in halves over the two D2H streams only while no H2D is pending: with both
+    // directions busy the host link is the limit and a split D2H takes it from the H2D.
+    const int parts = n_d2h_ == 2 && bytes >= kSplitBytes && !h2d_pending() ? 2 : 1;
+    StreamRef copy;
+    if (int rc = make_copy(parts, &copy)) return rc;
+    const StreamRef dep = std::static_pointer_cast<StreamCopy>(gates_[gate].order.on_read(copy));
+    const uint64_t half = parts == 2 ? bytes / 2 / 4096 * 4096 : bytes;
+    for (int k = 0; k < parts; ++k) {
+      hipStream_t s = d2h_[k];
+      if ((e = hipStreamWaitEvent(s, tmp_, 0)) != hipSuccess) return (int)e;
+      if (int rc = wait_for(s, dep)) return rc;
+      const uint64_t off = k ? half : 0, len = k ? bytes - half : half;
+      if (int rc = move(s, host(dst) + off, (const char*)src + off, len, true, copy->ev[k])) return rc;
+    }
+    st_.d2h_bytes += bytes;
+    *out = copy;
+    return 0;
   }
 
   int h2d(void* dst, const void* src, uint64_t bytes, const CopyRef& after, int gate, CopyRef* out) override {
-    hipError_t e;
+    StreamRef copy;
+    if (int rc = make_copy(1, &copy)) return rc;
     Gate& g = gates_[gate];
-    if (g.consumed_recorded && (e = hipStreamWaitEvent(h2d_, g.consumed, 0)) != hipSuccess) return (int)e;
-    auto prev = std::dynamic_pointer_cast<StreamCopy>(after);
-    if (prev && (e = hipStreamWaitEvent(h2d_, prev->ev, 0)) != hipSuccess) return (int)e;
-    return copy(h2d_, dst, alias_(alias_ctx_, (char*)src), bytes, false, gate, out);
+    hipError_t e;
+    if (g.consumed && (e = hipStreamWaitEvent(h2d_, g.consumed, 0)) != hipSuccess) return (int)e;
+    if (int rc = wait_for(h2d_, std::static_pointer_cast<StreamCopy>(after))) return rc;
+    if (int rc = wait_for(h2d_, std::static_pointer_cast<StreamCopy>(g.order.on_write(copy)))) return rc;
+    if (int rc = move(h2d_, (char*)dst, host(src), bytes, false, copy->ev[0])) return rc;
+    st_.h2d_bytes += bytes;
+    last_h2d_ = copy;
+    *out = copy;
+    return 0;
   }
 
   int writeback(void* dst, const void* src, uint64_t bytes, int gate, CopyRef* out) override {
-    hipError_t e;
+    StreamRef copy;
+    if (int rc = make_copy(1, &copy)) return rc;
     Gate& g = gates_[gate];
-    if (g.consumed_recorded && (e = hipStreamWaitEvent(d2h_, g.consumed, 0)) != hipSuccess) return (int)e;
-    return copy(d2h_, alias_(alias_ctx_, (char*)dst), src, bytes, true, gate, out);
+    hipError_t e;
+    if (g.consumed && (e = hipStreamWaitEvent(d2h_[0], g.consumed, 0)) != hipSuccess) return (int)e;
+    if (int rc = wait_for(d2h_[0], std::static_pointer_cast<StreamCopy>(g.order.on_read(copy)))) return rc;
+    if (int rc = move(d2h_[0], host(dst), (const char*)src, bytes, true, copy->ev[0])) return rc;
+    st_.d2h_bytes += bytes;
+    *out = copy;
+    return 0;
   }
 
+  // The compute stream waits for the gate's last copy: GPU-side, the host does not block.
   int wait(int gate, hipStream_t compute) override {
-    Gate& g = gates_[gate];
-    if (!g.used) return 0;
-    return (int)hipStreamWaitEvent(compute, g.ready, 0);
+    return wait_for(compute, std::static_pointer_cast<StreamCopy>(gates_[gate].order.last));
   }
 
   int consumed(int gate, hipStream_t compute) override {
     Gate& g = gates_[gate];
-    hipError_t e = hipEventRecord(g.consumed, compute);
-    g.consumed_recorded = e == hipSuccess;
-    return (int)e;
+    hipError_t e;
+    if (!g.consumed && (e = hipEventCreateWithFlags(&g.consumed, hipEventDisableTiming)) != hipSuccess) return (int)e;
+    return (int)hipEventRecord(g.consumed, compute);
   }
 
   int synchronize() override {
     hipError_t e;
-    if (d2h_ && (e = hipStreamSynchronize(d2h_)) != hipSuccess) return (int)e;
+    for (hipStream_t s : d2h_)
+      if (s && (e = hipStreamSynchronize(s)) != hipSuccess) return (int)e;
     if (h2d_ && (e = hipStreamSynchronize(h2d_)) != hipSuccess) return (int)e;
     process_timings(true);
     return 0;
@@ -740,16 +822,25 @@ class StreamLink : public Link {
     process_timings(false);
     *out = st_;
   }
+
   void reset_stats() override {
     process_timings(false);
     st_ = LinkStats();
+    last_end_ms_[0] = last_end_ms_[1] = -1.0;
+    if (base_ && timings_.empty()) {
+      // re-base the interval clock so float milliseconds stay precise over long runs
+      (void)hipEventRecord(base_, d2h_[0]);
+    }
   }
-  const char* name() const override { return "kernel"; }
+
+  const char* name() const override { return method_ == kDma ? "hipdma" : "kernel"; }
 
  private:
+  static constexpr uint64_t kSplitBytes = 2ull << 20;
+
   struct Gate {
-    hipEvent_t ready = nullptr, consumed = nullptr;
-    bool used = false, consumed_recorded = false;
+    GateOrder<CopyRef> order;       // order.last: the gate's last copy
+    hipEvent_t consumed = nullptr;  // the slot's last consumer on a compute stream
   };
   struct Timing {
     hipEvent_t start, end;
@@ -757,7 +848,45 @@ class StreamLink : public Link {
     bool d2h;
   };
 
-  int copy(hipStream_t s, void* dst, const void* src, uint64_t bytes, bool to_host, int gate, CopyRef* out) {
+  char* host(const void* p) {
+    return method_ == kCopyKernel ? alias_(alias_ctx_, (char*)p) : (char*)p;
+  }
+
+  bool h2d_pending() const { return last_h2d_ && !last_h2d_->done(); }
+
+  int make_copy(int parts, StreamRef* out) {
+    auto c = std::make_shared<StreamCopy>();
+    c->pool = &pool_;
+    c->pool_mu = &pool_mu_;
+    for (int k = 0; k < parts; ++k) {
+      {
+        std::lock_guard<std::mutex> lock(pool_mu_);
+        if (!pool_.empty()) {
+          c->ev[k] = pool_.back();
+          pool_.pop_back();
+        }
+      }
+      if (!c->ev[k]) {
+        hipError_t e = hipEventCreateWithFlags(&c->ev[k], hipEventDisableTiming);
+        if (e != hipSuccess) return (int)e;
+      }
+      c->parts = k + 1;
+    }
+    *out = std::move(c);
+    return 0;
+  }
+
+  static int wait_for(hipStream_t s, const StreamRef& c) {
+    if (!c) return 0;
+    for (int k = 0; k < c->parts; ++k) {
+      hipError_t e = hipStreamWaitEvent(s, c->ev[k], 0);
+      if (e != hipSuccess) return (int)e;
+    }
+    return 0;
+  }
+
+  // Enqueue one copy on `s` and record `done` after it.
+  int move(hipStream_t s, char* dst, const char* src, uint64_t bytes, bool to_host, hipEvent_t done) {
     hipError_t e;
     Timing t{nullptr, nullptr, bytes, to_host};
     if (timing_) {
@@ -765,45 +894,33 @@ class StreamLink : public Link {
       if ((e = hipEventCreate(&t.end)) != hipSuccess) return (int)e;
       if ((e = hipEventRecord(t.start, s)) != hipSuccess) return (int)e;
     }
-    if (int rc = launch_link_copy(dst, src, bytes, blocks_, s)) return rc;
+    if (method_ == kDma) {
+      if ((e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDeviceNoCU, s)) != hipSuccess) return (int)e;
+    } else if (int rc = launch_link_copy(dst, src, bytes, blocks_, s)) {
+      return rc;
+    }
     if (timing_) {
       if ((e = hipEventRecord(t.end, s)) != hipSuccess) return (int)e;
       timings_.push_back(t);
     }
-    auto c = std::make_shared<StreamCopy>();
-    {
-      std::lock_guard<std::mutex> lock(pool_mu_);
-      if (!pool_.empty()) {
-        c->ev = pool_.back();
-        pool_.pop_back();
-      }
-    }
-    if (!c->ev && (e = hipEventCreateWithFlags(&c->ev, hipEventDisableTiming)) != hipSuccess) return (int)e;
-    c->pool = &pool_;
-    c->pool_mu = &pool_mu_;
-    if ((e = hipEventRecord(c->ev, s)) != hipSuccess) return (int)e;
-    Gate& g = gates_[gate];
-    if ((e = hipEventRecord(g.ready, s)) != hipSuccess) return (int)e;
-    g.used = true;
-    (to_host ? st_.d2h_bytes : st_.h2d_bytes) += bytes;
-    *out = c;
-    return 0;
+    return (int)hipEventRecord(done, s);
   }
 
+  // Busy time per direction: the union of the copies' [start, end] intervals, measured against
+  // one base event (copies of one direction may overlap on the two D2H streams).
   void process_timings(bool wait) {
     while (!timings_.empty()) {
       Timing& t = timings_.front();
       if (wait) (void)hipEventSynchronize(t.end);
       else if (hipEventQuery(t.end) != hipSuccess) break;
-      float ms = 0;
-      if (hipEventElapsedTime(&ms, t.start, t.end) == hipSuccess) {
-        if (t.d2h) {
-          st_.d2h_ms += ms;
-          st_.d2h_done_bytes += t.bytes;
-        } else {
-          st_.h2d_ms += ms;
-          st_.h2d_done_bytes += t.bytes;
-        }
+      float a = 0, b = 0;
+      if (hipEventElapsedTime(&a, base_, t.start) == hipSuccess && hipEventElapsedTime(&b, base_, t.end) == hipSuccess) {
+        const int d = t.d2h ? 0 : 1;
+        const double s = std::max<double>(a, last_end_ms_[d]);
+        const double busy = b > s ? b - s : 0.0;
+        (t.d2h ? st_.d2h_ms : st_.h2d_ms) += busy;
+        (t.d2h ? st_.d2h_done_bytes : st_.h2d_done_bytes) += t.bytes;
+        last_end_ms_[d] = std::max<double>(last_end_ms_[d], b);
       }
       (void)hipEventDestroy(t.start);
       (void)hipEventDestroy(t.end);
@@ -811,16 +928,21 @@ class StreamLink : public Link {
     }
   }
 
+  Method method_ = kDma;
   uint32_t blocks_ = 16;
   bool timing_ = false;
   char* (*alias_)(void*, char*) = nullptr;
   void* alias_ctx_ = nullptr;
-  hipStream_t d2h_ = nullptr, h2d_ = nullptr;
-  hipEvent_t tmp_ = nullptr;
+  int n_d2h_ = 1;
+  hipStream_t d2h_[2] = {nullptr, nullptr};
+  hipStream_t h2d_ = nullptr;
+  hipEvent_t tmp_ = nullptr, base_ = nullptr;
   std::vector<Gate> gates_;
+  StreamRef last_h2d_;
   std::mutex pool_mu_;
   std::vector<hipEvent_t> pool_;
   std::deque<Timing> timings_;
+  double last_end_ms_[2] = {-1.0, -1.0};
   LinkStats st_;
 };
 
@@ -838,7 +960,18 @@ std::unique_ptr<Link> make_stream_link(int device, uint32_t copy_blocks, bool ti
                                        void* alias_ctx, std::string& err, int* status) {
   (void)device;
   auto link = std::make_unique<StreamLink>();
-  *status = link->init(copy_blocks, timing, alias, alias_ctx);
+  *status = link->init(StreamLink::kCopyKernel, copy_blocks, timing, false, alias, alias_ctx);
+  if (*status) {
+    err = "creating the copy streams failed";
+    return nullptr;
+  }
+  return link;
+}
+
+std::unique_ptr<Link> make_hip_dma_link(int device, bool split_d2h, bool timing, std::string& err, int* status) {
+  (void)device;
+  auto link = std::make_unique<StreamLink>();
+  *status = link->init(StreamLink::kDma, 0, timing, split_d2h, nullptr, nullptr);
   if (*status) {
     err = "creating the copy streams failed";
     return nullptr;

@@ -11,8 +11,12 @@
 //                 copy -> compute : the host waits for the copy's HSA signal before it enqueues
 //                                   the dependent kernels (wait()).
 //               No GPU queue ever waits on host-written memory, and every wait is bounded.
-//   StreamLink  a copy kernel on dedicated HIP streams ordered with HIP events. Kept for
-//               comparison: shader copies contend with compute for compute units.
+//   StreamLink  copies on dedicated HIP streams, ordered with HIP events only (every wait is a
+//               hipStreamWaitEvent; the host never blocks for a copy). Two methods:
+//                 DMA          hipMemcpyAsync with hipMemcpyDeviceToDeviceNoCU between pinned
+//                              host and device memory, which the HIP runtime runs on the SDMA
+//                              engines; D2H optionally split in halves over two streams,
+//                 copy kernel  the engine's copy kernel (comparison: contends for CUs).
 //
 // A "gate" is the ordering point of one device slot (staging or restore): copies into or out
 // of the slot go through its gate, and the compute stream waits on the gate before it touches
@@ -80,5 +84,8 @@ std::unique_ptr<Link> make_sdma_link(int device, uint32_t d2h_engine, uint32_t h
 // `alias` maps a pinned host pointer to its device-visible address for the copy kernel.
 std::unique_ptr<Link> make_stream_link(int device, uint32_t copy_blocks, bool timing, char* (*alias)(void*, char*),
                                        void* alias_ctx, std::string& err, int* status);
+// SDMA copies through HIP streams (StreamLink, DMA method); split_d2h: D2H copies of 2 MiB or
+// more go out as two halves on two streams while no H2D is pending.
+std::unique_ptr<Link> make_hip_dma_link(int device, bool split_d2h, bool timing, std::string& err, int* status);
 
 }  // namespace mo

@@ -28,6 +28,7 @@ MO_FLAG_KERNEL_COPY = 0x2
 MO_FLAG_KERNEL_TIMING = 0x4
 MO_FLAG_NO_STAGED_RESTORE = 0x8
 MO_FLAG_EAGER_PACK = 0x10
+MO_FLAG_HIP_DMA = 0x20
 MO_TENSOR_BF16_HIGH = 0x1
 
 NO_GROUP = (1 << 64) - 1

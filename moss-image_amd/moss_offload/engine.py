@@ -41,6 +41,11 @@ class EngineConfig:
     timing: bool = False
     kernel_timing: bool = False
     kernel_copy: bool = False
+    # Host-link transport: "sdma" drives the SDMA engines through the HSA runtime (an issuer
+    # thread orders copies; an unpack waits on the host for its H2D), "hipdma" enqueues the same
+    # DMA copies on dedicated HIP streams ordered by hipStreamWaitEvent only (an unpack never
+    # blocks the host). kernel_copy=True overrides both with the copy-kernel comparison.
+    link: str = "sdma"
     copy_kernel_blocks: int = 16
     d2h_engine: int = 0
     h2d_engine: int = 0
@@ -84,7 +89,10 @@ class EngineConfig:
             | (_native.MO_FLAG_KERNEL_TIMING if self.kernel_timing else 0)
             | (0 if self.staged_restore else _native.MO_FLAG_NO_STAGED_RESTORE)
             | (0 if self.batch_packs else _native.MO_FLAG_EAGER_PACK)
+            | (_native.MO_FLAG_HIP_DMA if self.link == "hipdma" else 0)
         )
+        if self.link not in ("sdma", "hipdma"):
+            raise ValueError(f"link must be 'sdma' or 'hipdma', got {self.link!r}")
         cfg.copy_kernel_blocks = self.copy_kernel_blocks
         cfg.d2h_engine = self.d2h_engine
         cfg.h2d_engine = self.h2d_engine

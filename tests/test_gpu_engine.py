@@ -55,12 +55,15 @@ def _restore_and_check(engine, handles, device, order):
 
 
 @pytest.mark.parametrize("staged", [False, True])
-@pytest.mark.parametrize("kernel_copy", [False, True])
+@pytest.mark.parametrize("link", ["sdma", "hipdma", "kernel"])
 @pytest.mark.parametrize("seed", [0, 1])
-def test_groups_round_trip_lifo(seed, kernel_copy, staged) -> None:
+def test_groups_round_trip_lifo(seed, link, staged) -> None:
     device = torch.device("cuda", 0)
-    engine = _engine(kernel_copy=kernel_copy, timing=True, staged_restore=staged)
-    assert engine.link_name() == ("kernel" if kernel_copy else "sdma")
+    if link == "kernel":
+        engine = _engine(kernel_copy=True, timing=True, staged_restore=staged)
+    else:
+        engine = _engine(link=link, timing=True, staged_restore=staged)
+    assert engine.link_name() == link
     rng = random.Random(seed)
     stream = torch.cuda.current_stream(device).cuda_stream
     handles = []
@@ -91,6 +94,39 @@ def test_groups_round_trip_lifo(seed, kernel_copy, staged) -> None:
     stats = engine.stats()
     assert stats["groups_live"] == 0 and stats["host_bytes_in_use"] == 0
     assert stats["d2h_ms"] > 0 and stats["timed_d2h_bytes"] == stats["bytes_d2h"]
+    if link != "sdma":
+        assert stats["host_blocks"] == 0  # every copy -> compute order is a stream wait
+    engine.close()
+
+
+@pytest.mark.parametrize("d2h_engine", [0, 1])
+def test_hipdma_link_split_and_single_d2h_round_trip(d2h_engine) -> None:
+    # 8 MiB slots so that D2H copies reach the 2 MiB split size; d2h_engine=1 keeps one stream.
+    device = torch.device("cuda", 0)
+    cfg = EngineConfig(stage_slot_bytes=8 * MiB, stage_slots=3, restore_slots=2, host_chunk_bytes=32 * MiB,
+                       link="hipdma", d2h_engine=d2h_engine, timing=True)
+    engine = OffloadEngine(device, cfg)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    rng = random.Random(7 + d2h_engine)
+    handles, groups = [], []
+    for g in range(5):
+        members = []
+        for t in _tensors(rng, rng.randint(2, 8), device, big=True):
+            gid, idx = engine.pack(t, stream)
+            handles.append((t, gid, idx))
+            members.append(len(handles) - 1)
+        engine.commit(stream)
+        groups.append(members)
+    order = [i for members in reversed(groups) for i in reversed(members)]
+    _restore_and_check(engine, handles, device, order)
+    torch.cuda.synchronize(device)
+    for _, gid, idx in handles:
+        engine.drop(gid, idx)
+    engine.synchronize()
+    stats = engine.stats()
+    assert stats["copy_failures"] == 0 and stats["host_blocks"] == 0
+    assert stats["groups_live"] == 0 and stats["host_bytes_in_use"] == 0
+    assert stats["timed_d2h_bytes"] == stats["bytes_d2h"] > 0
     engine.close()
 
 

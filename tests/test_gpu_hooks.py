@@ -165,6 +165,40 @@ def test_bf16_lora_step_within_north_star_tolerance(checkpointing) -> None:
     _compare(actual, expected, rtol=1e-3, atol=1e-5)
 
 
+@pytest.fixture
+def hipdma_engine():
+    """Engines created inside the test use the HIP-stream DMA transport."""
+
+    from moss_offload import engine as engine_mod
+
+    engine_mod.reset_engines()
+    previous = engine_mod.configure()
+    engine_mod.configure(link="hipdma")
+    yield
+    gc.collect()
+    torch.cuda.synchronize()
+    engine_mod.reset_engines()
+    engine_mod.configure(link=previous.link)
+
+
+@pytest.mark.parametrize("checkpointing", [False, True])
+def test_hipdma_link_bf16_lora_step_restores_bit_exact(hipdma_engine, checkpointing) -> None:
+    from moss_offload import engine as engine_mod
+
+    device = torch.device("cuda", 0)
+    torch.manual_seed(904)
+    model = _tiny(layers=4, checkpointing=checkpointing, lora=True, dim=64, ffn=128).to(device).train()
+    latents, contexts = _inputs(device, shapes=((4, 8, 8),), text=(12,))
+    expected = _run(model, moss_offload.activation_cpu_offload, False, latents, contexts, autocast=True)
+    _Recording.checked = 0
+    actual = _run(model, _recording_context, True, latents, contexts, autocast=True)
+    assert _Recording.checked > 0
+    _compare(actual, expected, rtol=1e-3, atol=1e-5)
+    engine = engine_mod.get_engine(device)
+    assert engine.link_name() == "hipdma"
+    assert engine.stats()["host_blocks"] == 0
+
+
 def test_retain_graph_subset_grad_and_dropped_graph() -> None:
     device = torch.device("cuda", 0)
     torch.manual_seed(905)
