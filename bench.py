@@ -488,7 +488,7 @@ def calibration_copy(device, stream: int, repeats: int = 3) -> None:
 
 
 def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: int, restore_slots: int,
-          batch_packs: bool = True, d2h_engine: int = 0, h2d_engine: int = 0, narrow=None):
+          batch_packs: bool = True, d2h_engine: int = 0, h2d_engine: int = 0, narrow=None, link: str = "sdma"):
     """one regime-B block's saved set through pack -> D2H -> H2D -> unpack.
 
     Every iteration packs the block's tensors into one group (staging ring + SDMA D2H), commits
@@ -504,7 +504,7 @@ def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: 
     engine = OffloadEngine(device, EngineConfig(
         stage_slot_bytes=slot_mib << 20, stage_slots=stage_slots, restore_slots=restore_slots,
         timing=True, kernel_timing=True, staged_restore=False, prefetch=False, batch_packs=batch_packs,
-        d2h_engine=d2h_engine, h2d_engine=h2d_engine))
+        d2h_engine=d2h_engine, h2d_engine=h2d_engine, link=link))
     stream = torch.cuda.current_stream(device).cuda_stream
     payload = sum(t.numel() * t.element_size() for t in tensors)
     storages = {}
@@ -838,7 +838,8 @@ def run(args) -> dict:
             f"({sum(narrow)} bf16 casts narrowed: {moved / 1e6:.1f} MB over the link)")
         result["micro"] = micro(device, tensors, args.micro_iters, args.micro_warmup, args.slot_mib,
                                 args.stage_slots, args.restore_slots, batch_packs=not args.eager_pack,
-                                d2h_engine=args.d2h_engine, h2d_engine=args.h2d_engine, narrow=narrow)
+                                d2h_engine=args.d2h_engine, h2d_engine=args.h2d_engine, narrow=narrow,
+                                link=args.link)
         result["micro"].update(narrowed_tensors=sum(narrow), link_bytes_per_iter=moved)
         m = result["micro"]
         log(f"micro: {m['s_per_iter'] * 1e3:.2f} ms/iter, D2H {m['d2h_gbps']:.1f} GB/s, H2D {m['h2d_gbps']:.1f} GB/s, "

@@ -11,6 +11,9 @@ from .activation_offload import (
     _restore_layout,
     _storage_key,
     activation_cpu_offload,
+    hook_counters,
+    hook_features,
+    reset_hook_counters,
 )
 from .engine import EngineConfig, OffloadEngine, configure, get_engine, reset_engines
 
@@ -20,6 +23,9 @@ __all__ = [
     "_restore_layout",
     "_storage_key",
     "_OffloadedTensor",
+    "hook_counters",
+    "hook_features",
+    "reset_hook_counters",
     "EngineConfig",
     "OffloadEngine",
     "configure",

@@ -21,7 +21,9 @@ strides. Block boundaries come from forward hooks on ``model.layers``.
 
 from __future__ import annotations
 
+import collections
 import threading
+import warnings
 import weakref
 from contextlib import nullcontext
 from typing import ContextManager
@@ -259,6 +261,77 @@ def _cast_origin(tensor: torch.Tensor):
 
 _VIEW_NODES = ("ViewBackward0", "UnsafeViewBackward0", "ReshapeAliasBackward0")
 
+# What the pack hook did with each save, summed over every context of the process:
+#   resident      kept on the device (non-CUDA, parameter/buffer/staging storage, layout the
+#                 reference keeps resident, keep_last_blocks)
+#   offloaded     a new engine entry (its payload crosses the link)
+#   narrowed      of those, float32 casts sent as their bfloat16 high halves
+#   deduplicated  a view of bytes already offloaded: a second reference to that entry
+#   derived       a torch.mul product recomputed on unpack (nothing crosses the link)
+#   aliased       a second cast compared on the device with an earlier one
+#   empty         a save with no elements
+_COUNTS: collections.Counter = collections.Counter()
+
+
+def hook_counters() -> dict[str, int]:
+    """What the pack hook did with the saves it has seen (see ``_COUNTS``)."""
+
+    return dict(_COUNTS)
+
+
+def reset_hook_counters() -> None:
+    _COUNTS.clear()
+
+
+def hook_features() -> dict[str, bool]:
+    """Which graph-reading features of the pack hook work on the running torch.
+
+    Narrowed casts, recomputed products and aliased equal casts read private autograd state
+    (``ToCopyBackward0`` input metadata, ``MulBackward0``'s saved scalar, node edges). Each
+    fails closed: when the state is missing the save is offloaded whole. This probes each on a
+    tiny CPU graph, so a torch upgrade that removes one shows here instead of only as more
+    bytes over the link.
+    """
+
+    out = {}
+    source = torch.ones(8, dtype=torch.bfloat16, requires_grad=True)
+    cast = source.float()
+    out["narrow_bf16_casts"] = _bf16_exact(cast, cast)
+    out["alias_equal_casts"] = _cast_origin(cast) is not None
+    base = torch.ones(8, requires_grad=True) * 1.0
+    try:
+        product = base * 3.0
+        fn = product.grad_fn
+        ok = type(fn).__name__ == "MulBackward0" and fn._raw_saved_other.unpack_hook is None
+        other = fn._saved_other
+        ok = ok and isinstance(other, torch.Tensor) and other.dim() == 0 and float(other) == 3.0
+        ok = ok and fn.next_functions[0][0] is base.grad_fn
+    except (AttributeError, IndexError, RuntimeError):
+        ok = False
+    out["recompute_products"] = bool(ok)
+    return out
+
+
+_REPORTED = False
+
+
+def _report_features(config) -> None:
+    """Warn once per process about a configured feature the running torch cannot support."""
+
+    global _REPORTED
+    if _REPORTED:
+        return
+    _REPORTED = True
+    features = hook_features()
+    missing = [name for name, ok in features.items() if getattr(config, name, False) and not ok]
+    if missing:
+        warnings.warn(
+            "activation offload: " + ", ".join(missing) + " unavailable on torch " + torch.__version__
+            + " (private autograd state missing); those saves are offloaded whole",
+            RuntimeWarning,
+            stacklevel=3,
+        )
+
 
 def _numel(shape) -> int:
     n = 1
@@ -284,6 +357,7 @@ class _ActivationOffload:
         self.narrow = self.engine.config.narrow_bf16_casts
         self.recompute = self.engine.config.recompute_products
         self.alias = getattr(self.engine.config, "alias_equal_casts", False)
+        _report_features(self.engine.config)
         # cast origin (autograd node, output index) -> (handle, weak ref, version, stream) of an
         # offloaded cast, and the aliases whose device comparison has no result yet
         self._casts: dict[tuple, tuple] = {}
@@ -359,22 +433,27 @@ class _ActivationOffload:
 
     def pack(self, tensor: torch.Tensor):
         if tensor.device.type != "cuda" or tensor.layout != torch.strided or self.is_weight_backed(tensor):
+            _COUNTS["resident"] += 1
             return tensor
         if self._keep_from is not None and self._block is not None and self._block >= self._keep_from:
+            _COUNTS["resident"] += 1
             return tensor  # keep_last_blocks: needed first by backward
         view = _offload_view(tensor)
         if view is None or tensor.dim() > _native.MO_MAX_DIMS:
+            _COUNTS["resident"] += 1
             return tensor
         source, payload_shape = view
         shape, stride = tuple(tensor.shape), tuple(tensor.stride())
         device = tensor.device
         if source.numel() == 0:
+            _COUNTS["empty"] += 1
             return _OffloadedTensor(None, None, 0, device, tensor.dtype, shape, stride, payload_shape)
         if self._pending:
             self._poll()
         if self.recompute:
             derived = self._derive(tensor)
             if derived is not None:
+                _COUNTS["derived"] += 1
                 self._remember(tensor, derived)
                 return derived
         stream = torch.cuda.current_stream(device).cuda_stream
@@ -382,6 +461,7 @@ class _ActivationOffload:
         if origin is not None:
             alias = self._alias(tensor, origin, stream)
             if alias is not None:
+                _COUNTS["aliased"] += 1
                 self._remember(tensor, alias)
                 return alias
         key = None
@@ -393,11 +473,15 @@ class _ActivationOffload:
             if hit is not None:
                 ref, version, gid, idx = hit
                 if not ref.expired() and version == tensor._version and self.engine.acquire(gid, idx):
+                    _COUNTS["deduplicated"] += 1
                     self._shared.add(gid)
                     handle = _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
                     self._remember(tensor, handle)
                     return handle
-        gid, idx = self.engine.pack(source, stream, narrow=self.narrow and _bf16_exact(tensor, source))
+        narrow = self.narrow and _bf16_exact(tensor, source)
+        gid, idx = self.engine.pack(source, stream, narrow=narrow)
+        _COUNTS["offloaded"] += 1
+        _COUNTS["narrowed"] += narrow
         if key is not None:
             self._seen[key] = (StorageWeakRef(tensor.untyped_storage()), tensor._version, gid, idx)
         handle = _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)

@@ -409,3 +409,44 @@ def test_equal_casts_are_aliased_only_after_the_bytes_compare_equal() -> None:
     ctx._pending.clear()
     del alias
     assert ctx.engine.discarded == [1]
+
+
+def test_hook_features_probe_reports_each_graph_reading_feature() -> None:
+    # On this torch every feature works; when a probe's private state is gone it reports it off
+    # (and the hook then offloads those saves whole).
+    from moss_offload import activation_offload as ao
+
+    assert moss_offload.hook_features() == {
+        "narrow_bf16_casts": True,
+        "alias_equal_casts": True,
+        "recompute_products": True,
+    }
+    original = ao._bf16_exact
+    try:
+        ao._bf16_exact = lambda tensor, source: False
+        assert moss_offload.hook_features()["narrow_bf16_casts"] is False
+    finally:
+        ao._bf16_exact = original
+    original = ao._cast_origin
+    try:
+        ao._cast_origin = lambda tensor: None
+        assert moss_offload.hook_features()["alias_equal_casts"] is False
+    finally:
+        ao._cast_origin = original
+
+
+def test_missing_feature_is_reported_once_as_a_warning(monkeypatch) -> None:
+    import warnings
+
+    from moss_offload import activation_offload as ao
+
+    monkeypatch.setattr(ao, "_REPORTED", False)
+    monkeypatch.setattr(ao, "hook_features", lambda: {"narrow_bf16_casts": False, "alias_equal_casts": True,
+                                                      "recompute_products": True})
+    config = engine.EngineConfig()
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        ao._report_features(config)
+        ao._report_features(config)
+    messages = [str(w.message) for w in caught]
+    assert len(messages) == 1 and "narrow_bf16_casts" in messages[0]
