@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 8
+#define MO_ABI_VERSION 9
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -281,6 +281,44 @@ int mo_streamer_acquire(mo_streamer* streamer, uint32_t slot, uint64_t stream);
 /* The slot may be refilled once `stream` reaches this point. Replaces the slot.reusable events
  * of memory.py:193-225. */
 int mo_streamer_release(mo_streamer* streamer, uint32_t slot, uint64_t stream);
+
+/* ---- block ring: residency decided by the streamer (no reference counterpart as an ABI: the
+ * reference keeps this state in Python, training/memory.py:142-191 and
+ * training/trainable_offload.py:194-287). A block is identified by the caller's integer id and
+ * its pinned master (host address and size); every slot is a device buffer the caller attaches.
+ * A slot's generation counts its fills: calls naming a slot present the generation that
+ * mo_streamer_stage returned and fail with MO_E_STATE once the slot holds another block. */
+
+/* Give slot `slot` its device buffer of `capacity` bytes (dev 0 detaches an empty slot). */
+int mo_streamer_attach(mo_streamer* streamer, uint32_t slot, uint64_t dev, uint64_t capacity);
+
+/* Make block `block` resident: if a slot holds it, *slot names that slot and nothing is
+ * copied (*filled = 0). Otherwise a slot is chosen (an empty one, else the least recently
+ * staged one that is not pinned, does not hold `keep` and is large enough), its block is
+ * written back first if the slot is dirty, and a fill of `bytes` from `host` is issued behind
+ * the slot's last release point (*filled = 1). MO_E_STATE when no slot can be chosen. Never
+ * blocks the host. Replaces AsyncBlockStreamer._stage (memory.py:157-191) and the eviction and
+ * refill of TrainableBlockStreamer (trainable_offload.py:245-287). */
+int mo_streamer_stage(mo_streamer* streamer, int64_t block, uint64_t host, uint64_t bytes, int64_t keep,
+                      uint32_t* slot, uint64_t* generation, int* filled);
+
+/* A running execution reads the slot: while pinned it is never chosen for another block. */
+int mo_streamer_pin(mo_streamer* streamer, uint32_t slot, uint64_t generation);
+
+/* The execution is done with the slot once `stream` gets here: drops one pin and records the
+ * slot's release point (write-back and refill wait for it). */
+int mo_streamer_unpin(mo_streamer* streamer, uint32_t slot, uint64_t generation, uint64_t stream);
+
+/* Whether the slot's contents were updated on the device since its fill (copied back to the
+ * block's master before the slot takes another block, or at mo_streamer_evict). */
+int mo_streamer_mark_dirty(mo_streamer* streamer, uint32_t slot, uint64_t generation, int dirty);
+
+/* Empty an unpinned slot (writing a dirty block back first). */
+int mo_streamer_evict(mo_streamer* streamer, uint32_t slot);
+
+/* The slot's block (-1 = none), pins, dirty flag and generation (any output may be NULL). */
+int mo_streamer_slot_info(mo_streamer* streamer, uint32_t slot, int64_t* block, uint32_t* pins, int* dirty,
+                          uint64_t* generation);
 
 int mo_streamer_synchronize(mo_streamer* streamer);
 int mo_streamer_get_stats(mo_streamer* streamer, mo_streamer_stats* stats);

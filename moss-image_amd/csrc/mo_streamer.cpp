@@ -1,4 +1,12 @@
-// Frozen-block streaming: the native side of moss_offload.memory.AsyncBlockStreamer.
+// Block streaming: the native side of moss_offload.memory.AsyncBlockStreamer (frozen blocks)
+// and moss_offload.trainable_offload.TrainableBlockStreamer (blocks updated in place).
+//
+// The ring (mo_streamer_stage .. mo_streamer_slot_info) decides residency: which block each
+// device slot holds, how many running executions still read it (pins), whether it was written
+// on the device since its fill (dirty: copied back to its master before the slot is reused), and
+// which slot a new block replaces (an empty one, else the least recently staged that is neither
+// pinned nor kept for the block about to run beside it). Python only asks for a block and gets
+// a slot and its fill generation, which every later call on that slot must present.
 //
 // Replaces what training/memory.py does on its copy stream (AsyncBlockStreamer._stage,
 // memory.py:157-191, and the ready/reusable events of :193-225, :246-247): the frozen
@@ -33,12 +41,25 @@ int set_error(int code, const std::string& msg);
 int set_hip_error(int e, const char* what);
 }  // namespace mo
 
+// Residency of one device slot in the block ring (mo_streamer_stage and the calls after it).
+struct RingSlot {
+  uint64_t dev = 0, capacity = 0;  // the caller's device buffer (mo_streamer_attach)
+  int64_t block = -1;              // block held, -1 = none
+  uint64_t host = 0, bytes = 0;    // that block's pinned master
+  uint32_t pins = 0;               // executions still reading the slot
+  bool dirty = false;              // written on the device since its fill
+  uint64_t generation = 0;         // bumped by every fill
+  uint64_t last_use = 0;           // tick of the last stage that returned this slot
+};
+
 struct mo_streamer {
   std::mutex mu;
   int device = 0;
   std::unique_ptr<mo::Link> link;
   std::vector<int> gates;        // one per slot
   std::vector<mo::CopyRef> pending_writeback;  // per slot: the next fill waits for it
+  std::vector<RingSlot> ring;    // per slot
+  uint64_t tick = 0;
   uint64_t fills = 0, bytes = 0, writebacks = 0, writeback_bytes = 0;
 };
 
@@ -77,6 +98,49 @@ int check_slot(mo_streamer* s, uint32_t slot) {
   if (slot >= s->gates.size())
     return mo::set_error(MO_E_INVALID, "slot " + std::to_string(slot) + " out of range (" +
                                            std::to_string(s->gates.size()) + " slots)");
+  return 0;
+}
+
+int issue_fill(mo_streamer* s, uint32_t slot, uint64_t dst, uint64_t src, uint64_t bytes) {
+  mo::CopyRef copy;
+  if (int rc = s->link->h2d((void*)dst, (const void*)src, bytes, s->pending_writeback[slot], s->gates[slot], &copy))
+    return mo::set_hip_error(rc, "slot fill (SDMA H2D)");
+  s->pending_writeback[slot].reset();
+  s->fills++;
+  s->bytes += bytes;
+  return 0;
+}
+
+int issue_writeback(mo_streamer* s, uint32_t slot, uint64_t dst, uint64_t src, uint64_t bytes) {
+  mo::CopyRef copy;
+  if (int rc = s->link->writeback((void*)dst, (const void*)src, bytes, s->gates[slot], &copy))
+    return mo::set_hip_error(rc, "slot write-back (SDMA D2H)");
+  s->pending_writeback[slot] = std::move(copy);
+  s->writebacks++;
+  s->writeback_bytes += bytes;
+  return 0;
+}
+
+// The slot's block leaves it: a dirty slot is first copied back to the block's master, after
+// the slot's last release point; its next fill is ordered behind that copy.
+int vacate(mo_streamer* s, uint32_t k) {
+  RingSlot& r = s->ring[k];
+  if (r.block >= 0 && r.dirty && r.bytes)
+    if (int rc = issue_writeback(s, k, r.host, r.dev, r.bytes)) return rc;
+  r.block = -1;
+  r.host = r.bytes = 0;
+  r.dirty = false;
+  r.pins = 0;
+  return 0;
+}
+
+int check_generation(mo_streamer* s, uint32_t slot, uint64_t generation, const char* what) {
+  if (int rc = check_slot(s, slot)) return rc;
+  const RingSlot& r = s->ring[slot];
+  if (r.block < 0 || r.generation != generation)
+    return mo::set_error(MO_E_STATE, std::string(what) + ": slot " + std::to_string(slot) +
+                                         " no longer holds the block it held at generation " +
+                                         std::to_string(generation));
   return 0;
 }
 
@@ -120,6 +184,7 @@ int mo_streamer_create(int device, uint32_t slots, uint32_t h2d_engine, mo_strea
       s->gates.push_back(g);
     }
     s->pending_writeback.resize(slots);
+    s->ring.resize(slots);
     *out = s.release();
     return 0;
   } catch (const std::exception& ex) {
@@ -145,13 +210,7 @@ int mo_streamer_fill(mo_streamer* s, uint32_t slot, uint64_t dst, uint64_t src, 
     if (int rc = check_slot(s, slot)) return rc;
     if (!dst || !src) return mo::set_error(MO_E_INVALID, "null fill address");
     if (bytes == 0) return 0;
-    mo::CopyRef copy;
-    if (int rc = s->link->h2d((void*)dst, (const void*)src, bytes, s->pending_writeback[slot], s->gates[slot], &copy))
-      return mo::set_hip_error(rc, "slot fill (SDMA H2D)");
-    s->pending_writeback[slot].reset();
-    s->fills++;
-    s->bytes += bytes;
-    return 0;
+    return issue_fill(s, slot, dst, src, bytes);
   });
 }
 
@@ -160,12 +219,119 @@ int mo_streamer_writeback(mo_streamer* s, uint32_t slot, uint64_t dst, uint64_t 
     if (int rc = check_slot(s, slot)) return rc;
     if (!dst || !src) return mo::set_error(MO_E_INVALID, "null write-back address");
     if (bytes == 0) return 0;
-    mo::CopyRef copy;
-    if (int rc = s->link->writeback((void*)dst, (const void*)src, bytes, s->gates[slot], &copy))
-      return mo::set_hip_error(rc, "slot write-back (SDMA D2H)");
-    s->pending_writeback[slot] = std::move(copy);
-    s->writebacks++;
-    s->writeback_bytes += bytes;
+    return issue_writeback(s, slot, dst, src, bytes);
+  });
+}
+
+int mo_streamer_attach(mo_streamer* s, uint32_t slot, uint64_t dev, uint64_t capacity) {
+  MO_STREAMER_CALL(s, {
+    if (int rc = check_slot(s, slot)) return rc;
+    RingSlot& r = s->ring[slot];
+    if (r.block >= 0) return mo::set_error(MO_E_STATE, "mo_streamer_attach: slot " + std::to_string(slot) + " holds a block");
+    r.dev = dev;
+    r.capacity = dev ? capacity : 0;
+    return 0;
+  });
+}
+
+int mo_streamer_stage(mo_streamer* s, int64_t block, uint64_t host, uint64_t bytes, int64_t keep, uint32_t* slot,
+                      uint64_t* generation, int* filled) {
+  MO_STREAMER_CALL(s, {
+    if (!slot || !generation || !filled) return mo::set_error(MO_E_INVALID, "null output");
+    if (block < 0 || !host) return mo::set_error(MO_E_INVALID, "mo_streamer_stage: bad block or master");
+    *filled = 0;
+    const uint64_t now = ++s->tick;
+    for (uint32_t k = 0; k < s->ring.size(); ++k) {
+      RingSlot& r = s->ring[k];
+      if (r.block == block) {
+        if (r.host != host || r.bytes != bytes)
+          return mo::set_error(MO_E_INVALID, "mo_streamer_stage: block " + std::to_string(block) +
+                                                 " staged with a different master");
+        r.last_use = now;
+        *slot = k;
+        *generation = r.generation;
+        return 0;
+      }
+    }
+    // the victim: an attached slot large enough, not pinned, not holding `keep`; an empty one
+    // first, else the one used longest ago
+    int best = -1;
+    for (uint32_t k = 0; k < s->ring.size(); ++k) {
+      const RingSlot& r = s->ring[k];
+      if (!r.dev || r.capacity < bytes || r.pins || (keep >= 0 && r.block == keep)) continue;
+      if (best < 0) {
+        best = (int)k;
+        continue;
+      }
+      const RingSlot& b = s->ring[best];
+      const bool empty = r.block < 0;
+      const bool bempty = b.block < 0;
+      if ((empty && !bempty) || (empty == bempty && r.last_use < b.last_use)) best = (int)k;
+    }
+    if (best < 0)
+      return mo::set_error(MO_E_STATE, "no staging slot can take block " + std::to_string(block) +
+                                           ": every slot is in use by a running block or holds the block kept beside it");
+    if (int rc = vacate(s, (uint32_t)best)) return rc;
+    RingSlot& r = s->ring[best];
+    if (bytes)
+      if (int rc = issue_fill(s, (uint32_t)best, r.dev, host, bytes)) return rc;
+    r.block = block;
+    r.host = host;
+    r.bytes = bytes;
+    r.generation++;
+    r.last_use = now;
+    *slot = (uint32_t)best;
+    *generation = r.generation;
+    *filled = 1;
+    return 0;
+  });
+}
+
+int mo_streamer_pin(mo_streamer* s, uint32_t slot, uint64_t generation) {
+  MO_STREAMER_CALL(s, {
+    if (int rc = check_generation(s, slot, generation, "mo_streamer_pin")) return rc;
+    s->ring[slot].pins++;
+    return 0;
+  });
+}
+
+int mo_streamer_unpin(mo_streamer* s, uint32_t slot, uint64_t generation, uint64_t stream) {
+  MO_STREAMER_CALL(s, {
+    if (int rc = check_generation(s, slot, generation, "mo_streamer_unpin")) return rc;
+    RingSlot& r = s->ring[slot];
+    if (!r.pins) return mo::set_error(MO_E_STATE, "mo_streamer_unpin: slot " + std::to_string(slot) + " is not pinned");
+    if (int rc = s->link->consumed(s->gates[slot], (hipStream_t)stream)) return mo::set_hip_error(rc, "slot release");
+    r.pins--;
+    return 0;
+  });
+}
+
+int mo_streamer_mark_dirty(mo_streamer* s, uint32_t slot, uint64_t generation, int dirty) {
+  MO_STREAMER_CALL(s, {
+    if (int rc = check_generation(s, slot, generation, "mo_streamer_mark_dirty")) return rc;
+    s->ring[slot].dirty = dirty != 0;
+    return 0;
+  });
+}
+
+int mo_streamer_evict(mo_streamer* s, uint32_t slot) {
+  MO_STREAMER_CALL(s, {
+    if (int rc = check_slot(s, slot)) return rc;
+    if (s->ring[slot].pins)
+      return mo::set_error(MO_E_STATE, "mo_streamer_evict: slot " + std::to_string(slot) + " is in use by a running block");
+    return vacate(s, slot);
+  });
+}
+
+int mo_streamer_slot_info(mo_streamer* s, uint32_t slot, int64_t* block, uint32_t* pins, int* dirty,
+                          uint64_t* generation) {
+  MO_STREAMER_CALL(s, {
+    if (int rc = check_slot(s, slot)) return rc;
+    const RingSlot& r = s->ring[slot];
+    if (block) *block = r.block;
+    if (pins) *pins = r.pins;
+    if (dirty) *dirty = r.dirty ? 1 : 0;
+    if (generation) *generation = r.generation;
     return 0;
   });
 }

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 8
+MO_ABI_VERSION = 9
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -200,6 +200,15 @@ SIGNATURES: dict[str, tuple] = {
     "mo_streamer_writeback": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64, _u64, _u64]),
     "mo_streamer_acquire": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64]),
     "mo_streamer_release": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64]),
+    "mo_streamer_attach": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64, _u64]),
+    "mo_streamer_stage": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, _u64, _u64, ctypes.c_int64,
+                                         _P(ctypes.c_uint32), _P(_u64), _P(ctypes.c_int)]),
+    "mo_streamer_pin": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64]),
+    "mo_streamer_unpin": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64, _u64]),
+    "mo_streamer_mark_dirty": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _u64, ctypes.c_int]),
+    "mo_streamer_evict": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32]),
+    "mo_streamer_slot_info": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, _P(ctypes.c_int64),
+                                             _P(ctypes.c_uint32), _P(ctypes.c_int), _P(_u64)]),
     "mo_streamer_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
     "mo_streamer_get_stats": (ctypes.c_int, [ctypes.c_void_p, _P(MoStreamerStats)]),
     "mo_streamer_reset_stats": (ctypes.c_int, [ctypes.c_void_p]),
