@@ -152,6 +152,22 @@ int mo_gather(const mo_tensor* tensors, int n, uint64_t payload, const uint64_t*
 int mo_scatter(const mo_tensor* tensors, int n, uint64_t payload, const uint64_t* offsets,
                uint64_t stream);
 
+/* Gather n tensor views, in the payload format of mo_gather, into pinned host memory at `host`
+ * (host_bytes long) on `stream`, allocating nothing. offsets[i] (may be NULL) receives each
+ * payload's offset, as mo_payload_layout gives it; bytes between payloads are unspecified. The
+ * pack kernel gathers into a device scratch array that is part of the library's code object
+ * (64 MiB per device, reserved when the code object loads on that device and held until the
+ * process ends), then a DMA copies the payload to `host`. Payloads larger than the scratch are
+ * rejected with MO_E_INVALID, as is a host buffer that is too small or not pinned.
+ * No counterpart in the reference (it pins a fresh tensor per save, activation_offload.py:123):
+ * a variant of mo_pack for callers that cannot allocate, such as code under HIP graph capture or
+ * a serving loop that must not touch the allocator. The first call on a device loads the code
+ * object (set-up, not capturable); later calls only enqueue a kernel and a copy. Every call on
+ * one device shares its scratch: calls that overlap on that device (different streams with no
+ * order between them) race. */
+int mo_pack_to_host(const mo_tensor* tensors, int n, uint64_t host, uint64_t host_bytes, uint64_t* offsets,
+                    uint64_t stream);
+
 /* Copy `bytes` between device and pinned host memory with the engine's link-copy kernel
  * (direction 0 = device->host, 1 = host->device). Measures the copy-kernel alternative to
  * the DMA engines. */

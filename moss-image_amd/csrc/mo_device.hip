@@ -27,6 +27,14 @@
 
 #include "mo_kdesc.h"
 
+// The scratch of mo_pack_to_host (size kNoAllocScratchBytes). External linkage with a C name:
+// the host finds it in the loaded code object with hipModuleGetGlobal, once per device, and
+// passes that address to the pack kernel like any payload buffer (a static array would have no
+// symbol in the code object). Only the pack kernel writes it and the DMA reads it.
+extern "C" {
+__device__ __align__(256) unsigned char mo_noalloc_scratch[mo::kNoAllocScratchBytes];
+}
+
 namespace mo {
 
 __device__ __forceinline__ uint32_t fdiv(uint32_t n, uint32_t m, uint32_t s) {

@@ -1005,6 +1005,42 @@ int mo_scatter(const mo_tensor* tensors, int n, uint64_t payload, const uint64_t
   MO_GUARD_END
 }
 
+int mo_pack_to_host(const mo_tensor* tensors, int n, uint64_t host, uint64_t host_bytes, uint64_t* offsets,
+                    uint64_t stream) {
+  MO_GUARD_BEGIN
+  if (n < 0 || (n > 0 && !tensors) || !host) return mo::fail(MO_E_INVALID, "mo_pack_to_host: bad arguments");
+  std::vector<mo::Canon> cs;
+  std::vector<uint64_t> offs;
+  uint64_t total = 0;
+  if (int rc = mo::build_layout(tensors, n, cs, offs, &total)) return rc;
+  if (total > mo::kNoAllocScratchBytes)
+    return mo::fail(MO_E_INVALID, "mo_pack_to_host: a payload of " + std::to_string(total) +
+                                      " bytes exceeds its device scratch of " +
+                                      std::to_string(mo::kNoAllocScratchBytes) +
+                                      " bytes; split the tensors over several calls");
+  if (total > host_bytes)
+    return mo::fail(MO_E_INVALID, "mo_pack_to_host: the host buffer holds " + std::to_string(host_bytes) +
+                                      " bytes, the payload needs " + std::to_string(total));
+  // The DMA needs page-locked memory: a pageable buffer would make the runtime stage the copy
+  // through memory of its own.
+  hipPointerAttribute_t attr{};
+  if (hipPointerGetAttributes(&attr, (const void*)host) != hipSuccess || attr.type != hipMemoryTypeHost) {
+    (void)hipGetLastError();
+    return mo::fail(MO_E_INVALID, "mo_pack_to_host: the host buffer must be pinned (hipHostMalloc or pin_memory)");
+  }
+  uint64_t scratch = 0, scratch_bytes = 0;
+  if (int rc = mo::noalloc_scratch(&scratch, &scratch_bytes)) return mo::hip_fail(rc, "loading the device code object");
+  if (total) {
+    if (int rc = mo::run_copy(true, tensors, n, scratch, offs.data(), stream)) return rc;
+    hipError_t e = hipMemcpyAsync((void*)host, (const void*)scratch, total, hipMemcpyDeviceToHost, (hipStream_t)stream);
+    if (e != hipSuccess) return mo::hip_fail((int)e, "mo_pack_to_host: D2H copy of the payload");
+  }
+  if (offsets)
+    for (int i = 0; i < n; ++i) offsets[i] = offs[i];
+  return 0;
+  MO_GUARD_END
+}
+
 int mo_link_copy(uint64_t dst, uint64_t src, uint64_t bytes, int direction, uint32_t blocks, uint64_t stream) {
   MO_GUARD_BEGIN
   (void)direction;

@@ -52,6 +52,10 @@ class Launcher {
 
 int launch_link_copy(void* dst, const void* src, uint64_t bytes, uint32_t blocks, hipStream_t stream);
 
+// Device address and size of the current device's mo_noalloc_scratch (loads the code object on
+// first use on the device).
+int noalloc_scratch(uint64_t* ptr, uint64_t* bytes);
+
 // mo_equal_kernel over nbytes at a and b (16-byte aligned); writes 1 to *flag on a difference.
 int launch_equal(const void* a, const void* b, uint64_t nbytes, uint32_t* flag, hipStream_t stream);
 

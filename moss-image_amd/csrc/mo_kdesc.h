@@ -15,6 +15,10 @@ constexpr int kMaxOuter = MO_MAX_DIMS - 1;    // canonical dims beyond the inner
 constexpr int kMaxDesc = 16;                  // pieces per launch (kernel-argument budget)
 constexpr uint32_t kMaxTilesPerLaunch = 1u << 22;
 constexpr int kLinkUnroll = 8;                // 16-byte transfers in flight per lane (link copy)
+// Device scratch of mo_pack_to_host (the entry point that allocates nothing): a payload gathered
+// there waits for its DMA to the caller's pinned host buffer. One array per device, part of the
+// code object, so it is reserved when the code object is loaded and kept until the process ends.
+constexpr uint64_t kNoAllocScratchBytes = 64ull << 20;
 
 // NARROW: contiguous float32 on the tensor side, its high halves (bfloat16 bits) as the
 // payload; `first` and `nbytes` count payload bytes, the tensor side is twice that.

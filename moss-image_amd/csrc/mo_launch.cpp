@@ -36,6 +36,8 @@ struct DeviceModule {
   hipFunction_t pack = nullptr, unpack = nullptr, link = nullptr;
   hipFunction_t pack1 = nullptr, unpack1 = nullptr;  // single-piece launches
   hipFunction_t equal = nullptr;
+  // this device's copy of mo_noalloc_scratch (every device holds its own, at its own address)
+  uint64_t scratch = 0, scratch_bytes = 0;
 };
 
 std::mutex g_modules_mu;
@@ -50,6 +52,14 @@ int load_functions(DeviceModule& m) {
   if ((e = hipModuleGetFunction(&m.pack1, m.module, "mo_pack1_kernel")) != hipSuccess) return (int)e;
   if ((e = hipModuleGetFunction(&m.unpack1, m.module, "mo_unpack1_kernel")) != hipSuccess) return (int)e;
   if ((e = hipModuleGetFunction(&m.equal, m.module, "mo_equal_kernel")) != hipSuccess) return (int)e;
+  // Set-up of the allocation-free entry point, once per device with that device current: the
+  // device address of this module's scratch array. From here on only this address is used.
+  hipDeviceptr_t scratch = nullptr;
+  size_t bytes = 0;
+  if ((e = hipModuleGetGlobal(&scratch, &bytes, m.module, "mo_noalloc_scratch")) != hipSuccess) return (int)e;
+  if (!scratch || bytes != kNoAllocScratchBytes || (uint64_t)scratch % 256) return (int)hipErrorInvalidSymbol;
+  m.scratch = (uint64_t)scratch;
+  m.scratch_bytes = bytes;
   return 0;
 }
 
@@ -68,6 +78,15 @@ static int module_of_device(DeviceModule* out) {
     it = g_modules.emplace(device, m).first;
   }
   *out = it->second;
+  return 0;
+}
+
+// The current device's scratch of mo_pack_to_host (its code object loaded on first use).
+int noalloc_scratch(uint64_t* ptr, uint64_t* bytes) {
+  DeviceModule m;
+  if (int rc = module_of_device(&m)) return rc;
+  *ptr = m.scratch;
+  *bytes = m.scratch_bytes;
   return 0;
 }
 

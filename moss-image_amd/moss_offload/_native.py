@@ -171,6 +171,7 @@ SIGNATURES: dict[str, tuple] = {
     "mo_gather": (ctypes.c_int, [_P(MoTensor), ctypes.c_int, _u64, _P(_u64), _u64]),
     "mo_scatter": (ctypes.c_int, [_P(MoTensor), ctypes.c_int, _u64, _P(_u64), _u64]),
     "mo_link_copy": (ctypes.c_int, [_u64, _u64, _u64, ctypes.c_int, ctypes.c_uint32, _u64]),
+    "mo_pack_to_host": (ctypes.c_int, [_P(MoTensor), ctypes.c_int, _u64, _u64, _P(_u64), _u64]),
     "mo_create": (ctypes.c_int, [ctypes.c_int, _P(MoConfig), _P(ctypes.c_void_p)]),
     "mo_destroy": (ctypes.c_int, [ctypes.c_void_p]),
     "mo_pack": (ctypes.c_int, [ctypes.c_void_p, _P(MoTensor), ctypes.c_int, _u64, _P(MoRef)]),
