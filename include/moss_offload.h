@@ -59,6 +59,16 @@ extern "C" {
                                       2 MiB or more are split over two copy streams while no
                                       H2D is pending, unless d2h_engine has exactly one bit */
 
+/* Cache policy of the kernels. Default: pack reads saved tensors with ordinary loads and writes
+   the staging slot with streaming (non-temporal) stores; unpack reads the restore slot with
+   non-temporal loads and writes restored tensors with streaming stores. */
+#define MO_FLAG_PACK_NT_LOAD 0x40  /* the pack kernel reads saved tensors with non-temporal
+                                      (streaming) loads                                   */
+#define MO_FLAG_UNPACK_CACHED_LOAD 0x80 /* the unpack kernel reads the payload with ordinary
+                                           loads instead of non-temporal ones             */
+#define MO_FLAG_UNPACK_CACHED_STORE 0x100 /* the unpack kernel writes restored tensors with
+                                             ordinary stores instead of streaming ones      */
+
 /*
  * A strided tensor view on the device. `ptr` is the address of logical element (0,...,0),
  * which is the lowest address because all strides are non-negative. Strides are in

@@ -121,6 +121,47 @@ __device__ __forceinline__ void st16_stream(char* p, uint4 v) {
   const mo_u32x4 x = {v.x, v.y, v.z, v.w};
   __builtin_nontemporal_store(x, (MO_GLOBAL mo_u32x4*)p);
 }
+
+// Full tiles whose cache policy the launch picks at run time (KDesc.cache) use buffer
+// instructions, whose cache-policy operand is an immediate of the instruction: the policy arms of
+// a switch then stay separate code paths. With ordinary loads and stores the arms differ only in a
+// non-temporal hint, which the optimizer treats as metadata: it merges the arms into one and drops
+// the hint. The resource spans one tile: raw access, stride 0, num_records = the tile's bytes,
+// word 3 = DATA_FORMAT 32 (untyped buffer access on gfx9-family targets).
+constexpr int kAuxNt = 2;  // cache-policy operand: bit 1 = nt on gfx940-family targets
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, (int)bytes, 0x00020000);
+}
+
+// A full CONTIG tile: kUnroll 16-byte loads a lane in flight, then the stores.
+template <bool kNtLoad, bool kNtStore>
+__device__ __forceinline__ void contig_tile(char* dst, const char* src, uint32_t tid) {
+  const __amdgpu_buffer_rsrc_t s = tile_rsrc(src, kTileBytes), t = tile_rsrc(dst, kTileBytes);
+  mo_u32x4 v[kUnroll];
+#pragma unroll
+  for (int k = 0; k < kUnroll; ++k)
+    v[k] = __builtin_amdgcn_raw_buffer_load_b128(s, (uint32_t)(k * kThreads + tid) * 16, 0, kNtLoad ? kAuxNt : 0);
+#pragma unroll
+  for (int k = 0; k < kUnroll; ++k)
+    __builtin_amdgcn_raw_buffer_store_b128(v[k], t, (uint32_t)(k * kThreads + tid) * 16, 0, kNtStore ? kAuxNt : 0);
+}
+
+// A full NARROW unpack tile: 8 contiguous payload bytes (4 bfloat16 values) <-> 16 contiguous
+// float32 tensor bytes a lane and round, so each instruction covers one span.
+template <bool kNtLoad, bool kNtStore>
+__device__ __forceinline__ void widen_tile(char* tensor32, const char* payload, uint32_t tid) {
+  constexpr int kRounds = 2 * kUnroll;
+  const __amdgpu_buffer_rsrc_t p = tile_rsrc(payload, kTileBytes), t = tile_rsrc(tensor32, 2 * kTileBytes);
+  mo_u32x2 v[kRounds];
+#pragma unroll
+  for (int k = 0; k < kRounds; ++k)
+    v[k] = __builtin_amdgcn_raw_buffer_load_b64(p, (uint32_t)(k * kThreads + tid) * 8, 0, kNtLoad ? kAuxNt : 0);
+#pragma unroll
+  for (int k = 0; k < kRounds; ++k)
+    __builtin_amdgcn_raw_buffer_store_b128(mo_u32x4{v[k].x << 16, v[k].x & 0xffff0000u, v[k].y << 16, v[k].y & 0xffff0000u},
+                                           t, (uint32_t)(k * kThreads + tid) * 16, 0, kNtStore ? kAuxNt : 0);
+}
+
 // Payload-side store: streaming when packing (the payload is the staging buffer).
 template <bool kPack>
 __device__ __forceinline__ void st16_out(char* p, uint4 v) {
@@ -151,10 +192,15 @@ __device__ __forceinline__ void narrow_chunk(char* payload16, char* tensor32) {
   }
 }
 
-// One 16 KiB tile (`tile`, numbered within the launch) of piece `d`.
 template <bool kPack>
+__device__ __forceinline__ void copy_tile_elem(const KDesc& d, uint64_t tile_off, uint32_t tile_bytes, char* payload,
+                                               char* tensor, uint32_t eb, uint32_t tid);
+
+// One 16 KiB tile (`tile`, numbered within the launch) of piece `d`. kElem: the launch may hold
+// ELEM pieces, whose LDS staging buffer every workgroup of the launch then reserves; launches
+// without them use the instantiation that reserves no LDS.
+template <bool kPack, bool kElem>
 __device__ __forceinline__ void copy_tile(const KDesc& d, uint32_t tile) {
-  __shared__ uint4 lds[kTileBytes / 16];
   const uint32_t tid = threadIdx.x;
   const uint64_t tile_off = (uint64_t)(tile - d.tile0) * kTileBytes;  // bytes into the piece
   const uint64_t left = d.nbytes - tile_off;
@@ -168,11 +214,12 @@ __device__ __forceinline__ void copy_tile(const KDesc& d, uint32_t tile) {
     const char* src = kPack ? t : payload;
     char* dst = kPack ? payload : t;
     if (tile_bytes == kTileBytes) {
-      uint4 v[kUnroll];
-#pragma unroll
-      for (int k = 0; k < kUnroll; ++k) v[k] = ld16(src + (size_t)(k * kThreads + tid) * 16);
-#pragma unroll
-      for (int k = 0; k < kUnroll; ++k) st16_out<kPack>(dst + (size_t)(k * kThreads + tid) * 16, v[k]);
+      switch (d.cache & (kCacheNtLoad | kCacheNtStore)) {
+        case 0: contig_tile<false, false>(dst, src, tid); break;
+        case kCacheNtLoad: contig_tile<true, false>(dst, src, tid); break;
+        case kCacheNtStore: contig_tile<false, true>(dst, src, tid); break;
+        default: contig_tile<true, true>(dst, src, tid); break;
+      }
     } else {
       const uint32_t nvec = tile_bytes / 16;
       for (uint32_t c = tid; c < nvec; c += kThreads) st16_out<kPack>(dst + (size_t)c * 16, ld16(src + (size_t)c * 16));
@@ -184,11 +231,9 @@ __device__ __forceinline__ void copy_tile(const KDesc& d, uint32_t tile) {
   if (d.path == kPathNarrow) {
     // payload offsets count bfloat16 bits; the float32 tensor side is twice as far in. A full
     // tile, measured both ways on the block microbench: pack keeps 16-byte streaming stores (a
-    // lane reads the 32 tensor bytes of one payload chunk); unpack moves 8 contiguous payload
-    // bytes <-> 16 contiguous tensor bytes a lane, so each instruction covers one span.
+    // lane reads the 32 tensor bytes of one payload chunk); unpack is widen_tile.
     char* const t = tensor + 2 * (d.first + tile_off);
     if (tile_bytes == kTileBytes) {
-      constexpr int kRounds = 2 * kUnroll;
       if (kPack) {
         uint4 a[kUnroll], b[kUnroll];
 #pragma unroll
@@ -199,13 +244,12 @@ __device__ __forceinline__ void copy_tile(const KDesc& d, uint32_t tile) {
 #pragma unroll
         for (int k = 0; k < kUnroll; ++k) st16_stream(payload + (size_t)(k * kThreads + tid) * 16, high_halves(a[k], b[k]));
       } else {
-        mo_u32x2 v[kRounds];
-#pragma unroll
-        for (int k = 0; k < kRounds; ++k) v[k] = *(const MO_GLOBAL mo_u32x2*)(payload + (size_t)(k * kThreads + tid) * 8);
-#pragma unroll
-        for (int k = 0; k < kRounds; ++k)
-          st16(t + (size_t)(k * kThreads + tid) * 16,
-               make_uint4(v[k].x << 16, v[k].x & 0xffff0000u, v[k].y << 16, v[k].y & 0xffff0000u));
+        switch (d.cache & (kCacheNtLoad | kCacheNtStore)) {
+          case 0: widen_tile<false, false>(t, payload, tid); break;
+          case kCacheNtLoad: widen_tile<true, false>(t, payload, tid); break;
+          case kCacheNtStore: widen_tile<false, true>(t, payload, tid); break;
+          default: widen_tile<true, true>(t, payload, tid); break;
+        }
       }
     } else {
       const uint32_t nvec = tile_bytes / 16;
@@ -245,7 +289,14 @@ __device__ __forceinline__ void copy_tile(const KDesc& d, uint32_t tile) {
     return;
   }
 
-  // ELEM: LDS-staged element gather / scatter.
+  if constexpr (kElem) copy_tile_elem<kPack>(d, tile_off, tile_bytes, payload, tensor, eb, tid);
+}
+
+// ELEM: LDS-staged element gather / scatter of one tile.
+template <bool kPack>
+__device__ __forceinline__ void copy_tile_elem(const KDesc& d, uint64_t tile_off, uint32_t tile_bytes, char* payload,
+                                               char* tensor, uint32_t eb, uint32_t tid) {
+  __shared__ uint4 lds[kTileBytes / 16];
   char* const sbuf = (char*)lds;
   const uint32_t nelem = tile_bytes / eb;
   const uint32_t e0 = (uint32_t)d.first + (uint32_t)(tile_off / eb);
@@ -267,34 +318,51 @@ __device__ __forceinline__ void copy_tile(const KDesc& d, uint32_t tile) {
 
 // Several pieces: the workgroup's piece is the last one starting at or before its tile. The
 // starts are one contiguous array (unused entries UINT32_MAX), compared without branches.
-template <bool kPack>
+template <bool kPack, bool kElem>
 __device__ __forceinline__ void copy_body(const LaunchArgs& args) {
   const uint32_t tile = blockIdx.x;
   uint32_t i = 0;
 #pragma unroll
   for (int k = 1; k < kMaxDesc; ++k) i += args.tile0[k] <= tile ? 1u : 0u;
-  copy_tile<kPack>(args.d[i], tile);
+  copy_tile<kPack, kElem>(args.d[i], tile);
 }
 
 }  // namespace mo
 
 extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_pack_kernel(const mo::LaunchArgs args) {
-  mo::copy_body<true>(args);
+  mo::copy_body<true, false>(args);
 }
 
 extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_unpack_kernel(const mo::LaunchArgs args) {
-  mo::copy_body<false>(args);
+  mo::copy_body<false, false>(args);
+}
+
+// The same with ELEM pieces in the launch (16 KiB of LDS a workgroup).
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_pack_elem_kernel(const mo::LaunchArgs args) {
+  mo::copy_body<true, true>(args);
+}
+
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_unpack_elem_kernel(const mo::LaunchArgs args) {
+  mo::copy_body<false, true>(args);
 }
 
 // One piece (tile0 == 0): the same work with a single descriptor as the kernel argument, which
 // cuts the argument block a launch carries from sizeof(LaunchArgs) to sizeof(KDesc). Most
 // launches move one saved tensor.
 extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_pack1_kernel(const mo::KDesc d) {
-  mo::copy_tile<true>(d, blockIdx.x);
+  mo::copy_tile<true, false>(d, blockIdx.x);
 }
 
 extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_unpack1_kernel(const mo::KDesc d) {
-  mo::copy_tile<false>(d, blockIdx.x);
+  mo::copy_tile<false, false>(d, blockIdx.x);
+}
+
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_pack1_elem_kernel(const mo::KDesc d) {
+  mo::copy_tile<true, true>(d, blockIdx.x);
+}
+
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_unpack1_elem_kernel(const mo::KDesc d) {
+  mo::copy_tile<false, true>(d, blockIdx.x);
 }
 
 // Byte equality of two ranges (both 16-byte aligned), one 16 KiB tile per workgroup. Lanes

@@ -48,6 +48,7 @@ class Launcher {
   uint64_t bytes_ = 0;          // all bytes added
   uint64_t pending_bytes_ = 0;  // bytes of the batch not launched yet
   uint64_t pending_hbm_ = 0;    // device-memory bytes the batch reads and writes
+  bool has_elem_ = false;       // the pending batch holds an ELEM piece (LDS-staged kernel)
 };
 
 int launch_link_copy(void* dst, const void* src, uint64_t bytes, uint32_t blocks, hipStream_t stream);

@@ -24,6 +24,11 @@ constexpr uint64_t kNoAllocScratchBytes = 64ull << 20;
 // payload; `first` and `nbytes` count payload bytes, the tensor side is twice that.
 enum : uint8_t { kPathContig = 0, kPathRuns = 1, kPathElem = 2, kPathNarrow = 3 };
 
+// Cache policy of a piece (KDesc::cache): non-temporal loads of the side read (the tensor when
+// packing, the payload when unpacking) and non-temporal stores of the side written. Streaming
+// accesses do not allocate in the GPU caches, which suits bytes that are read or written once.
+enum : uint8_t { kCacheNtLoad = 1, kCacheNtStore = 2 };
+
 struct KFastDiv {
   uint32_t d, m, s;
 };
@@ -39,7 +44,7 @@ struct KDesc {
   uint8_t path;
   uint8_t eb;
   uint8_t nouter;
-  uint8_t pad;
+  uint8_t cache;          // kCache* bits for the CONTIG and NARROW paths
   KFastDiv inner;               // units per innermost run
   KFastDiv outer[kMaxOuter];    // sizes of the outer dims, innermost first
   uint64_t ostride[kMaxOuter];  // byte strides of the outer dims

@@ -35,6 +35,8 @@ struct DeviceModule {
   hipModule_t module = nullptr;
   hipFunction_t pack = nullptr, unpack = nullptr, link = nullptr;
   hipFunction_t pack1 = nullptr, unpack1 = nullptr;  // single-piece launches
+  // the same four with ELEM pieces in the launch (they reserve the LDS staging buffer)
+  hipFunction_t pack_elem = nullptr, unpack_elem = nullptr, pack1_elem = nullptr, unpack1_elem = nullptr;
   hipFunction_t equal = nullptr;
   // this device's copy of mo_noalloc_scratch (every device holds its own, at its own address)
   uint64_t scratch = 0, scratch_bytes = 0;
@@ -51,6 +53,10 @@ int load_functions(DeviceModule& m) {
   if ((e = hipModuleGetFunction(&m.link, m.module, "mo_link_copy_kernel")) != hipSuccess) return (int)e;
   if ((e = hipModuleGetFunction(&m.pack1, m.module, "mo_pack1_kernel")) != hipSuccess) return (int)e;
   if ((e = hipModuleGetFunction(&m.unpack1, m.module, "mo_unpack1_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.pack_elem, m.module, "mo_pack_elem_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.unpack_elem, m.module, "mo_unpack_elem_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.pack1_elem, m.module, "mo_pack1_elem_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.unpack1_elem, m.module, "mo_unpack1_elem_kernel")) != hipSuccess) return (int)e;
   if ((e = hipModuleGetFunction(&m.equal, m.module, "mo_equal_kernel")) != hipSuccess) return (int)e;
   // Set-up of the allocation-free entry point, once per device with that device current: the
   // device address of this module's scratch array. From here on only this address is used.
@@ -211,6 +217,7 @@ void Launcher::add(const KDesc& kd) {
   bytes_ += kd.nbytes;
   pending_bytes_ += kd.nbytes;
   pending_hbm_ += kd.nbytes * (kd.path == kPathNarrow ? 3 : 2);  // narrow: 2 B tensor-side per payload B
+  has_elem_ = has_elem_ || kd.path == kPathElem;
   args_.ndesc++;
   if (tiles_ > kMaxTilesPerLaunch) flush();
 }
@@ -222,7 +229,8 @@ int Launcher::flush() {
   if (status_ == 0) {
     DeviceModule m;
     status_ = module_of_device(&m);
-    fn = single ? (pack_ ? m.pack1 : m.unpack1) : (pack_ ? m.pack : m.unpack);
+    if (has_elem_) fn = single ? (pack_ ? m.pack1_elem : m.unpack1_elem) : (pack_ ? m.pack_elem : m.unpack_elem);
+    else fn = single ? (pack_ ? m.pack1 : m.unpack1) : (pack_ ? m.pack : m.unpack);
   }
   hipEvent_t t0 = nullptr, t1 = nullptr;
   if (status_ == 0 && timer_) status_ = timer_->events(&t0, &t1);
@@ -242,6 +250,7 @@ int Launcher::flush() {
   tiles_ = 0;
   pending_bytes_ = 0;
   pending_hbm_ = 0;
+  has_elem_ = false;
   return status_;
 }
 

@@ -29,6 +29,9 @@ MO_FLAG_KERNEL_TIMING = 0x4
 MO_FLAG_NO_STAGED_RESTORE = 0x8
 MO_FLAG_EAGER_PACK = 0x10
 MO_FLAG_HIP_DMA = 0x20
+MO_FLAG_PACK_NT_LOAD = 0x40
+MO_FLAG_UNPACK_CACHED_LOAD = 0x80
+MO_FLAG_UNPACK_CACHED_STORE = 0x100
 MO_TENSOR_BF16_HIGH = 0x1
 
 NO_GROUP = (1 << 64) - 1

@@ -46,6 +46,11 @@ class EngineConfig:
     # DMA copies on dedicated HIP streams ordered by hipStreamWaitEvent only (an unpack never
     # blocks the host). kernel_copy=True overrides both with the copy-kernel comparison.
     link: str = "sdma"
+    # Cache policy of the kernels (measured choices are the defaults): non-temporal loads of the
+    # saved tensors in pack, of the payload in unpack, and streaming stores of restored tensors.
+    pack_nt_load: bool = False
+    unpack_nt_load: bool = True
+    unpack_nt_store: bool = True
     copy_kernel_blocks: int = 16
     d2h_engine: int = 0
     h2d_engine: int = 0
@@ -90,6 +95,9 @@ class EngineConfig:
             | (0 if self.staged_restore else _native.MO_FLAG_NO_STAGED_RESTORE)
             | (0 if self.batch_packs else _native.MO_FLAG_EAGER_PACK)
             | (_native.MO_FLAG_HIP_DMA if self.link == "hipdma" else 0)
+            | (_native.MO_FLAG_PACK_NT_LOAD if self.pack_nt_load else 0)
+            | (0 if self.unpack_nt_load else _native.MO_FLAG_UNPACK_CACHED_LOAD)
+            | (0 if self.unpack_nt_store else _native.MO_FLAG_UNPACK_CACHED_STORE)
         )
         if self.link not in ("sdma", "hipdma"):
             raise ValueError(f"link must be 'sdma' or 'hipdma', got {self.link!r}")

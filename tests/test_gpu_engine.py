@@ -314,13 +314,18 @@ def test_save_modified_in_place_before_its_gather(batch) -> None:
     engine.close()
 
 
-def test_narrowed_float32_pieces_across_slots() -> None:
+@pytest.mark.parametrize("pack_nt_load", [False, True])
+@pytest.mark.parametrize("unpack_nt_load", [False, True])
+@pytest.mark.parametrize("unpack_nt_store", [False, True])
+def test_narrowed_float32_pieces_across_slots(pack_nt_load, unpack_nt_load, unpack_nt_store) -> None:
     """bf16-exact float32 tensors packed narrowed (MO_TENSOR_BF16_HIGH), larger than a 2 MiB
     slot so that their pieces split across slots (the tensor side of a later piece starts at
-    twice its payload offset), between plain tensors; every restore is bitwise."""
+    twice its payload offset), between plain tensors; every restore is bitwise. Run under every
+    cache policy of the kernels: each policy is its own code path of the full CONTIG and NARROW
+    tiles."""
 
     device = torch.device("cuda", 0)
-    engine = _engine()
+    engine = _engine(pack_nt_load=pack_nt_load, unpack_nt_load=unpack_nt_load, unpack_nt_store=unpack_nt_store)
     stream = torch.cuda.current_stream(device).cuda_stream
     g = torch.Generator(device="cpu").manual_seed(21)
     handles, expected_bytes = [], 0
