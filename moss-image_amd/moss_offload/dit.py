@@ -174,16 +174,31 @@ def _condition_for_tokens(condition, sample_indices):
     return condition.index_select(0, sample_indices).unsqueeze(0)
 
 
-class Block(nn.Module):
-    """Joint image/text block with shared scale-shift-gate modulation (reference model.py:245-314)."""
+MLP_VARIANTS = ("situ", "gelu")
 
-    def __init__(self, dim: int, ffn_dim: int, heads: int) -> None:
+
+class Block(nn.Module):
+    """Joint image/text block with shared scale-shift-gate modulation (reference model.py:245-314).
+
+    ``mlp="situ"`` is the reference block: a fused up/gate projection into SiTU-GLU (:255, :312).
+    ``mlp="gelu"`` is the plain GELU MLP (tanh approximation) that BASELINE config 1 names in
+    words: ``ffn_up`` [dim -> ffn], GELU, ``ffn_down``. The reference has no such block; it is a
+    second producer of saves for the op-agnostic hooks (one bf16/fp32 ``[T, F]`` pre-activation
+    per block instead of SiTU's six intermediates).
+    """
+
+    def __init__(self, dim: int, ffn_dim: int, heads: int, mlp: str = "situ") -> None:
         super().__init__()
-        self.heads = heads
+        if mlp not in MLP_VARIANTS:
+            raise ValueError(f"mlp must be one of {MLP_VARIANTS}")
+        self.heads, self.mlp = heads, mlp
         self.norm1, self.norm2 = RMSNorm(dim), RMSNorm(dim)
         self.q_norm, self.k_norm = RMSNorm(dim // heads), RMSNorm(dim // heads)
         self.proj = nn.ModuleDict({name: nn.Linear(dim, dim, bias=False) for name in ("q", "k", "v", "o")})
-        self.proj["ffn_up_gate"] = nn.Linear(dim, 2 * ffn_dim, bias=False)
+        if mlp == "gelu":
+            self.proj["ffn_up"] = nn.Linear(dim, ffn_dim, bias=False)
+        else:
+            self.proj["ffn_up_gate"] = nn.Linear(dim, 2 * ffn_dim, bias=False)
         self.proj["ffn_down"] = nn.Linear(ffn_dim, dim, bias=False)
 
     def forward(self, tokens, rope, modulation, cu_seqlens=None):
@@ -201,8 +216,12 @@ class Block(nn.Module):
         hidden = self.norm2(tokens)
         hidden = hidden * (1 + _condition_for_tokens(scale_ffn, index))
         hidden = hidden + _condition_for_tokens(shift_ffn, index)
-        up, gate = self.proj["ffn_up_gate"](hidden.to(weight_dtype)).chunk(2, -1)
-        return tokens + self.proj["ffn_down"](situ(up, gate)) * _condition_for_tokens(gate_ffn, index)
+        if self.mlp == "gelu":
+            activated = F.gelu(self.proj["ffn_up"](hidden.to(weight_dtype)), approximate="tanh")
+        else:
+            up, gate = self.proj["ffn_up_gate"](hidden.to(weight_dtype)).chunk(2, -1)
+            activated = situ(up, gate)
+        return tokens + self.proj["ffn_down"](activated) * _condition_for_tokens(gate_ffn, index)
 
 
 class RoPE(nn.Module):
@@ -255,6 +274,7 @@ class MOSSImageTransformer(nn.Module):
         gradient_checkpointing: bool = False,
         checkpoint_fraction: float = 1.0,
         activation_offload: bool = False,
+        mlp: str = "situ",
     ) -> None:
         super().__init__()
         if dim % num_heads or (dim // num_heads) % 8 or freq_dim % 2:
@@ -271,7 +291,7 @@ class MOSSImageTransformer(nn.Module):
         self.rope = RoPE(dim // num_heads, rope_base)
         self.time_embedding = nn.Sequential(nn.Linear(freq_dim, dim), nn.SiLU(), nn.Linear(dim, dim))
         self.shared_block_modulation = nn.Linear(dim, 6 * dim)
-        self.layers = nn.ModuleList([Block(dim, ffn_dim, num_heads) for _ in range(num_layers)])
+        self.layers = nn.ModuleList([Block(dim, ffn_dim, num_heads, mlp) for _ in range(num_layers)])
         self.final_norm_video = RMSNorm(dim)
         self.final_linear_video = nn.Linear(dim, latent_channels, bias=False)
         self.video_head_modulation = nn.Linear(dim, 2 * dim)

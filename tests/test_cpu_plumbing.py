@@ -5,7 +5,8 @@
   the native library. ``test_activation_offload_is_cpu_noop`` restates the reference's own test
   (training/tests/test_packed_features.py:188-198, seed 33, same tiny model sizes).
 - BASELINE config 1 on the CPU: one reference-topology block (hidden 512, 8x64 heads, MLP 2048,
-  fp32, 16x16 image + 64 text tokens) through the oracle's emulation of the reference hooks
+  fp32, 16x16 image + 64 text tokens), with the reference's SiTU-GLU MLP and with the GELU MLP
+  that BASELINE names, through the oracle's emulation of the reference hooks
   with CPU payloads. Every restored tensor is bitwise equal to its save, and the loss and
   every gradient are bitwise equal to the run without hooks. The manifest probe records the
   same offloaded set the hooks packed.
@@ -25,6 +26,7 @@ import weakref
 import gc
 from contextlib import nullcontext
 
+import pytest
 import torch
 
 import moss_offload
@@ -68,10 +70,10 @@ def test_gate_returns_nullcontext_without_touching_the_engine() -> None:
     assert not engine._ENGINES
 
 
-def _config1():
+def _config1(mlp="situ"):
     torch.manual_seed(0)
     model = dit.MOSSImageTransformer(
-        dim=512, ffn_dim=2048, num_heads=8, num_layers=1, text_dim=64, freq_dim=32, latent_channels=16,
+        dim=512, ffn_dim=2048, num_heads=8, num_layers=1, text_dim=64, freq_dim=32, latent_channels=16, mlp=mlp,
     )
     dit.init_weights(model)
     dit.inject_lora(model, rank=8, alpha=8.0, b_std=0.03)
@@ -91,8 +93,11 @@ def _step(model, latent, context, hooks):
     return out.detach(), loss.detach(), grads
 
 
-def test_config1_block_through_emulated_reference_hooks_is_bitwise_identity() -> None:
-    model, latent, context = _config1()
+@pytest.mark.parametrize("mlp", dit.MLP_VARIANTS)
+def test_config1_block_through_emulated_reference_hooks_is_bitwise_identity(mlp) -> None:
+    """Config 1 with the reference's SiTU-GLU block and with the GELU MLP BASELINE names."""
+
+    model, latent, context = _config1(mlp)
     expected = _step(copy.deepcopy(model), latent, context, nullcontext())
     recorder = reference_hooks.Recorder()
     hooked = copy.deepcopy(model)

@@ -127,13 +127,15 @@ def test_fp32_step_matches_no_offload_and_reference_hooks(checkpointing, lora) -
     _compare(actual, reference, rtol=5e-5, atol=5e-6)
 
 
-def test_config1_block_fp32_restores_bit_exact() -> None:
-    """BASELINE config 1 on the GPU: hidden 512, 8x64 heads, MLP 2048, 256 image + 64 text."""
+@pytest.mark.parametrize("mlp", dit.MLP_VARIANTS)
+def test_config1_block_fp32_restores_bit_exact(mlp) -> None:
+    """BASELINE config 1 on the GPU: hidden 512, 8x64 heads, MLP 2048 (the reference's SiTU-GLU,
+    and the GELU MLP BASELINE names), 256 image + 64 text."""
 
     device = torch.device("cuda", 0)
     torch.manual_seed(0)
     model = dit.MOSSImageTransformer(
-        dim=512, ffn_dim=2048, num_heads=8, num_layers=1, text_dim=64, freq_dim=32, latent_channels=16,
+        dim=512, ffn_dim=2048, num_heads=8, num_layers=1, text_dim=64, freq_dim=32, latent_channels=16, mlp=mlp,
     )
     dit.init_weights(model)
     model = model.to(device).train()
