@@ -17,6 +17,10 @@ sees each block's inputs. Regime B: no checkpointing, so the hook sees every act
 Prints ONE JSON line (stdout). Progress goes to stderr.
 
 Leg Q: the config-5 int8 weight-only GEMMs on the HIP MFMA kernels against the eager path.
+Leg BR: regime B on the first 16 blocks, where the reference hooks' pinned copies fit the host.
+Leg AH: regime A with 100 ms of host work after every step, on both host-link transports (the
+SDMA link's unpack waits on the host for its H2D; the HIP-stream link's never does).
+Parity: loss and LoRA gradients against hooks off in regimes A, B and B at 16 blocks.
 
   python bench.py [--steps K] [--warmup W] [--regimes M,Q,A,B] [--micro-iters N]
 """
@@ -261,16 +265,67 @@ def loss_and_backward(model, inputs, forward=config3_forward):
     return loss.detach()
 
 
+_SECOND_ENGINES: dict = {}
+
+
+def hipdma_offload_context(model, enabled, device):
+    """The engine's hooks on a second engine that moves its copies on HIP streams (link
+    "hipdma": ordered by hipStreamWaitEvent, so an unpack never blocks the host)."""
+
+    import torch
+    import moss_offload
+    from moss_offload.activation_offload import _ActivationOffload
+
+    if not enabled or device.type != "cuda" or not torch.is_grad_enabled():
+        return moss_offload.activation_cpu_offload(model, enabled, device)
+    return _ActivationOffload(model, device, engine=hipdma_engine(device))
+
+
+def hipdma_engine(device):
+    import dataclasses
+
+    from moss_offload.engine import OffloadEngine, get_engine
+
+    engine = _SECOND_ENGINES.get("hipdma")
+    if engine is None:
+        engine = OffloadEngine(device, dataclasses.replace(get_engine(device).config, link="hipdma"))
+        _SECOND_ENGINES["hipdma"] = engine
+    return engine
+
+
 def configure_mode(model, mode: str, regime: str):
     import moss_offload
 
     model.gradient_checkpointing = regime == "A"
     model.checkpoint_fraction = 1.0
     model.activation_offload = mode != "none"
-    model.offload_context = reference_offload_context if mode == "reference" else moss_offload.activation_cpu_offload
+    model.offload_context = {"reference": reference_offload_context,
+                             "engine_hipdma": hipdma_offload_context}.get(mode, moss_offload.activation_cpu_offload)
 
 
-def time_steps(model, opt, inputs, steps: int, warmup: int, label: str, forward=config3_forward):
+def mode_engine(device, mode: str):
+    """The engine a mode's hooks use (None for modes without one)."""
+
+    from moss_offload.engine import get_engine
+
+    if mode == "engine":
+        return get_engine(device)
+    if mode == "engine_hipdma":
+        return hipdma_engine(device)
+    return None
+
+
+def host_work(seconds: float) -> None:
+    """Busy the calling thread for ``seconds``: a trainer's per-step host work (data loading,
+    logging), which overlaps the GPU only if the host thread is ahead of it."""
+
+    end = time.perf_counter() + seconds
+    while time.perf_counter() < end:
+        pass
+
+
+def time_steps(model, opt, inputs, steps: int, warmup: int, label: str, forward=config3_forward,
+               host_work_s: float = 0.0):
     import torch
 
     for i in range(warmup):
@@ -278,6 +333,7 @@ def time_steps(model, opt, inputs, steps: int, warmup: int, label: str, forward=
         opt.zero_grad(set_to_none=True)
         loss_and_backward(model, inputs, forward)
         opt.step()
+        host_work(host_work_s)
         torch.cuda.synchronize()
         log(f"{label}: warmup {i + 1}/{warmup} {time.perf_counter() - t0:.3f} s")
     torch.cuda.synchronize()
@@ -288,6 +344,7 @@ def time_steps(model, opt, inputs, steps: int, warmup: int, label: str, forward=
         opt.zero_grad(set_to_none=True)
         loss_and_backward(model, inputs, forward)
         opt.step()
+        host_work(host_work_s)
     torch.cuda.synchronize()
     elapsed = (time.perf_counter() - start) / steps
     peak = torch.cuda.max_memory_allocated()
@@ -295,27 +352,55 @@ def time_steps(model, opt, inputs, steps: int, warmup: int, label: str, forward=
     return elapsed, peak
 
 
-def parity(model, inputs):
-    """Loss and adapter gradients of one step per mode from the same state (no optimizer)."""
-
+def _mode_step(model, inputs, mode: str, regime: str):
     import torch
 
-    results = {}
-    for mode in ("none", "engine", "reference"):
-        configure_mode(model, mode, "A")
-        model.zero_grad(set_to_none=True)
-        loss = loss_and_backward(model, inputs)
-        grads = [p.grad.detach().float().clone() for p in model.parameters() if p.grad is not None]
-        results[mode] = (loss.float(), grads)
+    configure_mode(model, mode, regime)
     model.zero_grad(set_to_none=True)
+    loss = loss_and_backward(model, inputs)
+    grads = [p.grad.detach().float().clone() for p in model.parameters() if p.grad is not None]
+    model.zero_grad(set_to_none=True)
+    if mode == "reference":
+        torch.cuda.synchronize()
+        torch._C._host_emptyCache()
+    return loss.float(), grads
+
+
+def _compare_to_none(results: dict) -> dict:
+    import torch
+
     base_loss, base_grads = results["none"]
     out = {}
-    for mode in ("engine", "reference"):
-        loss, grads = results[mode]
-        rel_loss = abs((loss - base_loss) / base_loss).item()
+    for mode, (loss, grads) in results.items():
+        if mode == "none":
+            continue
         num = sum(float((g - b).norm() ** 2) for g, b in zip(grads, base_grads)) ** 0.5
         den = sum(float(b.norm() ** 2) for b in base_grads) ** 0.5
-        out[mode] = {"loss_rel": rel_loss, "grad_rel": num / den, "loss_bitwise": bool(torch.equal(loss, base_loss))}
+        worst = max(float((g - b).norm() / b.norm().clamp_min(1e-30)) for g, b in zip(grads, base_grads))
+        out[mode] = {"loss_rel": abs((loss - base_loss) / base_loss).item(), "grad_rel": num / den,
+                     "worst_tensor_grad_rel": worst, "loss_bitwise": bool(torch.equal(loss, base_loss)),
+                     "grads_bitwise": all(torch.equal(g, b) for g, b in zip(grads, base_grads)),
+                     "lora_tensors": len(grads)}
+    return out
+
+
+def parity(model, inputs, ref_layers: int):
+    """Loss and adapter gradients of one step per mode from the same state (no optimizer step),
+    against hooks off: regime A (engine and reference hooks, 40 blocks), regime B (engine; the
+    reference's per-save pinned copies exceed the host's pinned-memory cap at 40 blocks), and
+    regime B at ``ref_layers`` blocks, where the reference hooks fit (engine and reference)."""
+
+    from torch import nn
+
+    out = {"A": _compare_to_none({m: _mode_step(model, inputs, m, "A") for m in ("none", "engine", "reference")}),
+           "B": _compare_to_none({m: _mode_step(model, inputs, m, "B") for m in ("none", "engine")})}
+    layers = model.layers
+    model.layers = nn.ModuleList(list(layers)[:ref_layers])
+    try:
+        out[f"B{ref_layers}"] = _compare_to_none(
+            {m: _mode_step(model, inputs, m, "B") for m in ("none", "engine", "reference")})
+    finally:
+        model.layers = layers
     return out
 
 
@@ -487,8 +572,78 @@ def calibration_copy(device, stream: int, repeats: int = 3) -> None:
     del buf
 
 
+def kernel_context_leg(device, nbytes: int = 28 << 20, reps: int = 24):
+    """Leg K: one-piece gathers and scatters of a regime-A checkpoint input's size (28 MiB),
+    timed per dispatch with HIP events on the launch stream, back to back and right after other
+    work: a GEMM with a 128 MiB output (what precedes an unpack in a checkpointed backward), a
+    GEMM of the same power draw with a 128 KiB output, a 128 MiB fill and a 1 GiB read. Shows
+    how much of a copy's in-step duration the state the previous kernel leaves behind sets."""
+
+    import ctypes
+    import statistics
+
+    import torch
+    from moss_offload import _native
+
+    lib = _native.load()
+    stream = torch.cuda.current_stream(device)
+    pool = 6
+    src = [torch.full((nbytes,), i + 1, dtype=torch.uint8, device=device) for i in range(pool)]
+    dst = [torch.zeros(nbytes, dtype=torch.uint8, device=device) for _ in range(pool)]
+    a = torch.randn(8192, 8192, device=device, dtype=torch.bfloat16)
+    out_big = torch.empty(8192, 8192, device=device, dtype=torch.bfloat16)
+    k1 = torch.randn(256, 1 << 20, device=device, dtype=torch.bfloat16)
+    k2 = torch.randn(1 << 20, 256, device=device, dtype=torch.bfloat16)
+    out_small = torch.empty(256, 256, device=device, dtype=torch.bfloat16)
+    fill_buf = torch.empty(128 << 20, dtype=torch.uint8, device=device)
+    read_buf = torch.randn(256 << 20, device=device)
+    sink = torch.empty((), device=device)
+    zero = (ctypes.c_uint64 * 1)(0)
+
+    def described(t):
+        arr = (_native.MoTensor * 1)()
+        _native.describe(t, arr[0])
+        return arr
+
+    def gather(r):
+        _native.check("mo_gather", lib.mo_gather(described(src[(r + 3) % pool]), 1, dst[r % pool].data_ptr(), zero,
+                                                 stream.cuda_stream))
+
+    def scatter(r):
+        _native.check("mo_scatter", lib.mo_scatter(described(dst[r % pool]), 1, src[(r + 3) % pool].data_ptr(), zero,
+                                                   stream.cuda_stream))
+
+    before = {
+        "back_to_back": None,
+        "gemm_128MiB_output": lambda: torch.mm(a, a, out=out_big),
+        "gemm_128KiB_output": lambda: torch.mm(k1, k2, out=out_small),
+        "fill_128MiB": lambda: fill_buf.fill_(7),
+        "read_1GiB": lambda: torch.sum(read_buf, dim=0, out=sink),
+    }
+    out = {"bytes_per_dispatch": nbytes, "dispatches": reps}
+    for name, fn in before.items():
+        row = {}
+        for kind, op in (("gather", gather), ("scatter", scatter)):
+            times = []
+            for r in range(reps + 3):
+                if fn is not None:
+                    fn()
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                op(r)
+                end.record(stream)
+                times.append((start, end))
+            torch.cuda.synchronize()
+            us = statistics.median(s.elapsed_time(e) * 1e3 for s, e in times[3:])
+            row[kind] = {"median_us": round(us, 2), "tb_s": round(2 * nbytes / us / 1e6, 3)}
+        out[name] = row
+        log(f"kernel context {name}: gather {row['gather']['median_us']} us, scatter {row['scatter']['median_us']} us")
+    return out
+
+
 def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: int, restore_slots: int,
-          batch_packs: bool = True, d2h_engine: int = 0, h2d_engine: int = 0, narrow=None, link: str = "sdma"):
+          batch_packs: bool = True, d2h_engine: int = 0, h2d_engine: int = 0, narrow=None, link: str = "sdma",
+          cache: dict | None = None):
     """one regime-B block's saved set through pack -> D2H -> H2D -> unpack.
 
     Every iteration packs the block's tensors into one group (staging ring + SDMA D2H), commits
@@ -504,7 +659,7 @@ def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: 
     engine = OffloadEngine(device, EngineConfig(
         stage_slot_bytes=slot_mib << 20, stage_slots=stage_slots, restore_slots=restore_slots,
         timing=True, kernel_timing=True, staged_restore=False, prefetch=False, batch_packs=batch_packs,
-        d2h_engine=d2h_engine, h2d_engine=h2d_engine, link=link))
+        d2h_engine=d2h_engine, h2d_engine=h2d_engine, link=link, **(cache or {})))
     stream = torch.cuda.current_stream(device).cuda_stream
     payload = sum(t.numel() * t.element_size() for t in tensors)
     storages = {}
@@ -803,6 +958,9 @@ def run(args) -> dict:
         staged_restore=not args.no_staged_restore,
         kernel_copy=args.kernel_copy,
         link=args.link,
+        pack_nt_load=args.pack_nt_load,
+        unpack_nt_load=not args.unpack_cached_load,
+        unpack_nt_store=not args.unpack_cached_store,
         batch_packs=not args.eager_pack,
         d2h_engine=args.d2h_engine,
         h2d_engine=args.h2d_engine,
@@ -821,10 +979,13 @@ def run(args) -> dict:
 
     peaks = link_peaks(device)
     log(f"host link: {peaks}")
+    # 256 MiB device-to-device copies with the engine's copy kernel: under rocprofv3 --pmc they
+    # scale FETCH_SIZE / WRITE_SIZE to bytes for any leg of this run
+    calibration_copy(device, torch.cuda.current_stream(device).cuda_stream)
 
-    result = {"regimes": {}, "link": peaks}
+    result = {"regimes": {}, "link": peaks, "hook_features": moss_offload.hook_features()}
     if not args.no_parity:
-        result["parity"] = parity(model, inputs)
+        result["parity"] = parity(model, inputs, args.ref_layers)
         log(f"parity: {result['parity']}")
 
     if "M" in args.regimes:
@@ -839,7 +1000,9 @@ def run(args) -> dict:
         result["micro"] = micro(device, tensors, args.micro_iters, args.micro_warmup, args.slot_mib,
                                 args.stage_slots, args.restore_slots, batch_packs=not args.eager_pack,
                                 d2h_engine=args.d2h_engine, h2d_engine=args.h2d_engine, narrow=narrow,
-                                link=args.link)
+                                link=args.link,
+                                cache=dict(pack_nt_load=args.pack_nt_load, unpack_nt_load=not args.unpack_cached_load,
+                                           unpack_nt_store=not args.unpack_cached_store))
         result["micro"].update(narrowed_tensors=sum(narrow), link_bytes_per_iter=moved)
         m = result["micro"]
         log(f"micro: {m['s_per_iter'] * 1e3:.2f} ms/iter, D2H {m['d2h_gbps']:.1f} GB/s, H2D {m['h2d_gbps']:.1f} GB/s, "
@@ -847,6 +1010,9 @@ def run(args) -> dict:
             f"{m['unpack_hbm_gbps']:.0f} GB/s, bitwise {m['bitwise_first'] and m['bitwise_last']}")
         del tensors
 
+    if "K" in args.regimes:
+        result["kernel_context"] = kernel_context_leg(device)
+        torch.cuda.empty_cache()
     if "Q" in args.regimes:
         result["int8_gemm"] = int8_gemm_leg(device)
         torch.cuda.empty_cache()
@@ -863,6 +1029,13 @@ def run(args) -> dict:
 
         if name in ("A", "B"):
             return model, opt, inputs, config3_forward, name
+        if name == "AH":  # regime A with host work after every step (the transports' host blocking)
+            return model, opt, inputs, config3_forward, "A"
+        if name == "BR":  # regime B on the first --ref-layers blocks, where the reference hooks fit
+            layers = model.layers
+            model.layers = torch.nn.ModuleList(list(layers)[: args.ref_layers])
+            cleanups.append(lambda: setattr(model, "layers", layers))
+            return model, opt, inputs, config3_forward, "B"
         if name == "BK":  # regime B with the engine keeping the last --keep-last-blocks blocks resident
             return model, opt, inputs, config3_forward, "B"
         if name == "A4":
@@ -941,7 +1114,7 @@ def run(args) -> dict:
             return model_f, opt_f, inputs, config3_forward, "A"
         raise ValueError(f"unknown regime {name}")
 
-    for regime_name in (r for r in args.regimes if r not in ("M", "Q", "G")):
+    def run_leg(regime_name):
         wl_model, wl_opt, wl_inputs, forward, regime = workload(regime_name)
         manifest = record_manifest(wl_model, wl_inputs, regime, forward)
         payload_unique = manifest.payload_bytes(unique=True)
@@ -951,8 +1124,13 @@ def run(args) -> dict:
             f"unique ({payload_copied / 1e9:.2f} GB as the reference copies it)")
         steps = args.steps if regime_name == "A" else max(1, args.steps_b)
         warmup = args.warmup if regime_name == "A" else max(1, args.warmup_b)
+        host_work_s = args.host_work_ms / 1e3 if regime_name == "AH" else 0.0
         if regime_name == "BK":
             entry_extra = {"keep_last_blocks": args.keep_last_blocks}
+        elif regime_name == "AH":
+            entry_extra = {"host_work_ms_per_step": args.host_work_ms}
+        elif regime_name == "BR":
+            entry_extra = {"layers": len(wl_model.layers)}
         else:
             entry_extra = {}
         block = [r for r in manifest.block if not r.resident]
@@ -963,23 +1141,37 @@ def run(args) -> dict:
         if regime_name == "B":
             entry["cpu_sample"] = manifest
         streamer = getattr(wl_model, "block_swap_manager", None)
-        for mode in args.modes:
+        modes = list(args.modes)
+        if regime_name == "AH" and "engine" in modes:
+            modes.insert(modes.index("engine") + 1, "engine_hipdma")
+        for mode in modes:
             if regime_name == "BK" and mode == "reference":
                 continue  # the reference offloads every block
             configure_mode(wl_model, mode, regime)
-            engine = get_engine(device)
+            engine = mode_engine(device, mode) or get_engine(device)
             engine.config.keep_last_blocks = args.keep_last_blocks if regime_name == "BK" else 0
+            # marks the start of each leg and mode in a kernel trace, and scales rocprofv3
+            # FETCH_SIZE / WRITE_SIZE to bytes in a counter run
+            calibration_copy(device, torch.cuda.current_stream(device).cuda_stream)
             engine.reset_stats()
+            moss_offload.reset_hook_counters()
             if streamer is not None:
                 streamer.reset_stats()
+            failure = None
             try:
-                seconds, peak = time_steps(wl_model, wl_opt, wl_inputs, steps, warmup, f"{regime_name}/{mode}", forward)
+                seconds, peak = time_steps(wl_model, wl_opt, wl_inputs, steps, warmup, f"{regime_name}/{mode}", forward,
+                                           host_work_s)
             except RuntimeError as exc:  # e.g. the reference hooks exhausting pinned host memory
                 import traceback
 
                 log(f"{regime_name}/{mode} failed: {exc}\n{traceback.format_exc(limit=-4)}")
-                entry[mode] = {"error": str(exc).splitlines()[0]}
+                failure = str(exc).splitlines()[0]
+            if failure is not None:
+                # the traceback held the failed step's graph, and with it every pinned copy it
+                # made; they are freed now, and the cached pinned blocks go back to the host
+                entry[mode] = {"error": failure}
                 wl_opt.zero_grad(set_to_none=True)
+                gc.collect()
                 torch.cuda.synchronize()
                 torch._C._host_emptyCache()
                 continue
@@ -1000,10 +1192,12 @@ def run(args) -> dict:
                     "writeback_busy_s_per_step": ss["writeback_busy_ms"] / 1e3 / n,
                     "writeback_gbps": ss["timed_writeback_bytes"] / max(ss["writeback_busy_ms"], 1e-9) / 1e6,
                 }
-            if mode == "engine":
+            if mode in ("engine", "engine_hipdma"):
                 engine.synchronize()
                 st = engine.stats()
                 n = steps + warmup  # reset before warmup: stats cover warmup + timed steps
+                record["link"] = engine.link_name()
+                record["hook_counters_per_step"] = {k: v / n for k, v in moss_offload.hook_counters().items()}
                 # the staging and restore rings are the engine's own hipMalloc, outside torch's
                 # allocator and so outside peak_device_bytes
                 rings = (engine.config.stage_slots + engine.config.restore_slots) * engine.config.stage_slot_bytes
@@ -1025,6 +1219,10 @@ def run(args) -> dict:
                     pack_bytes_per_launch=st["timed_pack_bytes"] / max(st["timed_pack_launches"], 1),
                     pack_hbm_bytes_per_launch=st["timed_pack_hbm_bytes"] / max(st["timed_pack_launches"], 1),
                     unpack_bytes_per_launch=st["timed_unpack_bytes"] / max(st["timed_unpack_launches"], 1),
+                    pack_launches_per_step=st["timed_pack_launches"] / n,
+                    unpack_launches_per_step=st["timed_unpack_launches"] / n,
+                    pack_hbm_bytes_per_step=st["timed_pack_hbm_bytes"] / n,
+                    unpack_hbm_bytes_per_step=st["timed_unpack_hbm_bytes"] / n,
                     host_blocks=st["host_blocks"],
                     host_block_ms=st["host_block_ms"],
                     staged_hits=st["staged_hits"],
@@ -1038,16 +1236,25 @@ def run(args) -> dict:
                 torch._C._host_emptyCache()
             entry[mode] = record
         none = entry.get("none", {}).get("s_per_it")
-        eng = entry.get("engine")
-        if none is not None and eng is not None and "s_per_it" in eng:
-            copy_s = eng["d2h_s_per_step"] + eng["h2d_s_per_step"]
-            exposed = eng["s_per_it"] - none
-            eng["hidden_fraction"] = min(1.0, max(0.0, 1.0 - exposed / copy_s)) if copy_s > 0 else None
-            eng["exposed_s"] = exposed
+        for name in ("engine", "engine_hipdma"):
+            eng = entry.get(name)
+            if none is not None and eng is not None and "s_per_it" in eng:
+                copy_s = eng["d2h_s_per_step"] + eng["h2d_s_per_step"]
+                exposed = eng["s_per_it"] - none
+                eng["hidden_fraction"] = min(1.0, max(0.0, 1.0 - exposed / copy_s)) if copy_s > 0 else None
+                eng["exposed_s"] = exposed
         ref = entry.get("reference")
         if none is not None and ref is not None and "s_per_it" in ref:
             ref["exposed_s"] = ref["s_per_it"] - none
-        result["regimes"][regime_name] = entry
+        return entry
+
+    cleanups = []
+    for regime_name in (r for r in args.regimes if r not in ("M", "K", "Q", "G")):
+        try:
+            result["regimes"][regime_name] = run_leg(regime_name)
+        finally:
+            while cleanups:
+                cleanups.pop()()
     return result
 
 
@@ -1056,17 +1263,27 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=6)
     parser.add_argument("--warmup", type=int, default=2)
-    parser.add_argument("--steps-b", type=int, default=2)
-    parser.add_argument("--warmup-b", type=int, default=1)
-    parser.add_argument("--regimes", default="M,Q,A,B",
-                        help="M = config-2 block microbench, Q = config-5 int8 GEMMs (HIP vs eager), "
-                        "A/B = config-3 steps (checkpointed / not), BK = regime B keeping the last "
+    parser.add_argument("--steps-b", type=int, default=5, help="timed steps of the legs other than A")
+    parser.add_argument("--warmup-b", type=int, default=2)
+    parser.add_argument("--regimes", default="M,K,Q,A,B,BR,AH",
+                        help="M = config-2 block microbench, K = 28 MiB gathers/scatters back to back and after "
+                        "other kernels (a GEMM with a large output, a fill, a read), Q = config-5 int8 GEMMs "
+                        "(HIP vs eager), "
+                        "A/B = config-3 steps (checkpointed / not), BR = regime B on --ref-layers blocks (none, "
+                        "engine and the reference hooks, which fit the pinned-memory cap there), AH = regime A "
+                        "with --host-work-ms of host work per step (none, engine on SDMA, engine on HIP "
+                        "streams), BK = regime B keeping the last "
                         "--keep-last-blocks blocks' saves resident, G = host gradient accumulation "
                         "(full-parameter config-3 dims, 2 micro-batches: device / engine / reference stash), "
                         "A4 = config 4 (2048^2, regime A), C5U/C5P = config 5 unpacked / packed (regime A), "
                         "S5 = config 5 packed with every block streamed from pinned host masters, "
                         "F3/F3S = full-parameter training at config-3 dims, resident / every block on the trainable ring")
-    parser.add_argument("--micro-iters", type=int, default=200)
+    parser.add_argument("--micro-iters", type=int, default=1000)
+    parser.add_argument("--ref-layers", type=int, default=16,
+                        help="blocks of the BR leg and of regime B's reference parity: the reference hooks pin one "
+                             "tensor per save, and 40 blocks of regime B exceed the host's pinned-memory cap")
+    parser.add_argument("--host-work-ms", type=float, default=100.0,
+                        help="AH leg: host work after every step, which overlaps the GPU only when the host is ahead")
     parser.add_argument("--micro-warmup", type=int, default=3)
     parser.add_argument("--modes", default="none,engine,reference")
     parser.add_argument("--layers", type=int, default=CONFIG3["num_layers"])
@@ -1084,6 +1301,11 @@ def main() -> int:
     parser.add_argument("--eager-pack", action="store_true",
                         help="one gather launch per save instead of one per staging segment")
     parser.add_argument("--kernel-copy", action="store_true", help="copy kernel on HIP streams instead of SDMA")
+    parser.add_argument("--pack-nt-load", action="store_true", help="pack reads saves with non-temporal loads")
+    parser.add_argument("--unpack-cached-load", action="store_true",
+                        help="unpack reads payloads with ordinary loads instead of non-temporal ones")
+    parser.add_argument("--unpack-cached-store", action="store_true",
+                        help="unpack writes restored tensors with ordinary stores instead of streaming ones")
     parser.add_argument("--link", default="sdma", choices=("sdma", "hipdma"),
                         help="host-link transport: SDMA through HSA with host-side ordering, or the same DMA "
                              "copies on HIP streams ordered by hipStreamWaitEvent")

@@ -343,10 +343,11 @@ def _numel(shape) -> int:
 class _ActivationOffload:
     """The context returned for an enabled offload: hooks + block boundaries + dedupe."""
 
-    def __init__(self, model: nn.Module, device: torch.device) -> None:
+    def __init__(self, model: nn.Module, device: torch.device, engine: OffloadEngine | None = None) -> None:
         self.model = model
         self.device = device
-        self.engine: OffloadEngine = get_engine(device)
+        # the device's shared engine, unless a caller brings its own (a second transport, say)
+        self.engine: OffloadEngine = engine if engine is not None else get_engine(device)
         # Reference :95-99: storages of CUDA parameters and buffers stay resident.
         self.resident_storages = {
             _storage_key(tensor)
