@@ -726,6 +726,8 @@ def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: 
         "unpack_bytes_per_launch": st["timed_unpack_bytes"] / max(st["timed_unpack_launches"], 1),
         "pack_hbm_bytes_per_launch": st["timed_pack_hbm_bytes"] / max(st["timed_pack_launches"], 1),
         "pack_launches_per_iter": st["timed_pack_launches"] / iters,
+        "wire_segments": st["wire_segments"],
+        "wire_ratio": (st["wire_bytes"] / st["wire_raw_bytes"]) if st["wire_raw_bytes"] else None,
         "unpack_launches_per_iter": st["timed_unpack_launches"] / iters,
         "host_blocks_per_iter": st["host_blocks"] / iters,
         "host_block_ms_per_iter": st["host_block_ms"] / iters,
@@ -965,6 +967,7 @@ def run(args) -> dict:
         d2h_engine=args.d2h_engine,
         h2d_engine=args.h2d_engine,
         narrow_bf16_casts=not args.no_narrow,
+        wire_coding=args.wire_coding,
     )
     model = build_model(device, args.layers)
     inputs = make_inputs(device)
@@ -1001,7 +1004,8 @@ def run(args) -> dict:
                                 args.stage_slots, args.restore_slots, batch_packs=not args.eager_pack,
                                 d2h_engine=args.d2h_engine, h2d_engine=args.h2d_engine, narrow=narrow,
                                 link=args.link,
-                                cache=dict(pack_nt_load=args.pack_nt_load, unpack_nt_load=not args.unpack_cached_load,
+                                cache=dict(wire_coding=args.micro_wire_coding,
+                                           pack_nt_load=args.pack_nt_load, unpack_nt_load=not args.unpack_cached_load,
                                            unpack_nt_store=not args.unpack_cached_store))
         result["micro"].update(narrowed_tensors=sum(narrow), link_bytes_per_iter=moved)
         m = result["micro"]
@@ -1198,9 +1202,9 @@ def run(args) -> dict:
                 n = steps + warmup  # reset before warmup: stats cover warmup + timed steps
                 record["link"] = engine.link_name()
                 record["hook_counters_per_step"] = {k: v / n for k, v in moss_offload.hook_counters().items()}
-                # the staging and restore rings are the engine's own hipMalloc, outside torch's
-                # allocator and so outside peak_device_bytes
-                rings = (engine.config.stage_slots + engine.config.restore_slots) * engine.config.stage_slot_bytes
+                # the staging and restore rings (and their wire buffers once coding ran) are the
+                # engine's own hipMalloc, outside torch's allocator and so outside peak_device_bytes
+                rings = st["device_ring_bytes"]
                 record.update(
                     engine_ring_bytes=rings,
                     peak_device_bytes_with_rings=peak + rings,
@@ -1219,6 +1223,8 @@ def run(args) -> dict:
                     pack_bytes_per_launch=st["timed_pack_bytes"] / max(st["timed_pack_launches"], 1),
                     pack_hbm_bytes_per_launch=st["timed_pack_hbm_bytes"] / max(st["timed_pack_launches"], 1),
                     unpack_bytes_per_launch=st["timed_unpack_bytes"] / max(st["timed_unpack_launches"], 1),
+                    wire_segments_per_step=st["wire_segments"] / n,
+                    wire_ratio=(st["wire_bytes"] / st["wire_raw_bytes"]) if st["wire_raw_bytes"] else None,
                     pack_launches_per_step=st["timed_pack_launches"] / n,
                     unpack_launches_per_step=st["timed_unpack_launches"] / n,
                     pack_hbm_bytes_per_step=st["timed_pack_hbm_bytes"] / n,
@@ -1306,6 +1312,12 @@ def main() -> int:
                         help="unpack reads payloads with ordinary loads instead of non-temporal ones")
     parser.add_argument("--unpack-cached-store", action="store_true",
                         help="unpack writes restored tensors with ordinary stores instead of streaming ones")
+    parser.add_argument("--wire-coding", default="auto", choices=("off", "on", "auto"),
+                        help="lossless coding of staging segments before D2H (SDMA link) in the step legs: off, on, "
+                             "or auto (only while two staging slots of D2H bytes are queued)")
+    parser.add_argument("--micro-wire-coding", default="off", choices=("off", "on", "auto"),
+                        help="wire coding in the block microbench, which measures the pack and unpack kernels "
+                             "(off by default: it refills its sources with random bits, which do not code)")
     parser.add_argument("--link", default="sdma", choices=("sdma", "hipdma"),
                         help="host-link transport: SDMA through HSA with host-side ordering, or the same DMA "
                              "copies on HIP streams ordered by hipStreamWaitEvent")

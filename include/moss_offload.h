@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 9
+#define MO_ABI_VERSION 10
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -68,6 +68,15 @@ extern "C" {
                                            loads instead of non-temporal ones             */
 #define MO_FLAG_UNPACK_CACHED_STORE 0x100 /* the unpack kernel writes restored tensors with
                                              ordinary stores instead of streaming ones      */
+#define MO_FLAG_WIRE_CODING 0x200 /* code every staging segment of at least 256 KiB with the
+                                     lossless wire coding (mo_wire_encode) before its D2H and
+                                     decode it after its H2D: bfloat16 activations cross the
+                                     host link in about 0.75 of their bytes. SDMA link only
+                                     (the coded length is read when the copy is issued);
+                                     costs one wire buffer per staging and restore slot     */
+#define MO_FLAG_WIRE_AUTO 0x400   /* the same, only for segments that close while the D2H
+                                     copies queued or in flight hold at least two staging
+                                     slots of bytes (the link is the bottleneck)            */
 
 /*
  * A strided tensor view on the device. `ptr` is the address of logical element (0,...,0),
@@ -139,6 +148,12 @@ typedef struct mo_stats {
   uint64_t timed_pack_launches, timed_unpack_launches;
   uint64_t timed_pack_hbm_bytes, timed_unpack_hbm_bytes; /* device-memory bytes read + written
                                                             by those launches                */
+  uint64_t wire_segments;      /* segments sent wire-coded (MO_FLAG_WIRE_*)               */
+  uint64_t wire_raw_bytes;     /* their payload bytes                                     */
+  uint64_t wire_bytes;         /* their coded bytes, counted as each D2H completes; bytes_d2h
+                                  and bytes_h2d count coded bytes for coded segments        */
+  uint64_t device_ring_bytes;  /* device memory the engine holds: staging and restore slots,
+                                  plus their wire buffers once wire coding has run          */
 } mo_stats;
 
 typedef struct mo_engine mo_engine;
@@ -161,6 +176,21 @@ int mo_gather(const mo_tensor* tensors, int n, uint64_t payload, const uint64_t*
  * Replaces restored.copy_(payload) at activation_offload.py:75-76. */
 int mo_scatter(const mo_tensor* tensors, int n, uint64_t payload, const uint64_t* offsets,
                uint64_t stream);
+
+/* Wire coding of a payload (lossless; no counterpart in the reference, which copies raw bytes).
+ * The engine codes staging segments with it before their D2H when MO_FLAG_WIRE_CODING (or
+ * MO_FLAG_WIRE_AUTO) is set. Sixteen-bit words keep their sign and mantissa as a byte and
+ * replace their 8-bit exponent by an offset of 0-8 bits from the smallest exponent of their
+ * 512-word block; bfloat16 activations shrink to about 0.75 of their bytes. Format in
+ * csrc/mo_wire.h. mo_wire_capacity: the largest coded size of raw_bytes (the wire buffer to
+ * provide). mo_wire_encode codes raw_bytes at device `raw` into device `wire` (3 launches on
+ * `stream`); the coded size is the stream's first u64 and is also written to pinned host memory
+ * at `host_total` (0: not). mo_wire_decode restores raw_bytes bytes from a coded stream of at
+ * most wire_bytes. Buffers 16-byte aligned, raw_bytes at most 2^31. */
+uint64_t mo_wire_capacity(uint64_t raw_bytes);
+int mo_wire_encode(uint64_t raw, uint64_t raw_bytes, uint64_t wire, uint64_t wire_capacity, uint64_t host_total,
+                   uint64_t stream);
+int mo_wire_decode(uint64_t wire, uint64_t wire_bytes, uint64_t raw, uint64_t raw_bytes, uint64_t stream);
 
 /* Gather n tensor views, in the payload format of mo_gather, into pinned host memory at `host`
  * (host_bytes long) on `stream`, allocating nothing. offsets[i] (may be NULL) receives each

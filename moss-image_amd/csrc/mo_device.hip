@@ -26,6 +26,7 @@
 #include <stdint.h>
 
 #include "mo_kdesc.h"
+#include "mo_wire.h"
 
 // The scratch of mo_pack_to_host (size kNoAllocScratchBytes). External linkage with a C name:
 // the host finds it in the loaded code object with hipModuleGetGlobal, once per device, and
@@ -419,5 +420,262 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_link_copy_kernel(c
   for (; base < nvec; base += lanes) st16(dst + base * 16, ld16(src + base * 16));
   if (blockIdx.x == 0) {
     for (uint64_t b = nvec * 16 + threadIdx.x; b < nbytes; b += kThreads) st<kG>(dst + b, ld<kG, uint8_t>(src + b));
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Wire coding of a staging segment (format in mo_wire.h): three kernels code a segment into a
+// wire buffer (block widths per tile, one-workgroup scan of the tile sizes into offsets plus
+// the header and the raw tail, then the tiles), and one kernel decodes it. Each workgroup codes
+// one tile of 32 blocks; each of its four waves takes 8 blocks, a lane 8 words (16 bytes) of
+// a block. Every store into the wire buffer goes through a buffer resource bounded by the
+// buffer's capacity, and the decoder reads the coded stream through one too, so a stream that
+// arrives damaged cannot make either kernel touch memory outside its buffers.
+namespace mo {
+
+__device__ __forceinline__ uint32_t wave_min(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, m, 64));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, m, 64));
+  return v;
+}
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int k) {
+  const uint32_t w = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
+  return (k & 1) ? w >> 16 : w & 0xffffu;
+}
+__device__ __forceinline__ uint32_t exponent_of(uint32_t word) { return (word >> 7) & 0xffu; }
+// bits needed for offsets 0..range
+__device__ __forceinline__ uint32_t width_of(uint32_t range) { return range ? 32u - __clz(range) : 0u; }
+
+// Exponent range of one block: the wave's 64 lanes hold its 512 words.
+__device__ __forceinline__ void block_range(const uint4& v, uint32_t& lo, uint32_t& hi) {
+  lo = 255;
+  hi = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t e = exponent_of(word_of(v, k));
+    lo = min(lo, e);
+    hi = max(hi, e);
+  }
+  lo = wave_min(lo);
+  hi = wave_max(hi);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wire_rsrc(const char* p, uint64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, (int)(bytes < 0x7fffffffull ? bytes : 0x7fffffffull),
+                                           0x00020000);
+}
+
+}  // namespace mo
+
+// Pass 1: the coded size of each tile, written into the stream's tile table.
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_sizes_kernel(const char* raw, uint64_t raw_bytes,
+                                                                                 char* wire, uint64_t wire_capacity) {
+  using namespace mo;
+  __shared__ uint32_t part[kThreads / 64];
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t nblocks = wire_blocks(raw_bytes);
+  const uint64_t tile = blockIdx.x;
+  uint32_t sum = 0;
+  for (int j = 0; j < 8; ++j) {
+    const uint64_t b = tile * kWireTileBlocks + wave * 8 + j;
+    if (b < nblocks) {  // the same for every lane of the wave
+      uint32_t lo, hi;
+      block_range(ld16(raw + b * kWireBlockBytes + lane * 16), lo, hi);
+      sum += wire_block_coded(width_of(hi - lo));
+    }
+  }
+  if (lane == 0) part[wave] = sum;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const __amdgpu_buffer_rsrc_t w = wire_rsrc(wire, wire_capacity);
+    __builtin_amdgcn_raw_buffer_store_b32(kWireTileHeader + part[0] + part[1] + part[2] + part[3], w,
+                                          (int)(kWireHeader + 4 * tile), 0, 0);
+  }
+}
+
+// Pass 2 (one workgroup of kWireScanThreads): tile sizes -> tile offsets (exclusive scan from
+// tiles_start), the header, the raw tail; the total also to `host_total` (pinned host memory,
+// may be null), where the copy engine's issuer reads it once this kernel has completed.
+extern "C" __global__ __launch_bounds__(mo::kWireScanThreads) void mo_wire_scan_kernel(const char* raw,
+                                                                                        uint64_t raw_bytes, char* wire,
+                                                                                        uint64_t wire_capacity,
+                                                                                        uint64_t* host_total) {
+  using namespace mo;
+  __shared__ uint32_t sh[kWireScanThreads];
+  const uint32_t tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t w = wire_rsrc(wire, wire_capacity);
+  const uint64_t tiles = wire_tiles(raw_bytes);
+  uint64_t carry = wire_tiles_start(raw_bytes);
+  for (uint64_t base = 0; base < tiles; base += kWireScanThreads) {
+    const uint64_t t = base + tid;
+    const uint32_t v = t < tiles ? __builtin_amdgcn_raw_buffer_load_b32(w, (int)(kWireHeader + 4 * t), 0, 0) : 0u;
+    sh[tid] = v;
+    __syncthreads();
+    for (uint32_t off = 1; off < kWireScanThreads; off <<= 1) {
+      const uint32_t x = tid >= off ? sh[tid - off] : 0u;
+      __syncthreads();
+      sh[tid] += x;
+      __syncthreads();
+    }
+    if (t < tiles)
+      __builtin_amdgcn_raw_buffer_store_b32((uint32_t)(carry + sh[tid] - v), w, (int)(kWireHeader + 4 * t), 0, 0);
+    const uint32_t chunk = sh[kWireScanThreads - 1];
+    __syncthreads();  // every lane has read sh before the next chunk overwrites it
+    carry += chunk;
+  }
+  const uint64_t tail = raw_bytes % kWireBlockBytes, tail_src = wire_blocks(raw_bytes) * kWireBlockBytes;
+  const uint64_t data_start = wire_data_start(raw_bytes);
+  for (uint64_t i = tid; i < tail; i += kWireScanThreads)
+    __builtin_amdgcn_raw_buffer_store_b8(ld<kG, uint8_t>(raw + tail_src + i), w, (int)(data_start + i), 0, 0);
+  if (tid == 0) {
+    __builtin_amdgcn_raw_buffer_store_b32((uint32_t)carry, w, 0, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32((uint32_t)(carry >> 32), w, 4, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32((uint32_t)raw_bytes, w, 8, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32((uint32_t)tiles, w, 12, 0, 0);
+    if (host_total) st<kG>((char*)host_total, carry);
+  }
+}
+
+// Pass 3: code each tile at its offset.
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_encode_kernel(const char* raw, uint64_t raw_bytes,
+                                                                                  char* wire, uint64_t wire_capacity) {
+  using namespace mo;
+  constexpr int kWaves = kThreads / 64;
+  __shared__ uint32_t width[kWireTileBlocks], base_e[kWireTileBlocks], pre[kWireTileBlocks];
+  __shared__ __attribute__((aligned(16))) unsigned char plane[kWaves][kWireBlockVals];
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t nblocks = wire_blocks(raw_bytes);
+  const uint64_t tile = blockIdx.x;
+  const __amdgpu_buffer_rsrc_t w = wire_rsrc(wire, wire_capacity);
+  const uint32_t toff = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(kWireHeader + 4 * tile), 0, 0);
+  uint4 v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t bl = wave * 8 + j;
+    const uint64_t b = tile * kWireTileBlocks + bl;
+    uint32_t lo = 0, hi = 0;
+    if (b < nblocks) {
+      v[j] = ld16(raw + b * kWireBlockBytes + lane * 16);
+      block_range(v[j], lo, hi);
+    } else {
+      v[j] = make_uint4(0, 0, 0, 0);
+    }
+    if (lane == 0) {
+      width[bl] = b < nblocks ? width_of(hi - lo) : 0u;
+      base_e[bl] = b < nblocks ? lo : 0u;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t acc = 0;
+    for (uint32_t k = 0; k < kWireTileBlocks; ++k) {
+      pre[k] = acc;
+      if (tile * kWireTileBlocks + k < nblocks) acc += wire_block_coded(width[k]);
+    }
+  }
+  if (threadIdx.x < kWireTileBlocks)
+    __builtin_amdgcn_raw_buffer_store_b16((unsigned short)((width[threadIdx.x] << 8) | base_e[threadIdx.x]), w,
+                                          (int)(toff + 2 * threadIdx.x), 0, 0);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t bl = wave * 8 + j;
+    const bool live = tile * kWireTileBlocks + bl < nblocks;
+    const uint32_t wd = width[bl], be = base_e[bl];
+    const uint32_t dst = toff + kWireTileHeader + pre[bl];
+    if (live) {
+      uint32_t sm_lo = 0, sm_hi = 0;
+      uint64_t acc = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t word = word_of(v[j], k);
+        const uint32_t sm = ((word >> 8) & 0x80u) | (word & 0x7fu);
+        if (k < 4) sm_lo |= sm << (8 * k);
+        else sm_hi |= sm << (8 * (k - 4));
+        acc |= (uint64_t)(exponent_of(word) - be) << (k * wd);
+      }
+      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{sm_lo, sm_hi}, w, (int)(dst + 8 * lane), 0, 0);
+      for (uint32_t i = 0; i < wd; ++i) plane[wave][lane * wd + i] = (unsigned char)(acc >> (8 * i));
+    }
+    __syncthreads();
+    if (live && lane < 4 * wd) {
+      const mo_u32x4 chunk = *(const MO_LDS mo_u32x4*)(&plane[wave][16 * lane]);
+      __builtin_amdgcn_raw_buffer_store_b128(chunk, w, (int)(dst + kWireBlockVals + 16 * lane), 0, 0);
+    }
+    __syncthreads();  // the plane is rewritten by the next block
+  }
+}
+
+// Decode a coded stream of `raw_bytes` into `raw`. Grid: max(tiles, 1) workgroups; the first
+// also copies the raw tail. Reads go through a resource over [wire, wire + wire_bytes), writes
+// stay inside [raw, raw + raw_bytes) whatever the stream holds.
+extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_decode_kernel(const char* wire, uint64_t wire_bytes,
+                                                                                  uint64_t raw_bytes, char* raw) {
+  using namespace mo;
+  constexpr int kWaves = kThreads / 64;
+  __shared__ uint32_t width[kWireTileBlocks], base_e[kWireTileBlocks], pre[kWireTileBlocks];
+  __shared__ __attribute__((aligned(16))) unsigned char plane[kWaves][kWireBlockVals];
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t nblocks = wire_blocks(raw_bytes);
+  const uint64_t tile = blockIdx.x;
+  const __amdgpu_buffer_rsrc_t w = wire_rsrc(wire, wire_bytes);
+  const uint32_t toff = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(kWireHeader + 4 * tile), 0, 0);
+  if (threadIdx.x < kWireTileBlocks) {
+    const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(w, (int)(toff + 2 * threadIdx.x), 0, 0);
+    width[threadIdx.x] = min((h >> 8) & 0xfu, 8u);
+    base_e[threadIdx.x] = h & 0xffu;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t acc = 0;
+    for (uint32_t k = 0; k < kWireTileBlocks; ++k) {
+      pre[k] = acc;
+      acc += wire_block_coded(width[k]);
+    }
+  }
+  __syncthreads();
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t bl = wave * 8 + j;
+    const uint64_t b = tile * kWireTileBlocks + bl;
+    const bool live = b < nblocks;
+    const uint32_t wd = width[bl], be = base_e[bl];
+    const uint32_t src = toff + kWireTileHeader + pre[bl];
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 sm = {0, 0};
+    if (live) {
+      sm = __builtin_amdgcn_raw_buffer_load_b64(w, (int)(src + 8 * lane), 0, 0);
+      if (lane < 4 * wd)
+        *(MO_LDS mo_u32x4*)(&plane[wave][16 * lane]) =
+            __builtin_amdgcn_raw_buffer_load_b128(w, (int)(src + kWireBlockVals + 16 * lane), 0, 0);
+    }
+    __syncthreads();
+    if (live) {
+      uint64_t acc = 0;
+      for (uint32_t i = 0; i < wd; ++i) acc |= (uint64_t)plane[wave][lane * wd + i] << (8 * i);
+      const uint32_t mask = (1u << wd) - 1u;
+      uint32_t out[4];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t s = ((k < 4 ? sm[0] : sm[1]) >> (8 * (k & 3))) & 0xffu;
+        const uint32_t e = (be + ((uint32_t)(acc >> (k * wd)) & mask)) & 0xffu;
+        const uint32_t word = ((s & 0x80u) << 8) | (e << 7) | (s & 0x7fu);
+        if (k & 1) out[k >> 1] |= word << 16;
+        else out[k >> 1] = word;
+      }
+      st16(raw + b * kWireBlockBytes + lane * 16, make_uint4(out[0], out[1], out[2], out[3]));
+    }
+    __syncthreads();
+  }
+  if (tile == 0) {
+    const uint64_t tail = raw_bytes % kWireBlockBytes, tail_dst = nblocks * kWireBlockBytes;
+    const uint64_t data_start = wire_data_start(raw_bytes);
+    for (uint64_t i = threadIdx.x; i < tail; i += kThreads)
+      st<kG>(raw + tail_dst + i, (uint8_t)__builtin_amdgcn_raw_buffer_load_b8(w, (int)(data_start + i), 0, 0));
   }
 }

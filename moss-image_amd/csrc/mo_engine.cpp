@@ -234,6 +234,11 @@ struct Segment {
   bool prefetched = false;
   int restore_slot = -1;
   uint64_t restore_gen = 0;
+  // Wire-coded: the host copy (host_bytes long, wire_capacity(bytes)) holds the coded stream,
+  // whose first u64 is its length; a fetch brings it into the restore slot's wire buffer and
+  // the unpack decodes it into the slot first.
+  bool wire = false;
+  uint64_t host_bytes = 0;
 };
 
 struct Entry {
@@ -253,6 +258,8 @@ struct StageSlot {
   uint64_t used = 0;
   uint64_t fill_gen = 0;  // bumped every time the slot is reset for refilling
   int gate = -1;
+  char* wire = nullptr;    // coded streams of the slot's segments (wire coding)
+  uint64_t wire_used = 0;  // reset with `used`
 };
 
 struct RestoreSlot {
@@ -263,12 +270,22 @@ struct RestoreSlot {
   uint64_t tick = 0;
   bool consumed = true;  // scattered at least once since fetched (or empty)
   int gate = -1;
+  char* wire = nullptr;  // a coded segment's stream as fetched (wire coding)
+  bool decoded = true;   // dev holds the fetched segment's raw bytes
 };
 
 struct PendingFree {
   char* host;
   uint64_t bytes;
   CopyRef copies[2];
+};
+
+// Coded bytes of a wire-coded copy, counted once the copy has completed (they are the first
+// u64 of the host copy, known only after the coding kernels ran).
+struct PendingCount {
+  const char* host;
+  CopyRef copy;
+  bool d2h;
 };
 
 struct Timing {
@@ -298,6 +315,8 @@ struct Engine {
   uint64_t gen_counter = 0, tick = 0;
   std::vector<hipEvent_t> timing_pool;
   std::deque<PendingFree> pending;
+  std::deque<PendingCount> counts;
+  uint64_t wire_slot_bytes = 0;  // each staging and restore slot's wire buffer, once allocated
   std::deque<Timing> timings;
   mo_stats st{};
 
@@ -479,7 +498,29 @@ struct Engine {
   }
 
   // ---- deferred host frees ----
+  // Count the coded bytes of wire-coded copies that have completed (before any host free).
+  void process_counts(bool wait) {
+    while (!counts.empty()) {
+      PendingCount& c = counts.front();
+      if (!idle(c.copy)) {
+        if (!wait) break;
+        const auto deadline = std::chrono::steady_clock::now() + std::chrono::seconds(300);
+        while (!idle(c.copy) && std::chrono::steady_clock::now() < deadline)
+          std::this_thread::sleep_for(std::chrono::microseconds(50));
+        if (!idle(c.copy)) break;
+      }
+      if (!c.copy->failed()) {
+        uint64_t total = 0;
+        memcpy(&total, c.host, sizeof(total));
+        (c.d2h ? st.bytes_d2h : st.bytes_h2d) += total;
+        if (c.d2h) st.wire_bytes += total;
+      }
+      counts.pop_front();
+    }
+  }
+
   int process_pending(bool wait) {
+    process_counts(wait);
     const auto deadline = std::chrono::steady_clock::now() + std::chrono::seconds(300);
     for (auto it = pending.begin(); it != pending.end();) {
       bool done = idle(it->copies[0]) && idle(it->copies[1]);
@@ -506,7 +547,30 @@ struct Engine {
     StageSlot& slot = stage[seg.stage_slot];
     seg.bytes = slot.used - seg.stage_off;
     open_seg = -1;
+    if (wire_wanted(seg.bytes)) {
+      if (int rc = ensure_wire()) return rc;
+      const uint64_t cap = wire_capacity(seg.bytes);
+      if (slot.wire_used + cap <= wire_slot_bytes) {
+        char* w = slot.wire + slot.wire_used;
+        if (int rc = pool.alloc(cap, &seg.host)) return rc;
+        seg.host_bytes = cap;
+        // the coded length goes straight to the host copy's first u64, where the copy engine's
+        // issuer reads it once the coding kernels have completed
+        MO_HIP((hipError_t)wire_encode((uint64_t)(slot.dev + seg.stage_off), seg.bytes, (uint64_t)w, cap,
+                                        (uint64_t)seg.host, stream));
+        MO_LINK(link->d2h_sized(seg.host, w, (const volatile uint64_t*)seg.host, cap, stream, slot.gate, &seg.d2h));
+        slot.wire_used += (cap + 255) & ~uint64_t(255);
+        seg.wire = true;
+        seg.committed = true;
+        st.d2h_copies++;
+        st.wire_segments++;
+        st.wire_raw_bytes += seg.bytes;
+        counts.push_back(PendingCount{seg.host, seg.d2h, true});
+        return 0;
+      }
+    }
     if (int rc = pool.alloc(seg.bytes, &seg.host)) return rc;
+    seg.host_bytes = seg.bytes;
     MO_LINK(link->d2h(seg.host, slot.dev + seg.stage_off, seg.bytes, stream, slot.gate, &seg.d2h));
     seg.committed = true;
     st.d2h_copies++;
@@ -514,12 +578,42 @@ struct Engine {
     return 0;
   }
 
+  // Whether to code a closing segment: MO_FLAG_WIRE_CODING codes every segment of at least
+  // kWireMinBytes; MO_FLAG_WIRE_AUTO once the link is behind in this forward: the staging ring
+  // came round to a slot whose D2H was still on the copy engines (issued, not finished), so the
+  // pack had to wait for the link, not for the GPU to reach the copy. It stays on until the
+  // next unpack (the backward has begun). A checkpointed step's few MB per block leave the
+  // ring idle and are never coded; a non-checkpointed forward fills it within a few blocks and
+  // codes from then on. Only a transport that sizes copies at issue can carry coded segments.
+  static constexpr uint64_t kWireMinBytes = 256ull << 10;
+  bool link_behind = false;
+  bool wire_wanted(uint64_t bytes) {
+    if (!(cfg.flags & (MO_FLAG_WIRE_CODING | MO_FLAG_WIRE_AUTO)) || bytes < kWireMinBytes) return false;
+    if (!link->sized_copies()) return false;
+    if (cfg.flags & MO_FLAG_WIRE_CODING) return true;
+    return link_behind;
+  }
+
+  // Wire buffers, allocated on first use: one per staging slot (the coded streams of its
+  // segments) and one per restore slot (a fetched stream).
+  int ensure_wire() {
+    if (wire_slot_bytes) return 0;
+    const uint64_t bytes = ((wire_capacity(cfg.stage_slot_bytes) + cfg.stage_slot_bytes / 64 + (2ull << 20)) + 4095) &
+                           ~uint64_t(4095);
+    for (auto& s : stage) MO_HIP(hipMalloc(&s.wire, bytes));
+    for (auto& r : restore) MO_HIP(hipMalloc(&r.wire, bytes));
+    wire_slot_bytes = bytes;
+    return 0;
+  }
+
   int advance_slot(hipStream_t stream) {
     stage_cur = (stage_cur + 1) % (int)stage.size();
     StageSlot& s = stage[stage_cur];
     st.stage_slot_waits++;
+    if (link->link_busy(s.gate)) link_behind = true;
     MO_LINK(link->wait(s.gate, stream));
     s.used = 0;
+    s.wire_used = 0;
     s.fill_gen++;
     return 0;
   }
@@ -694,7 +788,16 @@ struct Engine {
       return fail(MO_E_STATE, "group " + std::to_string(g.id) + " segment " + std::to_string(si) +
                                   " has no host copy (its D2H was never issued)");
     CopyRef copy;
-    MO_LINK(link->h2d(r.dev, seg.host, seg.bytes, seg.d2h, r.gate, &copy));
+    if (seg.wire) {
+      MO_LINK(link->h2d_sized(r.wire, seg.host, (const volatile uint64_t*)seg.host, seg.host_bytes, seg.d2h, r.gate,
+                              &copy));
+      counts.push_back(PendingCount{seg.host, copy, false});
+      r.decoded = false;
+    } else {
+      MO_LINK(link->h2d(r.dev, seg.host, seg.bytes, seg.d2h, r.gate, &copy));
+      st.bytes_h2d += seg.bytes;
+      r.decoded = true;
+    }
     seg.h2d = std::move(copy);
     r.group = g.id;
     r.seg = si;
@@ -704,7 +807,6 @@ struct Engine {
     seg.restore_slot = k;
     seg.restore_gen = r.gen;
     st.h2d_copies++;
-    st.bytes_h2d += seg.bytes;
     return 0;
   }
 
@@ -726,6 +828,7 @@ struct Engine {
 
   int unpack(uint64_t gid, const uint64_t* dst, uint32_t n, hipStream_t stream) {
     if (int rc = check_link()) return rc;
+    link_behind = false;
     process_pending(false);
     Group* g = find(gid);
     if (!g) return fail(MO_E_INVALID, "mo_unpack: unknown group " + std::to_string(gid));
@@ -762,6 +865,12 @@ struct Engine {
       seg.prefetched = false;
       if (r) {
         MO_LINK(link->wait(r->gate, stream));
+        if (!r->decoded) {
+          // the coded stream has landed (wait): decode it into the slot on this stream, ahead
+          // of the unpack kernels that read the slot
+          MO_HIP((hipError_t)wire_decode((uint64_t)r->wire, seg.host_bytes, (uint64_t)r->dev, seg.bytes, stream));
+          r->decoded = true;
+        }
         src = r->dev;
       }
       KernelTimer timer(this, false);
@@ -799,7 +908,7 @@ struct Engine {
       open_seg = -1;
     }
     for (Segment& seg : g->segs) {
-      if (seg.host) pending.push_back(PendingFree{seg.host, seg.bytes, {seg.d2h, seg.h2d}});
+      if (seg.host) pending.push_back(PendingFree{seg.host, seg.host_bytes, {seg.d2h, seg.h2d}});
       if (seg.restore_slot >= 0) {
         RestoreSlot& r = restore[seg.restore_slot];
         if (r.group == g->id && r.gen == seg.restore_gen) {
@@ -822,6 +931,7 @@ struct Engine {
 
   void fill_stats(mo_stats* out) {
     process_timings(false);
+    process_counts(false);
     LinkStats ls;
     link->stats(&ls);
     st.d2h_ms = ls.d2h_ms;
@@ -838,6 +948,7 @@ struct Engine {
     st.host_bytes_in_use = pool.in_use();
     st.host_bytes_peak = pool.peak();
     st.host_bytes_reserved = pool.reserved();
+    st.device_ring_bytes = (stage.size() + restore.size()) * (cfg.stage_slot_bytes + wire_slot_bytes);
     *out = st;
   }
 
@@ -896,6 +1007,7 @@ struct Engine {
     groups.clear();
     (void)process_pending(true);
     pending.clear();
+    counts.clear();
     link.reset();
     for (auto& t : timings) {
       (void)hipEventDestroy(t.start);
@@ -910,10 +1022,14 @@ struct Engine {
     }
     if (eq_flags) (void)hipHostFree(eq_flags);
     eq_flags = nullptr;
-    for (auto& s : stage)
+    for (auto& s : stage) {
       if (s.dev) (void)hipFree(s.dev);
-    for (auto& r : restore)
+      if (s.wire) (void)hipFree(s.wire);
+    }
+    for (auto& r : restore) {
       if (r.dev) (void)hipFree(r.dev);
+      if (r.wire) (void)hipFree(r.wire);
+    }
     stage.clear();
     restore.clear();
     pool.release_all();
@@ -1020,6 +1136,32 @@ int mo_gather(const mo_tensor* tensors, int n, uint64_t payload, const uint64_t*
 int mo_scatter(const mo_tensor* tensors, int n, uint64_t payload, const uint64_t* offsets, uint64_t stream) {
   MO_GUARD_BEGIN
   return mo::run_copy(false, tensors, n, payload, offsets, stream);
+  MO_GUARD_END
+}
+
+uint64_t mo_wire_capacity(uint64_t raw_bytes) { return mo::wire_capacity(raw_bytes); }
+
+int mo_wire_encode(uint64_t raw, uint64_t raw_bytes, uint64_t wire, uint64_t wire_capacity, uint64_t host_total,
+                   uint64_t stream) {
+  MO_GUARD_BEGIN
+  std::string err;
+  if (int rc = mo::wire_check(raw, raw_bytes, wire, wire_capacity, err)) return mo::set_error(rc, "mo_wire_encode: " + err);
+  if (wire_capacity < mo::wire_capacity(raw_bytes))
+    return mo::set_error(MO_E_INVALID, "mo_wire_encode: wire buffer smaller than mo_wire_capacity(raw_bytes)");
+  if (host_total % 8) return mo::set_error(MO_E_INVALID, "mo_wire_encode: host_total must be 8-byte aligned");
+  if (int rc = mo::wire_encode(raw, raw_bytes, wire, wire_capacity, host_total, (hipStream_t)stream))
+    return mo::set_hip_error(rc, "mo_wire_encode launch");
+  return 0;
+  MO_GUARD_END
+}
+
+int mo_wire_decode(uint64_t wire, uint64_t wire_bytes, uint64_t raw, uint64_t raw_bytes, uint64_t stream) {
+  MO_GUARD_BEGIN
+  std::string err;
+  if (int rc = mo::wire_check(raw, raw_bytes, wire, wire_bytes, err)) return mo::set_error(rc, "mo_wire_decode: " + err);
+  if (int rc = mo::wire_decode(wire, wire_bytes, raw, raw_bytes, (hipStream_t)stream))
+    return mo::set_hip_error(rc, "mo_wire_decode launch");
+  return 0;
   MO_GUARD_END
 }
 

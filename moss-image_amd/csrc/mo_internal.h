@@ -8,6 +8,7 @@
 
 #include "mo_kdesc.h"
 #include "mo_layout.h"
+#include "mo_wire.h"
 
 namespace mo {
 
@@ -59,5 +60,16 @@ int noalloc_scratch(uint64_t* ptr, uint64_t* bytes);
 
 // mo_equal_kernel over nbytes at a and b (16-byte aligned); writes 1 to *flag on a difference.
 int launch_equal(const void* a, const void* b, uint64_t nbytes, uint32_t* flag, hipStream_t stream);
+
+// Wire coding of a segment (format and sizes in mo_wire.h). wire_encode codes `raw_bytes` at
+// `raw` into `wire` (capacity at least wire_capacity(raw_bytes)) with three launches on
+// `stream`, and also writes the coded size to pinned host memory at `host_total` (0: not).
+// wire_decode restores the raw bytes from a coded stream of at most `wire_bytes`. Both buffers
+// 16-byte aligned (wire_check).
+constexpr uint64_t kWireMaxRaw = 1ull << 31;
+int wire_check(uint64_t raw, uint64_t raw_bytes, uint64_t wire, uint64_t wire_bytes, std::string& err);
+int wire_encode(uint64_t raw, uint64_t raw_bytes, uint64_t wire, uint64_t capacity, uint64_t host_total,
+                hipStream_t stream);
+int wire_decode(uint64_t wire, uint64_t wire_bytes, uint64_t raw, uint64_t raw_bytes, hipStream_t stream);
 
 }  // namespace mo

@@ -38,6 +38,7 @@ struct DeviceModule {
   // the same four with ELEM pieces in the launch (they reserve the LDS staging buffer)
   hipFunction_t pack_elem = nullptr, unpack_elem = nullptr, pack1_elem = nullptr, unpack1_elem = nullptr;
   hipFunction_t equal = nullptr;
+  hipFunction_t wire_sizes = nullptr, wire_scan = nullptr, wire_encode = nullptr, wire_decode = nullptr;
   // this device's copy of mo_noalloc_scratch (every device holds its own, at its own address)
   uint64_t scratch = 0, scratch_bytes = 0;
 };
@@ -58,6 +59,10 @@ int load_functions(DeviceModule& m) {
   if ((e = hipModuleGetFunction(&m.pack1_elem, m.module, "mo_pack1_elem_kernel")) != hipSuccess) return (int)e;
   if ((e = hipModuleGetFunction(&m.unpack1_elem, m.module, "mo_unpack1_elem_kernel")) != hipSuccess) return (int)e;
   if ((e = hipModuleGetFunction(&m.equal, m.module, "mo_equal_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.wire_sizes, m.module, "mo_wire_sizes_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.wire_scan, m.module, "mo_wire_scan_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.wire_encode, m.module, "mo_wire_encode_kernel")) != hipSuccess) return (int)e;
+  if ((e = hipModuleGetFunction(&m.wire_decode, m.module, "mo_wire_decode_kernel")) != hipSuccess) return (int)e;
   // Set-up of the allocation-free entry point, once per device with that device current: the
   // device address of this module's scratch array. From here on only this address is used.
   hipDeviceptr_t scratch = nullptr;
@@ -280,6 +285,67 @@ int launch_equal(const void* a, const void* b, uint64_t nbytes, uint32_t* flag, 
   uint32_t* f = flag;
   void* params[] = {&x, &y, &n, &f};
   return (int)hipModuleLaunchKernel(m.equal, (uint32_t)tiles, 1, 1, kThreads, 1, 1, 0, stream, params, nullptr);
+}
+
+// Wire coding (mo_wire.h). The caller checks sizes and alignment (wire_check).
+int wire_check(uint64_t raw, uint64_t raw_bytes, uint64_t wire, uint64_t wire_bytes, std::string& err) {
+  if (raw_bytes > kWireMaxRaw) {
+    err = "segment too large for wire coding (at most " + std::to_string(kWireMaxRaw) + " bytes)";
+    return MO_E_INVALID;
+  }
+  if ((raw % 16) || (wire % 16)) {
+    err = "wire coding needs 16-byte aligned buffers";
+    return MO_E_INVALID;
+  }
+  if ((raw_bytes && !raw) || !wire) {
+    err = "null buffer";
+    return MO_E_INVALID;
+  }
+  (void)wire_bytes;
+  return 0;
+}
+
+int wire_encode(uint64_t raw, uint64_t raw_bytes, uint64_t wire, uint64_t capacity, uint64_t host_total,
+                hipStream_t stream) {
+  DeviceModule m;
+  if (int rc = module_of_device(&m)) return rc;
+  const uint64_t tiles = wire_tiles(raw_bytes);
+  const void* r = (const void*)raw;
+  void* w = (void*)wire;
+  uint64_t n = raw_bytes, cap = capacity;
+  void* ht = (void*)host_total;
+  hipError_t e;
+  if (tiles) {
+    void* params[] = {&r, &n, &w, &cap};
+    if ((e = hipModuleLaunchKernel(m.wire_sizes, (uint32_t)tiles, 1, 1, kThreads, 1, 1, 0, stream, params, nullptr)) !=
+        hipSuccess)
+      return (int)e;
+  }
+  {
+    void* params[] = {&r, &n, &w, &cap, &ht};
+    if ((e = hipModuleLaunchKernel(m.wire_scan, 1, 1, 1, kWireScanThreads, 1, 1, 0, stream, params, nullptr)) !=
+        hipSuccess)
+      return (int)e;
+  }
+  if (tiles) {
+    void* params[] = {&r, &n, &w, &cap};
+    if ((e = hipModuleLaunchKernel(m.wire_encode, (uint32_t)tiles, 1, 1, kThreads, 1, 1, 0, stream, params,
+                                   nullptr)) != hipSuccess)
+      return (int)e;
+  }
+  return 0;
+}
+
+int wire_decode(uint64_t wire, uint64_t wire_bytes, uint64_t raw, uint64_t raw_bytes, hipStream_t stream) {
+  DeviceModule m;
+  if (int rc = module_of_device(&m)) return rc;
+  const uint64_t tiles = wire_tiles(raw_bytes);
+  const void* w = (const void*)wire;
+  void* r = (void*)raw;
+  uint64_t wb = wire_bytes, n = raw_bytes;
+  void* params[] = {&w, &wb, &n, &r};
+  return (int)hipModuleLaunchKernel(m.wire_decode, (uint32_t)(tiles ? tiles : 1), 1, 1, kThreads, 1, 1, 0, stream,
+                                    params, nullptr);
 }
 
 }  // namespace mo

@@ -103,6 +103,7 @@ using EventRef = std::shared_ptr<EventHold>;
 struct SdmaCopy : CopyState {
   std::atomic<bool> finished{false};
   std::atomic<bool> fail{false};
+  std::atomic<bool> issued{false};  // handed to the copy engines
   bool to_host = true;
   uint64_t bytes = 0;
   int64_t issue_ns = 0;
@@ -125,6 +126,9 @@ struct Job {
   EventRef wait;  // issue after this HIP event completed
   SdmaRef after;  // and after this copy completed (the D2H that filled an H2D's source)
   SdmaRef prev;   // and after this earlier copy through the same gate (GateOrder)
+  // sized copy: the byte count is read from here at issue, clamped to [1, max_bytes]
+  const volatile uint64_t* size = nullptr;
+  uint64_t max_bytes = 0;
   // Polling of `wait` backs off while the compute stream is far behind (hipEventQuery is a
   // runtime call that competes with the application's own launches).
   int64_t next_query_ns = 0;
@@ -234,6 +238,16 @@ class SdmaLink : public Link {
   }
 
   int d2h(void* dst, const void* src, uint64_t bytes, hipStream_t compute, int gate, CopyRef* out) override {
+    return d2h_job(dst, src, bytes, compute, gate, out, nullptr);
+  }
+
+  int h2d(void* dst, const void* src, uint64_t bytes, const CopyRef& after, int gate, CopyRef* out) override {
+    return h2d_job(dst, src, bytes, after, gate, out, nullptr);
+  }
+
+  // `size` null: a copy of `bytes`; else a sized copy of at most `bytes` (see Link).
+  int d2h_job(void* dst, const void* src, uint64_t bytes, hipStream_t compute, int gate, CopyRef* out,
+              const volatile uint64_t* size) {
     EventRef ev;
     if (int rc = take_event(&ev)) return rc;
     hipError_t e = hipEventRecord(ev->ev, compute);
@@ -245,13 +259,16 @@ class SdmaLink : public Link {
     job.src = src;
     job.wait = std::move(ev);
     job.prev = gates_[gate].order.on_read(copy);
+    job.size = size;
+    job.max_bytes = bytes;
     enqueue(std::move(job));
     d2h_bytes_ += bytes;
     *out = copy;
     return 0;
   }
 
-  int h2d(void* dst, const void* src, uint64_t bytes, const CopyRef& after, int gate, CopyRef* out) override {
+  int h2d_job(void* dst, const void* src, uint64_t bytes, const CopyRef& after, int gate, CopyRef* out,
+              const volatile uint64_t* size) {
     auto copy = make_copy(false, bytes);
     h2d_inflight().fetch_add(1, std::memory_order_relaxed);
     copy->counted_h2d = true;
@@ -262,10 +279,29 @@ class SdmaLink : public Link {
     job.wait = gates_[gate].consumed;
     job.after = std::dynamic_pointer_cast<SdmaCopy>(after);
     job.prev = gates_[gate].order.on_write(copy);
+    job.size = size;
+    job.max_bytes = bytes;
     enqueue(std::move(job));
     h2d_bytes_ += bytes;
     *out = copy;
     return 0;
+  }
+
+  bool sized_copies() const override { return true; }
+
+  int d2h_sized(void* dst, const void* src, const volatile uint64_t* size, uint64_t max_bytes, hipStream_t compute,
+                int gate, CopyRef* out) override {
+    return d2h_job(dst, src, max_bytes, compute, gate, out, size);
+  }
+
+  int h2d_sized(void* dst, const void* src, const volatile uint64_t* size, uint64_t max_bytes, const CopyRef& after,
+                int gate, CopyRef* out) override {
+    return h2d_job(dst, src, max_bytes, after, gate, out, size);
+  }
+
+  bool link_busy(int gate) override {
+    const SdmaRef& c = gates_[gate].order.last;
+    return c && !c->done() && c->issued.load(std::memory_order_acquire);
   }
 
   int writeback(void* dst, const void* src, uint64_t bytes, int gate, CopyRef* out) override {
@@ -448,6 +484,7 @@ class SdmaLink : public Link {
       c->counted_h2d = false;
       h2d_inflight().fetch_sub(1, std::memory_order_relaxed);
     }
+
     const int64_t t = now_ns();
     if (failed) {
       c->fail.store(true, std::memory_order_release);
@@ -499,12 +536,20 @@ class SdmaLink : public Link {
       }
     }
     SdmaCopy& c = *job.copy;
+    if (job.size) {
+      // The dependency that produced *size has completed (its HIP event, or the D2H whose
+      // bytes begin with it): read the coded size now.
+      std::atomic_thread_fence(std::memory_order_acquire);
+      const uint64_t n = *job.size;
+      c.bytes = n == 0 ? 1 : (n > job.max_bytes ? job.max_bytes : n);
+    }
     const uint32_t* engines = c.to_host ? e_d2h_ : e_h2d_;
     const bool quiet = !c.to_host || h2d_inflight().load(std::memory_order_relaxed) == 0;
     const int parts = (c.to_host ? n_d2h_ : n_h2d_) > 1 && c.bytes >= kSplitBytes && quiet ? 2 : 1;
     const uint64_t half = parts == 2 ? c.bytes / 2 / 4096 * 4096 : c.bytes;
     c.parts_left = parts;
     c.issue_ns = now_ns();
+    c.issued.store(true, std::memory_order_release);
     if (c.to_host) {
       c.counted_d2h = true;
       d2h_inflight_++;
@@ -795,6 +840,12 @@ class StreamLink : public Link {
     st_.d2h_bytes += bytes;
     *out = copy;
     return 0;
+  }
+
+  // Copies on HIP streams are enqueued at once; whether one has started is not known here.
+  bool link_busy(int gate) override {
+    const auto& c = gates_[gate].order.last;
+    return c && !c->done();
   }
 
   // The compute stream waits for the gate's last copy: GPU-side, the host does not block.

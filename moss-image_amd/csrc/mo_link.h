@@ -41,7 +41,7 @@ struct CopyState {
 using CopyRef = std::shared_ptr<CopyState>;
 
 struct LinkStats {
-  uint64_t d2h_bytes = 0, h2d_bytes = 0;        // issued
+  uint64_t d2h_bytes = 0, h2d_bytes = 0;        // issued (sized copies: their largest size)
   uint64_t d2h_done_bytes = 0, h2d_done_bytes = 0;  // completed and timed
   double d2h_ms = 0, h2d_ms = 0;                // engine-busy time of completed copies
   uint64_t failures = 0;
@@ -70,6 +70,25 @@ class Link {
   virtual int consumed(int gate, hipStream_t compute) = 0;
   // Block until every copy issued so far finished.
   virtual int synchronize() = 0;
+  // Sized copies: the byte count is read from pinned host memory at `size` when the copy is
+  // issued, which is after its dependencies finished (for d2h_sized: the work enqueued on
+  // `compute`, which writes *size; for h2d_sized: `after`, whose bytes begin with it), and is
+  // clamped to [1, max_bytes]. Only a transport that issues copies after their dependencies
+  // can take them (sized_copies()).
+  virtual bool sized_copies() const { return false; }
+  virtual int d2h_sized(void* dst, const void* src, const volatile uint64_t* size, uint64_t max_bytes,
+                        hipStream_t compute, int gate, CopyRef* out) {
+    (void)dst, (void)src, (void)size, (void)max_bytes, (void)compute, (void)gate, (void)out;
+    return (int)hipErrorNotSupported;
+  }
+  virtual int h2d_sized(void* dst, const void* src, const volatile uint64_t* size, uint64_t max_bytes,
+                        const CopyRef& after, int gate, CopyRef* out) {
+    (void)dst, (void)src, (void)size, (void)max_bytes, (void)after, (void)gate, (void)out;
+    return (int)hipErrorNotSupported;
+  }
+  // Whether the gate's last copy is on the copy engines (its dependencies were met and it was
+  // issued) and has not finished: the link, not the work it waits for, holds the gate.
+  virtual bool link_busy(int gate) = 0;
   // Time copies by the DMA engine's own start and end stamps instead of the host clock at
   // issue and completion. False if the transport cannot (it keeps the host clock).
   virtual bool use_dma_timestamps() { return false; }

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 9
+MO_ABI_VERSION = 10
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -32,6 +32,8 @@ MO_FLAG_HIP_DMA = 0x20
 MO_FLAG_PACK_NT_LOAD = 0x40
 MO_FLAG_UNPACK_CACHED_LOAD = 0x80
 MO_FLAG_UNPACK_CACHED_STORE = 0x100
+MO_FLAG_WIRE_CODING = 0x200
+MO_FLAG_WIRE_AUTO = 0x400
 MO_TENSOR_BF16_HIGH = 0x1
 
 NO_GROUP = (1 << 64) - 1
@@ -111,6 +113,10 @@ class MoStats(ctypes.Structure):
         ("timed_unpack_launches", ctypes.c_uint64),
         ("timed_pack_hbm_bytes", ctypes.c_uint64),
         ("timed_unpack_hbm_bytes", ctypes.c_uint64),
+        ("wire_segments", ctypes.c_uint64),
+        ("wire_raw_bytes", ctypes.c_uint64),
+        ("wire_bytes", ctypes.c_uint64),
+        ("device_ring_bytes", ctypes.c_uint64),
     ]
 
     def as_dict(self) -> dict:
@@ -225,6 +231,9 @@ SIGNATURES: dict[str, tuple] = {
     "mo_gradacc_get_stats": (ctypes.c_int, [ctypes.c_void_p, _P(MoGradaccStats)]),
     "mo_gradacc_reset_stats": (ctypes.c_int, [ctypes.c_void_p]),
     "mo_int8_decode": (ctypes.c_int, [_u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32, _u64]),
+    "mo_wire_capacity": (_u64, [_u64]),
+    "mo_wire_encode": (ctypes.c_int, [_u64, _u64, _u64, _u64, _u64, _u64]),
+    "mo_wire_decode": (ctypes.c_int, [_u64, _u64, _u64, _u64, _u64]),
     "mo_int8_linear_forward": (ctypes.c_int, [_u64, _u64, _u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32,
                                               ctypes.c_uint32, _u64]),
     "mo_int8_linear_backward": (ctypes.c_int, [_u64, _u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32,

@@ -51,6 +51,12 @@ class EngineConfig:
     pack_nt_load: bool = False
     unpack_nt_load: bool = True
     unpack_nt_store: bool = True
+    # Lossless wire coding of staging segments on the SDMA link (MO_FLAG_WIRE_*): "off", "on"
+    # (every segment of at least 256 KiB), "auto" (only segments that close while at least two
+    # staging slots of D2H bytes are queued, i.e. while the link sets the pace). Coded segments
+    # cross the link in fewer bytes (bfloat16 activations: about 0.76) for HBM-bound coding
+    # kernels and one wire buffer per staging and restore slot, allocated on first use.
+    wire_coding: str = "auto"
     copy_kernel_blocks: int = 16
     d2h_engine: int = 0
     h2d_engine: int = 0
@@ -98,9 +104,12 @@ class EngineConfig:
             | (_native.MO_FLAG_PACK_NT_LOAD if self.pack_nt_load else 0)
             | (0 if self.unpack_nt_load else _native.MO_FLAG_UNPACK_CACHED_LOAD)
             | (0 if self.unpack_nt_store else _native.MO_FLAG_UNPACK_CACHED_STORE)
+            | {"off": 0, "on": _native.MO_FLAG_WIRE_CODING, "auto": _native.MO_FLAG_WIRE_AUTO}.get(self.wire_coding, 0)
         )
         if self.link not in ("sdma", "hipdma"):
             raise ValueError(f"link must be 'sdma' or 'hipdma', got {self.link!r}")
+        if self.wire_coding not in ("off", "on", "auto"):
+            raise ValueError(f"wire_coding must be 'off', 'on' or 'auto', got {self.wire_coding!r}")
         cfg.copy_kernel_blocks = self.copy_kernel_blocks
         cfg.d2h_engine = self.d2h_engine
         cfg.h2d_engine = self.h2d_engine

@@ -80,8 +80,11 @@ def test_groups_round_trip_lifo(seed, link, staged) -> None:
     order = [i for members in reversed(groups) for i in reversed(members)]
     _restore_and_check(engine, handles, device, order)
     torch.cuda.synchronize(device)
+    engine.synchronize()  # coded segments' link bytes are counted once their copies complete
     stats = engine.stats()
-    assert stats["bytes_d2h"] >= stats["bytes_packed"] > 0
+    # every packed byte crossed the link, raw or wire-coded (the default engine codes segments
+    # while two staging slots of D2H bytes are queued)
+    assert stats["bytes_d2h"] - stats["wire_bytes"] + stats["wire_raw_bytes"] >= stats["bytes_packed"] > 0
     assert stats["bytes_unpacked"] == stats["bytes_packed"]
     assert stats["stage_slot_waits"] > 0  # the ring wrapped
     assert stats["prefetch_hits"] > 0
@@ -417,7 +420,7 @@ def test_timed_link_rate_is_bounded_by_the_host_clock() -> None:
 
     import time
 
-    engine = _engine(timing=True)
+    engine = _engine(timing=True, wire_coding="off")  # raw copies: the link carries exactly the payload
     device = torch.device("cuda", 0)
     stream = torch.cuda.current_stream(device).cuda_stream
     src = torch.randint(0, 256, (32 * MiB,), dtype=torch.uint8, device=device)
@@ -437,3 +440,62 @@ def test_timed_link_rate_is_bounded_by_the_host_clock() -> None:
         assert 10 < rate < 70, rate
     finally:
         engine.close()
+
+
+@pytest.mark.parametrize("mode", ["on", "auto"])
+@pytest.mark.parametrize("staged", [False, True])
+def test_wire_coded_segments_round_trip(mode, staged) -> None:
+    """Segments wire-coded before their D2H and decoded after their H2D (MO_FLAG_WIRE_*):
+    random layouts and dtypes plus bfloat16 activations, across slot boundaries, restored
+    LIFO bitwise; the coded bytes are what crosses the link."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine(wire_coding=mode, timing=True, staged_restore=staged)
+    rng = random.Random(7)
+    g = torch.Generator(device="cpu").manual_seed(7)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    handles, groups = [], []
+    for k in range(6):
+        members = []
+        batch = _tensors(rng, rng.randint(1, 6), device, big=True)
+        batch.append(torch.randn(rng.randint(200_000, 900_000), generator=g).to(torch.bfloat16).to(device))
+        for t in batch:
+            gid, idx = engine.pack(t, stream)
+            handles.append((t, gid, idx))
+            members.append(len(handles) - 1)
+        engine.commit(stream)
+        groups.append(members)
+    order = [i for members in reversed(groups) for i in reversed(members)]
+    _restore_and_check(engine, handles, device, order)
+    engine.synchronize()
+    st = engine.stats()
+    assert st["copy_failures"] == 0
+    if mode == "on":
+        assert st["wire_segments"] > 0
+    if st["wire_segments"]:
+        # random-bit tensors code at width 8 (a little over raw); the coded size never exceeds
+        # the format's worst case
+        assert 0 < st["wire_bytes"] <= st["wire_raw_bytes"] * 1.003 + 4096 * st["wire_segments"]
+    assert st["bytes_unpacked"] == st["bytes_packed"]
+    for _, gid, idx in handles:
+        engine.drop(gid, idx)
+    engine.synchronize()
+    assert engine.stats()["host_bytes_in_use"] == 0
+    engine.close()
+
+
+def test_wire_coding_is_skipped_on_the_hip_stream_link() -> None:
+    """The HIP-stream transport enqueues copies before their sizes exist, so segments stay raw."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine(wire_coding="on", link="hipdma")
+    stream = torch.cuda.current_stream(device).cuda_stream
+    t = torch.randn(600_000, device=device).to(torch.bfloat16)
+    gid, idx = engine.pack(t, stream)
+    engine.commit(stream)
+    assert_bitwise(engine.restore(gid, idx, stream), t)
+    engine.synchronize()
+    assert engine.stats()["wire_segments"] == 0
+    engine.drop(gid, idx)
+    engine.synchronize()
+    engine.close()

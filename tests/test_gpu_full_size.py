@@ -158,14 +158,33 @@ def test_config2_block_saves_round_trip_bitwise(config3_model, link) -> None:
     gc.collect()
 
 
-def test_config3_regime_b_40_blocks_matches_no_offload(config3_model) -> None:
+@pytest.mark.parametrize("wire_coding", ["auto", "off"])
+def test_config3_regime_b_40_blocks_matches_no_offload(config3_model, wire_coding) -> None:
+    """Regime B at 40 blocks with the default engine (wire coding "auto": the forward's backlog
+    makes it code most segments) and with wire coding off."""
+
+    from moss_offload import engine as engine_mod
+
     device = torch.device("cuda", 0)
     inputs = bench.make_inputs(device)
     _regime(config3_model, "B")
     expected = _step(config3_model, inputs, bench.config3_forward, moss_offload.activation_cpu_offload, False)
-    actual, counters, checked = _engine_step(config3_model, inputs)
-    _compare(actual, expected, "config 3 regime B")
-    print(f"hook counters: {counters}, restores checked {checked}", flush=True)
+    previous = engine_mod._DEFAULT_CONFIG
+    moss_offload.reset_engines()
+    moss_offload.configure(wire_coding=wire_coding)
+    try:
+        actual, counters, checked = _engine_step(config3_model, inputs)
+        st = engine_mod.get_engine(device).stats()
+    finally:
+        moss_offload.reset_engines()
+        engine_mod._DEFAULT_CONFIG = previous
+    _compare(actual, expected, f"config 3 regime B, wire coding {wire_coding}")
+    print(f"hook counters: {counters}, restores checked {checked}, wire segments {st['wire_segments']}, "
+          f"coded/raw {st['wire_bytes'] / max(st['wire_raw_bytes'], 1):.3f}", flush=True)
+    if wire_coding == "auto":
+        assert st["wire_segments"] > 100 and st["wire_bytes"] < 0.85 * st["wire_raw_bytes"]
+    else:
+        assert st["wire_segments"] == 0
     # every transformation of the hook acted at this shape, and every restore was checked
     for kind in ("offloaded", "narrowed", "derived", "aliased", "deduplicated"):
         assert counters.get(kind, 0) >= 40, (kind, counters)

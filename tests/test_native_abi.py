@@ -24,7 +24,7 @@ CSRC = ROOT / "moss-image_amd" / "csrc"
 
 def _declared_functions() -> list[str]:
     text = HEADER.read_text()
-    return re.findall(r"^(?:int|const char\*)\s+(mo_\w+)\(", text, flags=re.M)
+    return re.findall(r"^(?:int|uint64_t|const char\*)\s+(mo_\w+)\(", text, flags=re.M)
 
 
 def test_library_exports_every_declared_symbol() -> None:
