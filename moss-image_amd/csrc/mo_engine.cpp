@@ -580,13 +580,15 @@ struct Engine {
 
   // Whether to code a closing segment: MO_FLAG_WIRE_CODING codes every segment of at least
   // kWireMinBytes; MO_FLAG_WIRE_AUTO once the link is behind in this forward: the staging ring
-  // came round to a slot whose D2H was still on the copy engines (issued, not finished), so the
-  // pack had to wait for the link, not for the GPU to reach the copy. It stays on until the
-  // next unpack (the backward has begun). A checkpointed step's few MB per block leave the
-  // ring idle and are never coded; a non-checkpointed forward fills it within a few blocks and
-  // codes from then on. Only a transport that sizes copies at issue can carry coded segments.
+  // came round, twice in a row, to a slot whose D2H was still on the copy engines (issued, not
+  // finished), so the pack had to wait for the link, not for the GPU to reach the copy. It
+  // stays on until the next unpack (the backward has begun). A checkpointed step's few MB per
+  // block leave the ring idle (at most a lone wrap lands on a copy just issued) and are not
+  // coded; a non-checkpointed forward fills the ring within a few blocks and codes from then
+  // on. Only a transport that sizes copies at issue can carry coded segments.
   static constexpr uint64_t kWireMinBytes = 256ull << 10;
   bool link_behind = false;
+  int busy_wraps = 0;  // consecutive slot advances that found the slot's D2H on the engines
   bool wire_wanted(uint64_t bytes) {
     if (!(cfg.flags & (MO_FLAG_WIRE_CODING | MO_FLAG_WIRE_AUTO)) || bytes < kWireMinBytes) return false;
     if (!link->sized_copies()) return false;
@@ -610,7 +612,8 @@ struct Engine {
     stage_cur = (stage_cur + 1) % (int)stage.size();
     StageSlot& s = stage[stage_cur];
     st.stage_slot_waits++;
-    if (link->link_busy(s.gate)) link_behind = true;
+    busy_wraps = link->link_busy(s.gate) ? busy_wraps + 1 : 0;
+    if (busy_wraps >= 2) link_behind = true;
     MO_LINK(link->wait(s.gate, stream));
     s.used = 0;
     s.wire_used = 0;
@@ -829,6 +832,7 @@ struct Engine {
   int unpack(uint64_t gid, const uint64_t* dst, uint32_t n, hipStream_t stream) {
     if (int rc = check_link()) return rc;
     link_behind = false;
+    busy_wraps = 0;
     process_pending(false);
     Group* g = find(gid);
     if (!g) return fail(MO_E_INVALID, "mo_unpack: unknown group " + std::to_string(gid));
