@@ -425,7 +425,7 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_link_copy_kernel(c
 
 // ------------------------------------------------------------------------------------------
 // Wire coding of a staging segment (format in mo_wire.h): three kernels code a segment into a
-// wire buffer (block widths per tile, one-workgroup scan of the tile sizes into offsets plus
+// wire buffer (block sizes per tile, one-workgroup scan of the tile sizes into offsets plus
 // the header and the raw tail, then the tiles), and one kernel decodes it. Each workgroup codes
 // one tile of 32 blocks; each of its four waves takes 8 blocks, a lane 8 words (16 bytes) of
 // a block. Every store into the wire buffer goes through a buffer resource bounded by the
@@ -443,31 +443,87 @@ __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
   for (int m = 32; m >= 1; m >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, m, 64));
   return v;
 }
+// Inclusive prefix sum over the wave's lanes.
+__device__ __forceinline__ uint32_t wave_scan(uint32_t v, uint32_t lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = (uint32_t)__shfl_up((int)v, d, 64);
+    if (lane >= (uint32_t)d) v += y;
+  }
+  return v;
+}
 __device__ __forceinline__ uint32_t word_of(const uint4& v, int k) {
   const uint32_t w = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
   return (k & 1) ? w >> 16 : w & 0xffffu;
 }
 __device__ __forceinline__ uint32_t exponent_of(uint32_t word) { return (word >> 7) & 0xffu; }
-// bits needed for offsets 0..range
-__device__ __forceinline__ uint32_t width_of(uint32_t range) { return range ? 32u - __clz(range) : 0u; }
 
-// Exponent range of one block: the wave's 64 lanes hold its 512 words.
-__device__ __forceinline__ void block_range(const uint4& v, uint32_t& lo, uint32_t& hi) {
-  lo = 255;
-  hi = 0;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wire_rsrc(const char* p, uint64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, (int)(bytes < 0x7fffffffull ? bytes : 0x7fffffffull),
+                                           0x00020000);
+}
+
+struct WireCode {
+  uint32_t width, base, escapes;
+};
+
+// The coding of one block (mo_wire.h): called by every wave of the workgroup the same number of
+// times (it synchronizes the workgroup), `hist` is the wave's 32 bins of LDS. Among width 8,
+// and widths 1-5 with a window of offsets s.. from the block's smallest exponent (no escapes
+// when every exponent fits 2^k values, else 2^k - 1 values and escapes), it takes the smallest
+// coded size, ties to the smaller width, then the smaller s.
+__device__ __forceinline__ WireCode wire_choose(const uint4& v, uint32_t lane, uint32_t* hist) {
+  uint32_t lo = 255, hi = 0;
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const uint32_t e = exponent_of(word_of(v, k));
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t e = exponent_of(word_of(v, j));
     lo = min(lo, e);
     hi = max(hi, e);
   }
   lo = wave_min(lo);
   hi = wave_max(hi);
+  if (lane < kWireBins) hist[lane] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 8; ++j) atomicAdd(&hist[min(exponent_of(word_of(v, j)) - lo, kWireBins - 1)], 1u);
+  __syncthreads();
+  const uint32_t h = lane < kWireBins ? hist[lane] : 0u;
+  const uint32_t p = wave_scan(h, lane) - h;  // lane i < 32: words in bins 0..i-1
+  uint32_t best = (wire_block_coded(8, 0) << 16) | (8u << 8);
+  uint32_t nesc[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (uint32_t k = 1; k <= 5; ++k) {
+    const uint32_t w = 1u << k;
+    const uint32_t s = lane;
+    const uint32_t pa = (uint32_t)__shfl((int)p, (int)min(s + w, kWireBins - 1), 64);
+    const uint32_t pb = (uint32_t)__shfl((int)p, (int)min(s + w - 1, kWireBins - 1), 64);
+    uint32_t esc = 0xffffu;
+    if (s + w <= kWireBins - 1 && pa - p == kWireBlockVals) esc = 0;
+    else if (s + w - 1 <= kWireBins - 1) esc = kWireBlockVals - (pb - p);
+    nesc[k] = esc;
+    if (esc != 0xffffu) best = min(best, (wire_block_coded(k, esc) << 16) | (k << 8) | s);
+  }
+  best = wave_min(best);
+  const uint32_t width = (best >> 8) & 0xffu, s = best & 0xffu;
+  if (hi == lo) return WireCode{0, lo, 0};
+  if (width == 8) return WireCode{8, 0, 0};
+  uint32_t mine = 0;
+#pragma unroll
+  for (uint32_t k = 1; k <= 5; ++k)
+    if (k == width) mine = nesc[k];
+  return WireCode{width, lo + s, (uint32_t)__shfl((int)mine, (int)s, 64)};
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t wire_rsrc(const char* p, uint64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, (int)(bytes < 0x7fffffffull ? bytes : 0x7fffffffull),
-                                           0x00020000);
+// The code of exponent e in a block coded as c; sets *escape for an escaped exponent.
+__device__ __forceinline__ uint32_t wire_code_of(uint32_t e, const WireCode& c, bool* escape) {
+  *escape = false;
+  if (c.width == 8) return e;
+  if (c.width == 0) return 0;
+  const uint32_t d = e - c.base;  // wraps for e < base
+  const uint32_t limit = c.escapes ? (1u << c.width) - 1u : (1u << c.width);
+  if (d < limit) return d;
+  *escape = true;
+  return (1u << c.width) - 1u;
 }
 
 }  // namespace mo
@@ -476,18 +532,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t wire_rsrc(const char* p, uint6
 extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_sizes_kernel(const char* raw, uint64_t raw_bytes,
                                                                                  char* wire, uint64_t wire_capacity) {
   using namespace mo;
-  __shared__ uint32_t part[kThreads / 64];
+  constexpr int kWaves = kThreads / 64;
+  __shared__ uint32_t hist[kWaves][kWireBins];
+  __shared__ uint32_t part[kWaves];
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t nblocks = wire_blocks(raw_bytes);
   const uint64_t tile = blockIdx.x;
+  uint4 v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint64_t b = tile * kWireTileBlocks + wave * 8 + j;
+    v[j] = b < nblocks ? ld16(raw + b * kWireBlockBytes + lane * 16) : make_uint4(0, 0, 0, 0);
+  }
   uint32_t sum = 0;
   for (int j = 0; j < 8; ++j) {
     const uint64_t b = tile * kWireTileBlocks + wave * 8 + j;
-    if (b < nblocks) {  // the same for every lane of the wave
-      uint32_t lo, hi;
-      block_range(ld16(raw + b * kWireBlockBytes + lane * 16), lo, hi);
-      sum += wire_block_coded(width_of(hi - lo));
-    }
+    const WireCode c = wire_choose(v[j], lane, hist[wave]);
+    if (b < nblocks) sum += wire_block_coded(c.width, c.escapes);
   }
   if (lane == 0) part[wave] = sum;
   __syncthreads();
@@ -546,69 +607,90 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_encode_kernel
                                                                                   char* wire, uint64_t wire_capacity) {
   using namespace mo;
   constexpr int kWaves = kThreads / 64;
-  __shared__ uint32_t width[kWireTileBlocks], base_e[kWireTileBlocks], pre[kWireTileBlocks];
+  __shared__ uint32_t hist[kWaves][kWireBins];
+  __shared__ uint32_t head[kWireTileBlocks], pre[kWireTileBlocks];
   __shared__ __attribute__((aligned(16))) unsigned char plane[kWaves][kWireBlockVals];
+  __shared__ __attribute__((aligned(16))) unsigned char escs[kWaves][kWireBlockVals];
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t nblocks = wire_blocks(raw_bytes);
   const uint64_t tile = blockIdx.x;
   const __amdgpu_buffer_rsrc_t w = wire_rsrc(wire, wire_capacity);
   const uint32_t toff = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(kWireHeader + 4 * tile), 0, 0);
   uint4 v[8];
+  WireCode code[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint64_t b = tile * kWireTileBlocks + wave * 8 + j;
+    v[j] = b < nblocks ? ld16(raw + b * kWireBlockBytes + lane * 16) : make_uint4(0, 0, 0, 0);
+  }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint32_t bl = wave * 8 + j;
-    const uint64_t b = tile * kWireTileBlocks + bl;
-    uint32_t lo = 0, hi = 0;
-    if (b < nblocks) {
-      v[j] = ld16(raw + b * kWireBlockBytes + lane * 16);
-      block_range(v[j], lo, hi);
-    } else {
-      v[j] = make_uint4(0, 0, 0, 0);
-    }
-    if (lane == 0) {
-      width[bl] = b < nblocks ? width_of(hi - lo) : 0u;
-      base_e[bl] = b < nblocks ? lo : 0u;
-    }
+    code[j] = wire_choose(v[j], lane, hist[wave]);
+    if (lane == 0)
+      head[bl] = tile * kWireTileBlocks + bl < nblocks ? (code[j].base | (code[j].width << 8) | (code[j].escapes << 12))
+                                                       : 0u;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t acc = 0;
     for (uint32_t k = 0; k < kWireTileBlocks; ++k) {
       pre[k] = acc;
-      if (tile * kWireTileBlocks + k < nblocks) acc += wire_block_coded(width[k]);
+      if (tile * kWireTileBlocks + k < nblocks) acc += wire_block_coded((head[k] >> 8) & 0xfu, head[k] >> 12);
     }
   }
   if (threadIdx.x < kWireTileBlocks)
-    __builtin_amdgcn_raw_buffer_store_b16((unsigned short)((width[threadIdx.x] << 8) | base_e[threadIdx.x]), w,
-                                          (int)(toff + 2 * threadIdx.x), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(head[threadIdx.x], w, (int)(toff + 4 * threadIdx.x), 0, 0);
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint32_t bl = wave * 8 + j;
     const bool live = tile * kWireTileBlocks + bl < nblocks;
-    const uint32_t wd = width[bl], be = base_e[bl];
+    const WireCode c = code[j];
     const uint32_t dst = toff + kWireTileHeader + pre[bl];
-    if (live) {
-      uint32_t sm_lo = 0, sm_hi = 0;
-      uint64_t acc = 0;
+    uint32_t sm_lo = 0, sm_hi = 0, nmine = 0;
+    uint64_t acc = 0;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t word = word_of(v[j], k);
-        const uint32_t sm = ((word >> 8) & 0x80u) | (word & 0x7fu);
-        if (k < 4) sm_lo |= sm << (8 * k);
-        else sm_hi |= sm << (8 * (k - 4));
-        acc |= (uint64_t)(exponent_of(word) - be) << (k * wd);
-      }
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t word = word_of(v[j], k);
+      const uint32_t sm = ((word >> 8) & 0x80u) | (word & 0x7fu);
+      if (k < 4) sm_lo |= sm << (8 * k);
+      else sm_hi |= sm << (8 * (k - 4));
+      bool escape;
+      acc |= (uint64_t)wire_code_of(exponent_of(word), c, &escape) << (k * c.width);
+      nmine += escape ? 1u : 0u;
+    }
+    uint32_t eoff = wave_scan(nmine, lane) - nmine;  // this lane's first escape, in word order
+    if (live) {
       typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
       __builtin_amdgcn_raw_buffer_store_b64(u32x2{sm_lo, sm_hi}, w, (int)(dst + 8 * lane), 0, 0);
-      for (uint32_t i = 0; i < wd; ++i) plane[wave][lane * wd + i] = (unsigned char)(acc >> (8 * i));
+      for (uint32_t i = 0; i < c.width; ++i) plane[wave][lane * c.width + i] = (unsigned char)(acc >> (8 * i));
+      if (nmine) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          bool escape;
+          const uint32_t e = exponent_of(word_of(v[j], k));
+          (void)wire_code_of(e, c, &escape);
+          if (escape) escs[wave][min(eoff++, kWireBlockVals - 1)] = (unsigned char)e;
+        }
+      }
+      // zero padding after the escapes, up to the next 16 bytes
+      const uint32_t padded = (uint32_t)wire_align16(c.escapes);
+      for (uint32_t i = c.escapes + lane; i < padded; i += 64) escs[wave][i] = 0;
     }
     __syncthreads();
-    if (live && lane < 4 * wd) {
-      const mo_u32x4 chunk = *(const MO_LDS mo_u32x4*)(&plane[wave][16 * lane]);
-      __builtin_amdgcn_raw_buffer_store_b128(chunk, w, (int)(dst + kWireBlockVals + 16 * lane), 0, 0);
+    if (live) {
+      if (lane < 4 * c.width) {
+        const mo_u32x4 chunk = *(const MO_LDS mo_u32x4*)(&plane[wave][16 * lane]);
+        __builtin_amdgcn_raw_buffer_store_b128(chunk, w, (int)(dst + kWireBlockVals + 16 * lane), 0, 0);
+      }
+      if (16 * lane < c.escapes) {
+        const mo_u32x4 chunk = *(const MO_LDS mo_u32x4*)(&escs[wave][16 * lane]);
+        __builtin_amdgcn_raw_buffer_store_b128(chunk, w, (int)(dst + kWireBlockVals + 64 * c.width + 16 * lane), 0,
+                                               0);
+      }
     }
-    __syncthreads();  // the plane is rewritten by the next block
+    __syncthreads();  // the LDS planes are rewritten by the next block
   }
 }
 
@@ -619,24 +701,25 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_decode_kernel
                                                                                   uint64_t raw_bytes, char* raw) {
   using namespace mo;
   constexpr int kWaves = kThreads / 64;
-  __shared__ uint32_t width[kWireTileBlocks], base_e[kWireTileBlocks], pre[kWireTileBlocks];
+  __shared__ uint32_t head[kWireTileBlocks], pre[kWireTileBlocks];
   __shared__ __attribute__((aligned(16))) unsigned char plane[kWaves][kWireBlockVals];
+  __shared__ __attribute__((aligned(16))) unsigned char escs[kWaves][kWireBlockVals];
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t nblocks = wire_blocks(raw_bytes);
   const uint64_t tile = blockIdx.x;
   const __amdgpu_buffer_rsrc_t w = wire_rsrc(wire, wire_bytes);
   const uint32_t toff = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(kWireHeader + 4 * tile), 0, 0);
   if (threadIdx.x < kWireTileBlocks) {
-    const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(w, (int)(toff + 2 * threadIdx.x), 0, 0);
-    width[threadIdx.x] = min((h >> 8) & 0xfu, 8u);
-    base_e[threadIdx.x] = h & 0xffu;
+    const uint32_t h = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(toff + 4 * threadIdx.x), 0, 0);
+    // clamp what a damaged header could hold: width 0-8, escapes 0-512
+    head[threadIdx.x] = (h & 0xffu) | (min((h >> 8) & 0xfu, 8u) << 8) | (min(h >> 12, kWireBlockVals) << 12);
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t acc = 0;
     for (uint32_t k = 0; k < kWireTileBlocks; ++k) {
       pre[k] = acc;
-      acc += wire_block_coded(width[k]);
+      acc += wire_block_coded((head[k] >> 8) & 0xfu, head[k] >> 12);
     }
   }
   __syncthreads();
@@ -644,26 +727,38 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_decode_kernel
     const uint32_t bl = wave * 8 + j;
     const uint64_t b = tile * kWireTileBlocks + bl;
     const bool live = b < nblocks;
-    const uint32_t wd = width[bl], be = base_e[bl];
+    const WireCode c{(head[bl] >> 8) & 0xfu, head[bl] & 0xffu, head[bl] >> 12};
     const uint32_t src = toff + kWireTileHeader + pre[bl];
     typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
     u32x2 sm = {0, 0};
     if (live) {
       sm = __builtin_amdgcn_raw_buffer_load_b64(w, (int)(src + 8 * lane), 0, 0);
-      if (lane < 4 * wd)
+      if (lane < 4 * c.width)
         *(MO_LDS mo_u32x4*)(&plane[wave][16 * lane]) =
             __builtin_amdgcn_raw_buffer_load_b128(w, (int)(src + kWireBlockVals + 16 * lane), 0, 0);
+      if (16 * lane < c.escapes)
+        *(MO_LDS mo_u32x4*)(&escs[wave][16 * lane]) = __builtin_amdgcn_raw_buffer_load_b128(
+            w, (int)(src + kWireBlockVals + 64 * c.width + 16 * lane), 0, 0);
     }
     __syncthreads();
+    uint64_t acc = 0;
+    for (uint32_t i = 0; i < c.width; ++i) acc |= (uint64_t)plane[wave][lane * c.width + i] << (8 * i);
+    const uint32_t mask = (1u << c.width) - 1u;
+    const uint32_t esc_code = c.escapes && c.width && c.width < 8 ? mask : 0xffffffffu;
+    uint32_t nmine = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) nmine += ((uint32_t)(acc >> (k * c.width)) & mask) == esc_code ? 1u : 0u;
+    uint32_t eoff = wave_scan(nmine, lane) - nmine;
     if (live) {
-      uint64_t acc = 0;
-      for (uint32_t i = 0; i < wd; ++i) acc |= (uint64_t)plane[wave][lane * wd + i] << (8 * i);
-      const uint32_t mask = (1u << wd) - 1u;
       uint32_t out[4];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const uint32_t s = ((k < 4 ? sm[0] : sm[1]) >> (8 * (k & 3))) & 0xffu;
-        const uint32_t e = (be + ((uint32_t)(acc >> (k * wd)) & mask)) & 0xffu;
+        const uint32_t code = (uint32_t)(acc >> (k * c.width)) & mask;
+        uint32_t e;
+        if (c.width == 8) e = code;
+        else if (code == esc_code) e = escs[wave][min(eoff++, kWireBlockVals - 1)];
+        else e = (c.base + code) & 0xffu;
         const uint32_t word = ((s & 0x80u) << 8) | (e << 7) | (s & 0x7fu);
         if (k & 1) out[k >> 1] |= word << 16;
         else out[k >> 1] = word;

@@ -1,13 +1,18 @@
-// Wire format of a coded staging segment: lossless exponent-plane coding of 16-bit words,
-// shared by the device kernels (mo_device.hip) and the host (mo_engine.cpp, mo_launch.cpp).
+// Wire format of a coded staging segment: lossless coding of the exponent fields of 16-bit
+// words, shared by the device kernels (mo_device.hip) and the host (mo_engine.cpp,
+// mo_launch.cpp).
 //
-// A segment's payload is a byte string whose pieces start 16-byte aligned, so the bfloat16
+// A segment's payload is a byte string whose pieces start 256-byte aligned, so the bfloat16
 // values it mostly holds sit on the 2-byte grid. The coder reads it as 16-bit words w =
-// s(1) e(8) m(7): it keeps each word's sign and mantissa as one byte, and replaces the 8-bit
-// exponent field by its offset from the smallest exponent of the word's block, in as few bits
-// as the block's exponent range needs (0 to 8). Words that are not bfloat16 (float32 low
-// halves, integers) code at width 8 and cost 1/512 more than raw. Decoding restores every
-// word bit for bit, NaN payloads included.
+// s(1) e(8) m(7): it keeps each word's sign and mantissa as one byte, and codes the 8-bit
+// exponent field per 512-word block in one of three ways, whichever is smallest:
+//   width 0       every exponent of the block equals `base`;
+//   width k 1..7  a k-bit code per word: code c < 2^k - 1 (or any c when the block has no
+//                 escapes) stands for exponent base + c; code 2^k - 1 marks an escape, whose
+//                 8-bit exponent follows in the block's escape bytes, in word order;
+//   width 8       the exponent bytes as they are.
+// Words that are not bfloat16 (float32 low halves, integers, random bits) take width 8 and
+// cost 1/256 more than raw. Decoding restores every word bit for bit, NaN payloads included.
 //
 // Layout (all offsets in bytes from the start of the coded stream, little-endian):
 //   [0, 16)            header: u64 total (coded bytes, header included), u32 raw bytes,
@@ -15,15 +20,15 @@
 //   [16, 16 + 4 T)     u32 offset of each tile's data
 //   data_start         the raw tail (raw bytes % kWireBlockBytes bytes, copied as is)
 //   tiles_start        the tiles, each 16-byte aligned:
-//                        kWireTileBlocks u16 block headers (width << 8 | base exponent;
+//                        kWireTileBlocks u32 block headers (base | width << 8 | escapes << 12;
 //                        zero for blocks past the end), then each block's data:
 //                          kWireBlockVals sign-mantissa bytes (byte i: word i's bit 15 as
 //                          bit 7, its bits 0-6 as bits 0-6),
-//                          kWireBlockVals exponent offsets of `width` bits, 64 * width bytes:
-//                          lane l of the coding wave packs words 8l..8l+7 into `width` bytes
-//                          at l * width, word 8l+k in bits [k * width, (k + 1) * width) of
-//                          that little-endian field.
-// A block of 512 words (1 KiB raw) codes to 512 + 64 * width bytes; a tile holds 32 blocks.
+//                          64 * width code bytes: lane l of the coding wave packs words
+//                          8l..8l+7 into `width` bytes at l * width, word 8l+k in bits
+//                          [k * width, (k + 1) * width) of that little-endian field,
+//                          the escapes' exponent bytes, zero-padded to a multiple of 16.
+// A tile holds 32 blocks of 512 words (1 KiB raw each).
 // Plain constexpr code (callable from device code too), no HIP headers, like mo_kdesc.h.
 #pragma once
 
@@ -36,8 +41,9 @@ constexpr uint32_t kWireBlockBytes = 2 * kWireBlockVals;              // raw byt
 constexpr uint32_t kWireTileBlocks = 32;                              // blocks per tile (one workgroup)
 constexpr uint32_t kWireTileRaw = kWireBlockBytes * kWireTileBlocks;  // 32 KiB raw per tile
 constexpr uint32_t kWireHeader = 16;
-constexpr uint32_t kWireTileHeader = 2 * kWireTileBlocks;
+constexpr uint32_t kWireTileHeader = 4 * kWireTileBlocks;
 constexpr uint32_t kWireScanThreads = 1024;  // the one workgroup of the offset scan
+constexpr uint32_t kWireBins = 32;           // exponent offsets 0..30 from the block minimum; 31 = farther
 
 constexpr uint64_t wire_align16(uint64_t x) { return (x + 15) & ~uint64_t(15); }
 constexpr uint64_t wire_blocks(uint64_t raw) { return raw / kWireBlockBytes; }
@@ -48,10 +54,13 @@ constexpr uint64_t wire_data_start(uint64_t raw) { return wire_align16(kWireHead
 constexpr uint64_t wire_tiles_start(uint64_t raw) {
   return wire_align16(wire_data_start(raw) + raw % kWireBlockBytes);
 }
-constexpr uint32_t wire_block_coded(uint32_t width) { return kWireBlockVals + 64 * width; }
-// Largest coded size of `raw` bytes (every block at width 8).
+// Coded bytes of one block: sign-mantissa bytes, codes, padded escape bytes.
+constexpr uint32_t wire_block_coded(uint32_t width, uint32_t escapes) {
+  return kWireBlockVals + 64 * width + (uint32_t)wire_align16(escapes);
+}
+// Largest coded size of `raw` bytes (every block at width 8, which the coder never exceeds).
 constexpr uint64_t wire_capacity(uint64_t raw) {
-  return wire_tiles_start(raw) + wire_tiles(raw) * (kWireTileHeader + (uint64_t)kWireTileBlocks * wire_block_coded(8));
+  return wire_tiles_start(raw) + wire_tiles(raw) * (kWireTileHeader + (uint64_t)kWireTileBlocks * wire_block_coded(8, 0));
 }
 
 }  // namespace mo

@@ -40,13 +40,33 @@ def test_special_values_and_widths() -> None:
     raw += nan_words + bytes(range(7))
     stream, _ = wm.encode(raw)
     assert wm.decode(stream, len(raw)) == raw
-    # width 0 block: 512 sign-mantissa bytes only; Gaussian blocks code to about 0.75 of raw
+    # width 0 block: 512 sign-mantissa bytes only; Gaussian blocks code to about 0.7 of raw
     g = _bf16_bytes(gauss)
     gs, _ = wm.encode(g)
-    assert len(gs) < 0.8 * len(g)
+    assert len(gs) < 0.75 * len(g)
     flat = _bf16_bytes(torch.full((32 * 512,), 1.5))
     fs, _ = wm.encode(flat)
     assert len(fs) == wm.tiles_start(len(flat)) + wm.TILE_HEADER + 32 * 512
+
+
+def test_choice_rule_closed_forms() -> None:
+    """The block coding the format fixes, on blocks whose best coding is known by hand."""
+
+    e = np.full(512, 120, np.uint32)
+    assert wm.choose(e) == (0, 120, 0)                       # one exponent
+    e[::2] = 121
+    assert wm.choose(e) == (1, 120, 0)                       # two values, no escapes: 1 bit
+    e[:4] = 200                                              # four far outliers
+    # 1-bit window {120} + 258 escapes: 512 + 64 + 272 bytes; 2-bit window {120, 121, 122} + 4
+    # escapes: 512 + 128 + 16 = 656 bytes, the smallest; width 8: 1024 bytes
+    assert wm.block_coded(2, 4) < min(wm.block_coded(1, 258), wm.block_coded(8, 0))
+    assert wm.choose(e) == (2, 120, 4)
+    e[:4] = 123                                              # now all inside 2 bits, no escapes:
+    assert wm.choose(e) == (2, 120, 0)                       # 512 + 128 bytes
+    e[:4] = 124                                              # one past it: escapes (656 bytes) beat
+    assert wm.choose(e) == (2, 120, 4)                       # 3 bits without them (704 bytes)
+    rnd = np.random.default_rng(0).integers(0, 256, 512).astype(np.uint32)
+    assert wm.choose(rnd)[0] == 8                            # random exponents: raw bytes
 
 
 def test_planted_mistakes_are_caught() -> None:
@@ -61,9 +81,9 @@ def test_planted_mistakes_are_caught() -> None:
     s[t0 + wm.TILE_HEADER] ^= 0x80
     assert wm.decode(bytes(s), len(raw)) != raw
     s = bytearray(stream)
-    w = int(np.frombuffer(stream[t0:t0 + 2], "<u2")[0]) >> 8
+    w = (int(np.frombuffer(stream[t0:t0 + 4], "<u4")[0]) >> 8) & 0xF
     assert w > 0
-    s[t0 + wm.TILE_HEADER + 512] ^= 0x01  # lowest bit of word 0's exponent offset
+    s[t0 + wm.TILE_HEADER + 512] ^= 0x01  # lowest bit of word 0's exponent code
     assert wm.decode(bytes(s), len(raw)) != raw
 
 
