@@ -528,7 +528,8 @@ __device__ __forceinline__ uint32_t wire_code_of(uint32_t e, const WireCode& c, 
 
 }  // namespace mo
 
-// Pass 1: the coded size of each tile, written into the stream's tile table.
+// Pass 1: each block's coding (its header, into the working space after the largest stream)
+// and the coded size of each tile, into the stream's tile table.
 extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_sizes_kernel(const char* raw, uint64_t raw_bytes,
                                                                                  char* wire, uint64_t wire_capacity) {
   using namespace mo;
@@ -538,6 +539,8 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_sizes_kernel(
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t nblocks = wire_blocks(raw_bytes);
   const uint64_t tile = blockIdx.x;
+  const __amdgpu_buffer_rsrc_t w = wire_rsrc(wire, wire_capacity);
+  const uint64_t scratch = wire_scratch_offset(raw_bytes);
   uint4 v[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -548,15 +551,18 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_sizes_kernel(
   for (int j = 0; j < 8; ++j) {
     const uint64_t b = tile * kWireTileBlocks + wave * 8 + j;
     const WireCode c = wire_choose(v[j], lane, hist[wave]);
-    if (b < nblocks) sum += wire_block_coded(c.width, c.escapes);
+    if (b < nblocks) {
+      sum += wire_block_coded(c.width, c.escapes);
+      if (lane == 0)
+        __builtin_amdgcn_raw_buffer_store_b32(c.base | (c.width << 8) | (c.escapes << 12), w, (int)(scratch + 4 * b), 0,
+                                              0);
+    }
   }
   if (lane == 0) part[wave] = sum;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const __amdgpu_buffer_rsrc_t w = wire_rsrc(wire, wire_capacity);
+  if (threadIdx.x == 0)
     __builtin_amdgcn_raw_buffer_store_b32(kWireTileHeader + part[0] + part[1] + part[2] + part[3], w,
                                           (int)(kWireHeader + 4 * tile), 0, 0);
-  }
 }
 
 // Pass 2 (one workgroup of kWireScanThreads): tile sizes -> tile offsets (exclusive scan from
@@ -607,7 +613,6 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_encode_kernel
                                                                                   char* wire, uint64_t wire_capacity) {
   using namespace mo;
   constexpr int kWaves = kThreads / 64;
-  __shared__ uint32_t hist[kWaves][kWireBins];
   __shared__ uint32_t head[kWireTileBlocks], pre[kWireTileBlocks];
   __shared__ __attribute__((aligned(16))) unsigned char plane[kWaves][kWireBlockVals];
   __shared__ __attribute__((aligned(16))) unsigned char escs[kWaves][kWireBlockVals];
@@ -616,20 +621,17 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_encode_kernel
   const uint64_t tile = blockIdx.x;
   const __amdgpu_buffer_rsrc_t w = wire_rsrc(wire, wire_capacity);
   const uint32_t toff = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(kWireHeader + 4 * tile), 0, 0);
+  const uint64_t scratch = wire_scratch_offset(raw_bytes);
   uint4 v[8];
-  WireCode code[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint64_t b = tile * kWireTileBlocks + wave * 8 + j;
     v[j] = b < nblocks ? ld16(raw + b * kWireBlockBytes + lane * 16) : make_uint4(0, 0, 0, 0);
   }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t bl = wave * 8 + j;
-    code[j] = wire_choose(v[j], lane, hist[wave]);
-    if (lane == 0)
-      head[bl] = tile * kWireTileBlocks + bl < nblocks ? (code[j].base | (code[j].width << 8) | (code[j].escapes << 12))
-                                                       : 0u;
+  if (threadIdx.x < kWireTileBlocks) {
+    // the block codings the sizing pass chose (zero past the end)
+    const uint64_t b = tile * kWireTileBlocks + threadIdx.x;
+    head[threadIdx.x] = b < nblocks ? __builtin_amdgcn_raw_buffer_load_b32(w, (int)(scratch + 4 * b), 0, 0) : 0u;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -646,7 +648,7 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_encode_kernel
   for (int j = 0; j < 8; ++j) {
     const uint32_t bl = wave * 8 + j;
     const bool live = tile * kWireTileBlocks + bl < nblocks;
-    const WireCode c = code[j];
+    const WireCode c{(head[bl] >> 8) & 0xfu, head[bl] & 0xffu, head[bl] >> 12};
     const uint32_t dst = toff + kWireTileHeader + pre[bl];
     uint32_t sm_lo = 0, sm_hi = 0, nmine = 0;
     uint64_t acc = 0;

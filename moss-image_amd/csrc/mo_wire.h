@@ -7,7 +7,7 @@
 // s(1) e(8) m(7): it keeps each word's sign and mantissa as one byte, and codes the 8-bit
 // exponent field per 512-word block in one of three ways, whichever is smallest:
 //   width 0       every exponent of the block equals `base`;
-//   width k 1..7  a k-bit code per word: code c < 2^k - 1 (or any c when the block has no
+//   width k 1..7  (the coder uses 1..5) a k-bit code per word: code c < 2^k - 1 (or any c when the block has no
 //                 escapes) stands for exponent base + c; code 2^k - 1 marks an escape, whose
 //                 8-bit exponent follows in the block's escape bytes, in word order;
 //   width 8       the exponent bytes as they are.
@@ -28,7 +28,9 @@
 //                          8l..8l+7 into `width` bytes at l * width, word 8l+k in bits
 //                          [k * width, (k + 1) * width) of that little-endian field,
 //                          the escapes' exponent bytes, zero-padded to a multiple of 16.
-// A tile holds 32 blocks of 512 words (1 KiB raw each).
+// A tile holds 32 blocks of 512 words (1 KiB raw each). The wire buffer a coder writes into
+// also holds, after the largest stream, its working space: each block's header as the sizing
+// pass chose it (wire_capacity covers both).
 // Plain constexpr code (callable from device code too), no HIP headers, like mo_kdesc.h.
 #pragma once
 
@@ -59,8 +61,13 @@ constexpr uint32_t wire_block_coded(uint32_t width, uint32_t escapes) {
   return kWireBlockVals + 64 * width + (uint32_t)wire_align16(escapes);
 }
 // Largest coded size of `raw` bytes (every block at width 8, which the coder never exceeds).
-constexpr uint64_t wire_capacity(uint64_t raw) {
+constexpr uint64_t wire_max_coded(uint64_t raw) {
   return wire_tiles_start(raw) + wire_tiles(raw) * (kWireTileHeader + (uint64_t)kWireTileBlocks * wire_block_coded(8, 0));
 }
+// The coder's working space after the largest stream: each block's header (u32), chosen once
+// by the sizing pass and read by the coding pass.
+constexpr uint64_t wire_scratch_offset(uint64_t raw) { return wire_align16(wire_max_coded(raw)); }
+// The wire buffer to provide for coding `raw` bytes: the largest stream plus the working space.
+constexpr uint64_t wire_capacity(uint64_t raw) { return wire_scratch_offset(raw) + 4 * wire_blocks(raw); }
 
 }  // namespace mo

@@ -20,7 +20,7 @@ def test_round_trip_random_bits(raw_bytes) -> None:
     rng = np.random.default_rng(raw_bytes)
     raw = rng.integers(0, 256, raw_bytes, dtype=np.uint8).tobytes()
     stream, defined = wm.encode(raw)
-    assert len(stream) <= wm.capacity(raw_bytes)
+    assert len(stream) <= wm.max_coded(raw_bytes) <= wm.capacity(raw_bytes)
     assert int(np.frombuffer(stream[:8], "<u8")[0]) == len(stream)
     assert wm.decode(stream, raw_bytes) == raw
 

@@ -41,8 +41,15 @@ def block_coded(width: int, escapes: int) -> int:
     return BLOCK_VALS + 64 * width + _align16(escapes)
 
 
-def capacity(raw_bytes: int) -> int:
+def max_coded(raw_bytes: int) -> int:
     return tiles_start(raw_bytes) + tiles_of(raw_bytes) * (TILE_HEADER + TILE_BLOCKS * block_coded(8, 0))
+
+
+def capacity(raw_bytes: int) -> int:
+    """The wire buffer the coder needs: the largest stream, then each block's header (u32) as
+    working space."""
+
+    return _align16(max_coded(raw_bytes)) + 4 * (raw_bytes // BLOCK_BYTES)
 
 
 def choose(e: np.ndarray) -> tuple[int, int, int]:
