@@ -467,12 +467,19 @@ struct WireCode {
   uint32_t width, base, escapes;
 };
 
-// The coding of one block (mo_wire.h): called by every wave of the workgroup the same number of
-// times (it synchronizes the workgroup), `hist` is the wave's 32 bins of LDS. Among width 8,
-// and widths 1-5 with a window of offsets s.. from the block's smallest exponent (no escapes
-// when every exponent fits 2^k values, else 2^k - 1 values and escapes), it takes the smallest
-// coded size, ties to the smaller width, then the smaller s.
-__device__ __forceinline__ WireCode wire_choose(const uint4& v, uint32_t lane, uint32_t* hist) {
+// Orders the wave's own LDS accesses (a wave's LDS operations execute in order; this keeps the
+// compiler from moving them across).
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// The coding of one block (mo_wire.h), by one wave; `hist` and `pref` are the wave's own 32
+// words of LDS each. Among width 8, and widths 1-5 with a window of offsets s.. from the
+// block's smallest exponent (no escapes when every exponent fits 2^k values, else 2^k - 1
+// values and escapes), it takes the smallest coded size, ties to the smaller width, then the
+// smaller s.
+__device__ __forceinline__ WireCode wire_choose(const uint4& v, uint32_t lane, uint32_t* hist, uint32_t* pref) {
   uint32_t lo = 255, hi = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -480,32 +487,35 @@ __device__ __forceinline__ WireCode wire_choose(const uint4& v, uint32_t lane, u
     lo = min(lo, e);
     hi = max(hi, e);
   }
-  lo = wave_min(lo);
-  hi = wave_max(hi);
+  const uint32_t span = wave_max(((255u - lo) << 8) | hi);  // one reduction for both ends
+  lo = 255u - (span >> 8);
+  hi = span & 0xffu;
+  if (hi == lo) return WireCode{0, lo, 0};
   if (lane < kWireBins) hist[lane] = 0;
-  __syncthreads();
+  wave_lds_fence();
 #pragma unroll
   for (int j = 0; j < 8; ++j) atomicAdd(&hist[min(exponent_of(word_of(v, j)) - lo, kWireBins - 1)], 1u);
-  __syncthreads();
+  wave_lds_fence();
   const uint32_t h = lane < kWireBins ? hist[lane] : 0u;
   const uint32_t p = wave_scan(h, lane) - h;  // lane i < 32: words in bins 0..i-1
+  if (lane < kWireBins) pref[lane] = p;
+  wave_lds_fence();
   uint32_t best = (wire_block_coded(8, 0) << 16) | (8u << 8);
   uint32_t nesc[6] = {0, 0, 0, 0, 0, 0};
 #pragma unroll
   for (uint32_t k = 1; k <= 5; ++k) {
     const uint32_t w = 1u << k;
     const uint32_t s = lane;
-    const uint32_t pa = (uint32_t)__shfl((int)p, (int)min(s + w, kWireBins - 1), 64);
-    const uint32_t pb = (uint32_t)__shfl((int)p, (int)min(s + w - 1, kWireBins - 1), 64);
     uint32_t esc = 0xffffu;
-    if (s + w <= kWireBins - 1 && pa - p == kWireBlockVals) esc = 0;
-    else if (s + w - 1 <= kWireBins - 1) esc = kWireBlockVals - (pb - p);
+    if (s + w - 1 <= kWireBins - 1) {
+      if (s + w <= kWireBins - 1 && pref[s + w] - p == kWireBlockVals) esc = 0;
+      else esc = kWireBlockVals - (pref[s + w - 1] - p);
+    }
     nesc[k] = esc;
     if (esc != 0xffffu) best = min(best, (wire_block_coded(k, esc) << 16) | (k << 8) | s);
   }
   best = wave_min(best);
   const uint32_t width = (best >> 8) & 0xffu, s = best & 0xffu;
-  if (hi == lo) return WireCode{0, lo, 0};
   if (width == 8) return WireCode{8, 0, 0};
   uint32_t mine = 0;
 #pragma unroll
@@ -534,7 +544,7 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_sizes_kernel(
                                                                                  char* wire, uint64_t wire_capacity) {
   using namespace mo;
   constexpr int kWaves = kThreads / 64;
-  __shared__ uint32_t hist[kWaves][kWireBins];
+  __shared__ uint32_t hist[kWaves][kWireBins], pref[kWaves][kWireBins];
   __shared__ uint32_t part[kWaves];
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t nblocks = wire_blocks(raw_bytes);
@@ -550,7 +560,7 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_sizes_kernel(
   uint32_t sum = 0;
   for (int j = 0; j < 8; ++j) {
     const uint64_t b = tile * kWireTileBlocks + wave * 8 + j;
-    const WireCode c = wire_choose(v[j], lane, hist[wave]);
+    const WireCode c = wire_choose(v[j], lane, hist[wave], pref[wave]);
     if (b < nblocks) {
       sum += wire_block_coded(c.width, c.escapes);
       if (lane == 0)
