@@ -487,10 +487,8 @@ __device__ __forceinline__ WireCode wire_choose(const uint4& v, uint32_t lane, u
     lo = min(lo, e);
     hi = max(hi, e);
   }
-  const uint32_t span = wave_max(((255u - lo) << 8) | hi);  // one reduction for both ends
-  lo = 255u - (span >> 8);
-  hi = span & 0xffu;
-  if (hi == lo) return WireCode{0, lo, 0};
+  lo = wave_min(lo);
+  if (__all(hi == lo)) return WireCode{0, lo, 0};  // every exponent of the block equals the smallest
   if (lane < kWireBins) hist[lane] = 0;
   wave_lds_fence();
 #pragma unroll

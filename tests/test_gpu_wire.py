@@ -5,7 +5,8 @@ Each case codes a device buffer, compares the coded stream byte for byte with th
 kernel wrote to pinned host memory, decodes into a buffer with sentinel guard bytes on both
 sides, and compares the result bitwise with the input. Inputs cover every width (random bits,
 one exponent, Gaussian activations, all exponent classes with NaN payloads, infinities,
-signed zeros and subnormals), partial tiles and raw tails, and a 50 MiB Gaussian buffer.
+signed zeros and subnormals, exponents that differ between the 8-word groups each lane of the
+coding wave reads), partial tiles and raw tails, and a 50 MiB Gaussian buffer.
 """
 
 from __future__ import annotations
@@ -33,6 +34,25 @@ def _content(kind: str, nbytes: int, seed: int) -> torch.Tensor:
         v = torch.randn(n, generator=g).to(torch.bfloat16)
     elif kind == "flat":
         v = torch.full((n,), 3.25, dtype=torch.bfloat16)
+    elif kind == "lanes":  # exponents that differ between 8-word lane groups (the coder's per-lane spans)
+        blocks = (n + 511) // 512
+        gen = np.random.default_rng(seed)
+        e = np.repeat(120 + gen.integers(0, 4, (blocks, 64)), 8, axis=1)
+        for b in range(blocks):
+            lane = b // 4 % 64
+            if b % 4 == 0:  # one lane holds the block's smallest exponent in all its words
+                e[b, 8 * lane:8 * lane + 8] = 119
+            elif b % 4 == 1:  # one lane below an otherwise constant block
+                e[b] = 125
+                e[b, 8 * lane:8 * lane + 8] = 124
+            elif b % 4 == 2:  # one exponent per lane, 64 apart from first to last
+                e[b] = np.repeat(90 + np.arange(64), 8)
+            else:  # one lane of zeros in a block near 1.0
+                e[b] = 127
+                e[b, 8 * lane:8 * lane + 8] = 0
+        sm = gen.integers(0, 1 << 16, e.shape) & 0x807F
+        words = (sm | (e << 7)).reshape(-1)[:n]
+        v = torch.from_numpy(words.astype(np.uint16).view(np.int16).copy()).view(torch.bfloat16)
     else:  # special: every exponent class, NaN payloads, infinities, zeros, subnormals
         words = torch.randint(0, 1 << 16, (n,), dtype=torch.int32, generator=g)
         words[::7] = 0x7F80 | (words[::7] & 0x807F)  # inf / NaN with random payloads
@@ -44,7 +64,7 @@ def _content(kind: str, nbytes: int, seed: int) -> torch.Tensor:
 CASES = [
     ("random", 16), ("random", 1024), ("random", 1040), ("gauss", 32 * 1024), ("gauss", 32 * 1024 + 1024 + 16),
     ("flat", 64 * 1024), ("special", 3 * 32 * 1024 + 5 * 1024 + 496), ("gauss", (1 << 20) + 48),
-    ("random", 40 * 1024 + 3), ("gauss", 0),
+    ("random", 40 * 1024 + 3), ("gauss", 0), ("lanes", 64 * 1024 * 4 + 2 * 1024),
 ]
 
 
