@@ -4,8 +4,9 @@ The activation-offload engine is op-agnostic, but what it moves (which tensors, 
 order, with which layouts and dtypes) is fixed by the model. This module restates the
 reference model's topology and op sequence so that the hooks receive the same saves as they
 do under ``training/model.py``: RMSNorm (:154-172), SiTU-GLU (:27-38), half-rotation RoPE
-(:41-56, :94-151), joint attention (:59-91) through SDPA (``performance.py:124-160``, varlen
-mask path ``:163-225``), the text adapter (:175-242), the single-stream joint block with
+(:41-56, :94-151), joint attention (:59-91) through SDPA (``performance.py:124-160``; packed
+sequences ``:163-225``, one SDPA call per sequence on a HIP device, the boolean-mask fallback
+on the CPU), the text adapter (:175-242), the single-stream joint block with
 shared 6-way modulation (:245-314), the time conditions (:546-567), the per-sample and packed
 forwards with the offload context around the traversal (:439-544), and selective
 checkpointing (:672-710, :780-789). LoRA follows ``training/lora.py:21-86`` and the int8
@@ -50,11 +51,21 @@ def rotate_rope(tokens: torch.Tensor, rope: torch.Tensor) -> torch.Tensor:
 
 def _attention_core(query, key, value, cu_seqlens):
     # performance.py:139-143 (normalised q/k follow the value dtype) and :163-225 (packed
-    # sequences isolated by a block-diagonal boolean mask).
+    # sequences). On a HIP device the packed sequences are attended one by one, which is what
+    # the reference's varlen kernel computes (performance.py:195-209, flash_attn_varlen_func):
+    # PyTorch-ROCm's SDPA with the block-diagonal boolean mask is not repeatable at the text
+    # adapter's 1600 packed tokens (its output and q/k gradients change once freed device
+    # memory holds other data), so a step without offloading would not reproduce itself. On the
+    # CPU the packed sequences are isolated by the reference's block-diagonal boolean mask
+    # (:215-225), its portable fallback.
     query = query.to(value.dtype)
     key = key.to(value.dtype)
     if cu_seqlens is None:
         return F.scaled_dot_product_attention(query, key, value)
+    if value.device.type == "cuda":
+        lengths = (cu_seqlens[1:] - cu_seqlens[:-1]).tolist()
+        parts = zip(query.split(lengths, 2), key.split(lengths, 2), value.split(lengths, 2))
+        return torch.cat([F.scaled_dot_product_attention(q, k, v) for q, k, v in parts], 2)
     lengths = cu_seqlens[1:] - cu_seqlens[:-1]
     labels = torch.repeat_interleave(
         torch.arange(lengths.numel(), device=value.device), lengths.to(device=value.device, dtype=torch.long)
