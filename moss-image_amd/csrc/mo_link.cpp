@@ -124,8 +124,9 @@ struct Job {
   void* dst = nullptr;
   const void* src = nullptr;
   EventRef wait;  // issue after this HIP event completed
-  SdmaRef after;  // and after this copy completed (the D2H that filled an H2D's source)
-  SdmaRef prev;   // and after this earlier copy through the same gate (GateOrder)
+  // and after these copies completed: the D2H that filled an H2D's source, and the earlier
+  // copies through the same gate that this one must follow (GateOrder)
+  std::vector<SdmaRef> deps;
   // sized copy: the byte count is read from here at issue, clamped to [1, max_bytes]
   const volatile uint64_t* size = nullptr;
   uint64_t max_bytes = 0;
@@ -258,7 +259,7 @@ class SdmaLink : public Link {
     job.dst = dst;
     job.src = src;
     job.wait = std::move(ev);
-    job.prev = gates_[gate].order.on_read(copy);
+    add_dep(job, gates_[gate].order.on_read(copy, copy_done));
     job.size = size;
     job.max_bytes = bytes;
     enqueue(std::move(job));
@@ -277,8 +278,8 @@ class SdmaLink : public Link {
     job.dst = dst;
     job.src = src;
     job.wait = gates_[gate].consumed;
-    job.after = std::dynamic_pointer_cast<SdmaCopy>(after);
-    job.prev = gates_[gate].order.on_write(copy);
+    add_dep(job, std::dynamic_pointer_cast<SdmaCopy>(after));
+    for (const SdmaRef& dep : gates_[gate].order.on_write(copy)) add_dep(job, dep);
     job.size = size;
     job.max_bytes = bytes;
     enqueue(std::move(job));
@@ -311,27 +312,37 @@ class SdmaLink : public Link {
     job.dst = dst;
     job.src = src;
     job.wait = gates_[gate].consumed;
-    job.prev = gates_[gate].order.on_read(copy);
+    add_dep(job, gates_[gate].order.on_read(copy, copy_done));
     enqueue(std::move(job));
     d2h_bytes_ += bytes;
     *out = copy;
     return 0;
   }
 
-  // Host-side: return once the gate's last copy finished. The caller enqueues the dependent
-  // GPU work afterwards, so stream order does the rest.
+  // Host-side: return once every copy that may still access the gate's slot finished (its
+  // last write and all reads since: two D2H copies of one staging slot may run on different
+  // engines and finish out of order). The caller enqueues the dependent GPU work afterwards,
+  // so stream order does the rest.
   int wait(int gate, hipStream_t compute) override {
     (void)compute;
-    const SdmaRef& c = gates_[gate].order.last;
-    if (!c || c->done()) return 0;
+    GateOrder<SdmaRef>& order = gates_[gate].order;
+    bool blocked = false, failed = false;
     const int64_t t0 = now_ns();
-    while (!c->done()) {
-      if (now_ns() - t0 > kWaitLimitNs) return MO_E_STATE;
-      short_sleep();
+    for (const SdmaRef& c : order.outstanding()) {
+      if (!c) continue;
+      while (!c->done()) {
+        if (now_ns() - t0 > kWaitLimitNs) return MO_E_STATE;
+        blocked = true;
+        short_sleep();
+      }
+      failed = failed || c->failed();
     }
-    host_blocks_++;
-    host_block_ns_ += (uint64_t)(now_ns() - t0);
-    return c->failed() ? MO_E_STATE : 0;
+    order.prune(copy_done);
+    if (blocked) {
+      host_blocks_++;
+      host_block_ns_ += (uint64_t)(now_ns() - t0);
+    }
+    return failed ? MO_E_STATE : 0;
   }
 
   int consumed(int gate, hipStream_t compute) override {
@@ -426,6 +437,11 @@ class SdmaLink : public Link {
   // 45.5 ms).
   static constexpr uint64_t kSplitBytes = 2ull << 20;
   std::atomic<int>& h2d_inflight() { return g_h2d_inflight[device_ < kMaxDevices && device_ >= 0 ? device_ : 0]; }
+
+  static bool copy_done(const SdmaRef& c) { return !c || c->done(); }
+  static void add_dep(Job& job, const SdmaRef& dep) {
+    if (dep) job.deps.push_back(dep);
+  }
 
   SdmaRef make_copy(bool to_host, uint64_t bytes) {
     auto c = std::make_shared<SdmaCopy>();
@@ -525,11 +541,11 @@ class SdmaLink : public Link {
         return true;
       }
     }
-    for (SdmaRef* dep : {&job.after, &job.prev}) {
-      if (!*dep) continue;
-      if (!(*dep)->done()) return false;
-      const bool bad = (*dep)->failed();
-      dep->reset();
+    while (!job.deps.empty()) {
+      const SdmaRef& dep = job.deps.back();
+      if (!dep->done()) return false;
+      const bool bad = dep->failed();
+      job.deps.pop_back();
       if (bad) {
         finish(job.copy, true);
         return true;
@@ -800,7 +816,7 @@ class StreamLink : public Link {
     const int parts = n_d2h_ == 2 && bytes >= kSplitBytes && !h2d_pending() ? 2 : 1;
     StreamRef copy;
     if (int rc = make_copy(parts, &copy)) return rc;
-    const StreamRef dep = std::static_pointer_cast<StreamCopy>(gates_[gate].order.on_read(copy));
+    const StreamRef dep = std::static_pointer_cast<StreamCopy>(gates_[gate].order.on_read(copy, copy_done));
     const uint64_t half = parts == 2 ? bytes / 2 / 4096 * 4096 : bytes;
     for (int k = 0; k < parts; ++k) {
       hipStream_t s = d2h_[k];
@@ -821,7 +837,8 @@ class StreamLink : public Link {
     hipError_t e;
     if (g.consumed && (e = hipStreamWaitEvent(h2d_, g.consumed, 0)) != hipSuccess) return (int)e;
     if (int rc = wait_for(h2d_, std::static_pointer_cast<StreamCopy>(after))) return rc;
-    if (int rc = wait_for(h2d_, std::static_pointer_cast<StreamCopy>(g.order.on_write(copy)))) return rc;
+    for (const CopyRef& dep : g.order.on_write(copy))
+      if (int rc = wait_for(h2d_, std::static_pointer_cast<StreamCopy>(dep))) return rc;
     if (int rc = move(h2d_, (char*)dst, host(src), bytes, false, copy->ev[0])) return rc;
     st_.h2d_bytes += bytes;
     last_h2d_ = copy;
@@ -835,7 +852,7 @@ class StreamLink : public Link {
     Gate& g = gates_[gate];
     hipError_t e;
     if (g.consumed && (e = hipStreamWaitEvent(d2h_[0], g.consumed, 0)) != hipSuccess) return (int)e;
-    if (int rc = wait_for(d2h_[0], std::static_pointer_cast<StreamCopy>(g.order.on_read(copy)))) return rc;
+    if (int rc = wait_for(d2h_[0], std::static_pointer_cast<StreamCopy>(g.order.on_read(copy, copy_done)))) return rc;
     if (int rc = move(d2h_[0], host(dst), (const char*)src, bytes, true, copy->ev[0])) return rc;
     st_.d2h_bytes += bytes;
     *out = copy;
@@ -848,9 +865,13 @@ class StreamLink : public Link {
     return c && !c->done();
   }
 
-  // The compute stream waits for the gate's last copy: GPU-side, the host does not block.
+  // The compute stream waits for every copy that may still access the gate's slot (its last
+  // write and all reads since, which may run on both D2H streams): GPU-side, the host does not
+  // block.
   int wait(int gate, hipStream_t compute) override {
-    return wait_for(compute, std::static_pointer_cast<StreamCopy>(gates_[gate].order.last));
+    for (const CopyRef& c : gates_[gate].order.outstanding())
+      if (int rc = wait_for(compute, std::static_pointer_cast<StreamCopy>(c))) return rc;
+    return 0;
   }
 
   int consumed(int gate, hipStream_t compute) override {
@@ -926,6 +947,8 @@ class StreamLink : public Link {
     *out = std::move(c);
     return 0;
   }
+
+  static bool copy_done(const CopyRef& c) { return !c || c->done(); }
 
   static int wait_for(hipStream_t s, const StreamRef& c) {
     if (!c) return 0;
