@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 10
+#define MO_ABI_VERSION 11
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */

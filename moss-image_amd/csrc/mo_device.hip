@@ -423,24 +423,29 @@ extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_link_copy_kernel(c
   }
 }
 
+
 // ------------------------------------------------------------------------------------------
 // Wire coding of a staging segment (format in mo_wire.h): three kernels code a segment into a
-// wire buffer (block sizes per tile, one-workgroup scan of the tile sizes into offsets plus
-// the header and the raw tail, then the tiles), and one kernel decodes it. Each workgroup codes
-// one tile of 32 blocks; each of its four waves takes 8 blocks, a lane 8 words (16 bytes) of
-// a block. Every store into the wire buffer goes through a buffer resource bounded by the
+// wire buffer (each tile's exponent model and rANS stream into the working space, with its
+// coded size; a one-workgroup scan of the tile sizes into offsets plus the header and the raw
+// tail; then each tile assembled at its offset), and one kernel decodes it. One wave codes or
+// decodes one tile, four waves a workgroup; the waves share no LDS and never wait for each
+// other. Every store into the wire buffer goes through a buffer resource bounded by the
 // buffer's capacity, and the decoder reads the coded stream through one too, so a stream that
 // arrives damaged cannot make either kernel touch memory outside its buffers.
 namespace mo {
+constexpr int kWireWaves = kThreads / 64;
+constexpr uint32_t kWireOob = 0x80000000u;  // a buffer offset past every wire buffer: the access is dropped
+static_assert(kWireWaves == (int)kWireTilesPerGroup, "one wave per tile");
 
-__device__ __forceinline__ uint32_t wave_min(uint32_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, m, 64));
-  return v;
-}
 __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, m, 64));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += (uint32_t)__shfl_xor((int)v, m, 64);
   return v;
 }
 // Inclusive prefix sum over the wave's lanes.
@@ -452,125 +457,185 @@ __device__ __forceinline__ uint32_t wave_scan(uint32_t v, uint32_t lane) {
   }
   return v;
 }
+// Inclusive prefix maximum over the wave's lanes (values >= 0), by DPP moves: shifts by 1, 2, 4
+// and 8 lanes within each row of 16, then row 0's last lane into row 1 and row 2's into row 3,
+// then lane 31 into rows 2 and 3. Lanes a move has no source for take 0.
+__device__ __forceinline__ uint32_t wave_scan_max_dpp(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false));  // row_shr:1
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false));  // row_shr:2
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false));  // row_shr:4
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false));  // row_shr:8
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return v;
+}
+// Lanes below this one whose bit is set in `mask`.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
 __device__ __forceinline__ uint32_t word_of(const uint4& v, int k) {
   const uint32_t w = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
   return (k & 1) ? w >> 16 : w & 0xffffu;
 }
 __device__ __forceinline__ uint32_t exponent_of(uint32_t word) { return (word >> 7) & 0xffu; }
-
+__device__ __forceinline__ uint32_t sign_mantissa_of(uint32_t word) { return ((word >> 8) & 0x80u) | (word & 0x7fu); }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t wire_rsrc(const char* p, uint64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, (int)(bytes < 0x7fffffffull ? bytes : 0x7fffffffull),
                                            0x00020000);
 }
-
-struct WireCode {
-  uint32_t width, base, escapes;
-};
-
 // Orders the wave's own LDS accesses (a wave's LDS operations execute in order; this keeps the
 // compiler from moving them across).
 __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
 }
-
-// The coding of one block (mo_wire.h), by one wave; `hist` and `pref` are the wave's own 32
-// words of LDS each. Among width 8, and widths 1-5 with a window of offsets s.. from the
-// block's smallest exponent (no escapes when every exponent fits 2^k values, else 2^k - 1
-// values and escapes), it takes the smallest coded size, ties to the smaller width, then the
-// smaller s.
-__device__ __forceinline__ WireCode wire_choose(const uint4& v, uint32_t lane, uint32_t* hist, uint32_t* pref) {
-  uint32_t lo = 255, hi = 0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t e = exponent_of(word_of(v, j));
-    lo = min(lo, e);
-    hi = max(hi, e);
-  }
-  lo = wave_min(lo);
-  if (__all(hi == lo)) return WireCode{0, lo, 0};  // every exponent of the block equals the smallest
-  if (lane < kWireBins) hist[lane] = 0;
-  wave_lds_fence();
-#pragma unroll
-  for (int j = 0; j < 8; ++j) atomicAdd(&hist[min(exponent_of(word_of(v, j)) - lo, kWireBins - 1)], 1u);
-  wave_lds_fence();
-  const uint32_t h = lane < kWireBins ? hist[lane] : 0u;
-  const uint32_t p = wave_scan(h, lane) - h;  // lane i < 32: words in bins 0..i-1
-  if (lane < kWireBins) pref[lane] = p;
-  wave_lds_fence();
-  uint32_t best = (wire_block_coded(8, 0) << 16) | (8u << 8);
-  uint32_t nesc[6] = {0, 0, 0, 0, 0, 0};
-#pragma unroll
-  for (uint32_t k = 1; k <= 5; ++k) {
-    const uint32_t w = 1u << k;
-    const uint32_t s = lane;
-    uint32_t esc = 0xffffu;
-    if (s + w - 1 <= kWireBins - 1) {
-      if (s + w <= kWireBins - 1 && pref[s + w] - p == kWireBlockVals) esc = 0;
-      else esc = kWireBlockVals - (pref[s + w - 1] - p);
-    }
-    nesc[k] = esc;
-    if (esc != 0xffffu) best = min(best, (wire_block_coded(k, esc) << 16) | (k << 8) | s);
-  }
-  best = wave_min(best);
-  const uint32_t width = (best >> 8) & 0xffu, s = best & 0xffu;
-  if (width == 8) return WireCode{8, 0, 0};
-  uint32_t mine = 0;
-#pragma unroll
-  for (uint32_t k = 1; k <= 5; ++k)
-    if (k == width) mine = nesc[k];
-  return WireCode{width, lo + s, (uint32_t)__shfl((int)mine, (int)s, 64)};
-}
-
-// The code of exponent e in a block coded as c; sets *escape for an escaped exponent.
-__device__ __forceinline__ uint32_t wire_code_of(uint32_t e, const WireCode& c, bool* escape) {
-  *escape = false;
-  if (c.width == 8) return e;
-  if (c.width == 0) return 0;
-  const uint32_t d = e - c.base;  // wraps for e < base
-  const uint32_t limit = c.escapes ? (1u << c.width) - 1u : (1u << c.width);
-  if (d < limit) return d;
-  *escape = true;
-  return (1u << c.width) - 1u;
-}
-
+// Coder table entry of one exponent: frequency (bits 0-12), cumulative frequency (bits 13-24)
+// and the shift of its division magic (bits 25-28).
+__device__ __forceinline__ uint32_t shift_of(uint32_t f) { return f > 1 ? 32u - (uint32_t)__clz((int)(f - 1)) : 0u; }
 }  // namespace mo
 
-// Pass 1: each block's coding (its header, into the working space after the largest stream)
-// and the coded size of each tile, into the stream's tile table.
+// Pass 1: each tile's exponent frequencies, normalised, its rANS stream and final states in the
+// working space, and the tile's coded size into the stream's tile table. One wave per tile, 3.5
+// KiB of LDS a wave: the counts, then each exponent's coder entry and division magic, and one
+// group's exponents. State l codes the tile's words 64 j + l, so a group of 8 rounds is 1 KiB of
+// consecutive words: one 16-byte load a lane, moved to LDS, read back one byte a round.
 extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_sizes_kernel(const char* raw, uint64_t raw_bytes,
                                                                                  char* wire, uint64_t wire_capacity) {
   using namespace mo;
-  constexpr int kWaves = kThreads / 64;
-  __shared__ uint32_t hist[kWaves][kWireBins], pref[kWaves][kWireBins];
-  __shared__ uint32_t part[kWaves];
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t nblocks = wire_blocks(raw_bytes);
-  const uint64_t tile = blockIdx.x;
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  __shared__ uint32_t counts[kWireWaves][256];
+  __shared__ u32x2 coder[kWireWaves][256];  // {entry, magic}: entry = f | c << 13 | shift << 25
+  __shared__ __attribute__((aligned(16))) unsigned char groups[kWireWaves][8 * kWireLanes];
+  const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint64_t tile = (uint64_t)blockIdx.x * kWireTilesPerGroup + wave;
+  if (tile >= wire_tiles(raw_bytes)) return;  // wave-uniform; the waves never synchronise
+  const uint32_t n = wire_tile_words(raw_bytes, tile), J = n / kWireLanes, nb = n / kWireBlockVals;
+  const char* src = raw + tile * kWireTileRaw;
   const __amdgpu_buffer_rsrc_t w = wire_rsrc(wire, wire_capacity);
-  const uint64_t scratch = wire_scratch_offset(raw_bytes);
-  uint4 v[8];
+  const uint32_t rec = (uint32_t)(wire_scratch_offset(raw_bytes) + tile * kWireScratchTile);
+  MO_LDS uint32_t* const cnt = (MO_LDS uint32_t*)counts[wave];
+  MO_LDS u32x2* const cod = (MO_LDS u32x2*)coder[wave];
+  for (uint32_t b = lane; b < 256; b += 64) cnt[b] = 0;
+  wave_lds_fence();
+  // Histogram: 8 loads of 16 bytes a lane in flight; each lane adds its 8 exponents once per
+  // distinct value (neighbouring words mostly share exponents, and same-address LDS atomics of
+  // a wave serialise).
+  for (uint32_t c0 = 0; c0 < n / 8; c0 += 8 * 64) {
+    uint4 v[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint64_t b = tile * kWireTileBlocks + wave * 8 + j;
-    v[j] = b < nblocks ? ld16(raw + b * kWireBlockBytes + lane * 16) : make_uint4(0, 0, 0, 0);
-  }
-  uint32_t sum = 0;
-  for (int j = 0; j < 8; ++j) {
-    const uint64_t b = tile * kWireTileBlocks + wave * 8 + j;
-    const WireCode c = wire_choose(v[j], lane, hist[wave], pref[wave]);
-    if (b < nblocks) {
-      sum += wire_block_coded(c.width, c.escapes);
-      if (lane == 0)
-        __builtin_amdgcn_raw_buffer_store_b32(c.base | (c.width << 8) | (c.escapes << 12), w, (int)(scratch + 4 * b), 0,
-                                              0);
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t c = c0 + 64 * i + lane;
+      v[i] = c < n / 8 ? ld16(src + 16 * (uint64_t)c) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (c0 + 64 * i + lane >= n / 8) continue;
+      uint32_t e[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) e[k] = exponent_of(word_of(v[i], k));
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        uint32_t same = 0;
+        bool first = true;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          same += e[q] == e[k] ? 1u : 0u;
+          if (q < k && e[q] == e[k]) first = false;
+        }
+        if (first) atomicAdd(&counts[wave][e[k]], same);
+      }
     }
   }
-  if (lane == 0) part[wave] = sum;
-  __syncthreads();
-  if (threadIdx.x == 0)
-    __builtin_amdgcn_raw_buffer_store_b32(kWireTileHeader + part[0] + part[1] + part[2] + part[3], w,
-                                          (int)(kWireHeader + 4 * tile), 0, 0);
+  wave_lds_fence();
+  // Normalised frequencies: lane l owns exponents 4l .. 4l + 3.
+  uint32_t f[4], fsum = 0, best = 0, pres = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t e = 4 * lane + k, c = cnt[e];
+    f[k] = c ? max(1u, 8u * c / nb) : 0u;  // floor(c * 4096 / n), n = 512 nb
+    fsum += f[k];
+    pres += c ? 1u : 0u;
+    best = max(best, (c << 8) | (255u - e));  // most frequent, the smallest exponent on ties
+  }
+  fsum = wave_sum(fsum);
+  best = wave_max(best);
+  const uint32_t top_e = 255u - (best & 0xffu);
+  uint32_t mine = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    if (4 * lane + k == top_e) mine = f[k];
+  const int adjusted = (int)__shfl((int)mine, (int)(top_e >> 2), 64) + (int)(1u << kWireProbBits) - (int)fsum;
+  bool raw_tile = adjusted < 1;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    if (4 * lane + k == top_e) f[k] = (uint32_t)adjusted;
+  // cumulative frequencies, the table (ascending exponents) and the coder entries
+  const uint32_t lsum = f[0] + f[1] + f[2] + f[3];
+  uint32_t cum = wave_scan(lsum, lane) - lsum;
+  const uint32_t rank_incl = wave_scan(pres, lane);
+  const uint32_t nsym = (uint32_t)__shfl((int)rank_incl, 63, 64);
+  uint32_t rank = rank_incl - pres;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t e = 4 * lane + k;
+    if (f[k]) {
+      __builtin_amdgcn_raw_buffer_store_b32(e | (f[k] << 8), w, (int)(rec + kWireScratchTable + 4 * rank), 0, 0);
+      ++rank;
+      const uint32_t s = shift_of(f[k]);
+      cod[e] = u32x2{f[k] | (cum << 13) | (s << 25), (uint32_t)(((((uint64_t)1 << s) - f[k]) << 32) / f[k] + 1)};
+    }
+    cum += f[k];
+  }
+  wave_lds_fence();
+  // rANS over j = J-1 .. 0; the stream fills the working space from its end downwards
+  uint32_t x = kWireStateLow, top = J * kWireLanes;
+  if (!raw_tile) {
+    MO_LDS unsigned char* const grp = (MO_LDS unsigned char*)groups[wave];
+    const int ngroups = (int)(J / 8);
+    uint4 next = ld16(src + 1024 * (uint64_t)(ngroups - 1) + 16 * lane);
+    for (int g = ngroups - 1; g >= 0; --g) {
+      const uint4 v = next;
+      next = ld16(src + 1024 * (uint64_t)(g > 0 ? g - 1 : 0) + 16 * lane);  // the last one is a spare
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        lo |= exponent_of(word_of(v, k)) << (8 * k);
+        hi |= exponent_of(word_of(v, k + 4)) << (8 * k);
+      }
+      wave_lds_fence();  // the previous group's reads are done
+      *(MO_LDS u32x2*)(grp + 8 * lane) = u32x2{lo, hi};
+      wave_lds_fence();
+#pragma unroll
+      for (int r = 7; r >= 0; --r) {
+        const u32x2 t = cod[grp[64 * r + lane]];
+        const uint32_t fr = t[0] & 0x1fffu, c = (t[0] >> 13) & 0xfffu, s = t[0] >> 25;
+        const bool emit = (uint64_t)x >= ((uint64_t)fr << 20);
+        const uint64_t bal = __ballot(emit);
+        const uint32_t count = (uint32_t)__popcll(bal);
+        // every lane stores, a lane that emits nothing at an offset the buffer drops: a fixed
+        // number of stores a group, which keeps the compiler's wait for `next` exact
+        __builtin_amdgcn_raw_buffer_store_b16(
+            (unsigned short)(x & 0xffffu), w,
+            emit ? (int)(rec + kWireScratchStream + 2 * (top - count + lanes_below(bal))) : (int)kWireOob, 0, 0);
+        x = emit ? x >> 16 : x;
+        top -= count;
+        const uint32_t q = (uint32_t)(((uint64_t)__umulhi(t[1], x) + x) >> s);  // x / fr
+        x = (q << kWireProbBits) + (x - q * fr) + c;
+      }
+    }
+  }
+  const uint32_t nwords = J * kWireLanes - top;
+  __builtin_amdgcn_raw_buffer_store_b32(x, w, (int)(rec + kWireScratchStates + 4 * lane), 0, 0);
+  const uint32_t rans = wire_rans_tile(n, nsym, nwords), plain = wire_raw_tile(n);
+  raw_tile = raw_tile || rans >= plain;
+  if (lane == 0) {
+    const uint32_t size = raw_tile ? plain : rans;
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    __builtin_amdgcn_raw_buffer_store_b128(
+        u32x4{raw_tile ? kWireModeRaw : (kWireModeRans | (nsym << 8)), raw_tile ? 0u : nwords, top, size}, w,
+        (int)rec, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(size, w, (int)(kWireHeader + 4 * tile), 0, 0);
+  }
 }
 
 // Pass 2 (one workgroup of kWireScanThreads): tile sizes -> tile offsets (exclusive scan from
@@ -616,171 +681,183 @@ extern "C" __global__ __launch_bounds__(mo::kWireScanThreads) void mo_wire_scan_
   }
 }
 
-// Pass 3: code each tile at its offset.
+// Pass 3: assemble each tile at its offset (header, then the raw words, or the sign-mantissa
+// bytes, table, final states and stream from the working space). One wave per tile.
 extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_encode_kernel(const char* raw, uint64_t raw_bytes,
                                                                                   char* wire, uint64_t wire_capacity) {
   using namespace mo;
-  constexpr int kWaves = kThreads / 64;
-  __shared__ uint32_t head[kWireTileBlocks], pre[kWireTileBlocks];
-  __shared__ __attribute__((aligned(16))) unsigned char plane[kWaves][kWireBlockVals];
-  __shared__ __attribute__((aligned(16))) unsigned char escs[kWaves][kWireBlockVals];
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t nblocks = wire_blocks(raw_bytes);
-  const uint64_t tile = blockIdx.x;
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint64_t tile = (uint64_t)blockIdx.x * kWireTilesPerGroup + wave;
+  if (tile >= wire_tiles(raw_bytes)) return;
+  const uint32_t n = wire_tile_words(raw_bytes, tile);
+  const char* src = raw + tile * kWireTileRaw;
   const __amdgpu_buffer_rsrc_t w = wire_rsrc(wire, wire_capacity);
+  const uint32_t rec = (uint32_t)(wire_scratch_offset(raw_bytes) + tile * kWireScratchTile);
   const uint32_t toff = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(kWireHeader + 4 * tile), 0, 0);
-  const uint64_t scratch = wire_scratch_offset(raw_bytes);
-  uint4 v[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint64_t b = tile * kWireTileBlocks + wave * 8 + j;
-    v[j] = b < nblocks ? ld16(raw + b * kWireBlockBytes + lane * 16) : make_uint4(0, 0, 0, 0);
+  const u32x4 r = __builtin_amdgcn_raw_buffer_load_b128(w, (int)rec, 0, 0);
+  const uint32_t head = r[0], nwords = r[1], first = r[2];
+  if (lane == 0) __builtin_amdgcn_raw_buffer_store_b128(u32x4{head, nwords, 0u, 0u}, w, (int)toff, 0, 0);
+  const uint32_t body = toff + kWireTileHeader;
+  if ((head & 3u) == kWireModeRaw) {
+    for (uint32_t c = lane; c < n / 8; c += 64) {
+      const uint4 v = ld16(src + 16 * (uint64_t)c);
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, w, (int)(body + 16 * c), 0, 0);
+    }
+    return;
   }
-  if (threadIdx.x < kWireTileBlocks) {
-    // the block codings the sizing pass chose (zero past the end)
-    const uint64_t b = tile * kWireTileBlocks + threadIdx.x;
-    head[threadIdx.x] = b < nblocks ? __builtin_amdgcn_raw_buffer_load_b32(w, (int)(scratch + 4 * b), 0, 0) : 0u;
+  const uint32_t nsym = head >> 8;
+  // sign-mantissa bytes: 16 words in, 16 bytes out a lane and round
+  for (uint32_t c = lane; c < n / 16; c += 64) {
+    const uint4 a = ld16(src + 32 * (uint64_t)c), b = ld16(src + 32 * (uint64_t)c + 16);
+    uint32_t o[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < 16; ++k) o[k >> 2] |= sign_mantissa_of(word_of(k < 8 ? a : b, k & 7)) << (8 * (k & 3));
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{o[0], o[1], o[2], o[3]}, w, (int)(body + 16 * c), 0, 0);
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t acc = 0;
-    for (uint32_t k = 0; k < kWireTileBlocks; ++k) {
-      pre[k] = acc;
-      if (tile * kWireTileBlocks + k < nblocks) acc += wire_block_coded((head[k] >> 8) & 0xfu, head[k] >> 12);
-    }
+  // table, zero-padded to 16 bytes
+  const uint32_t tab = body + n, tab_words = (uint32_t)wire_align16(4 * nsym) / 4;
+  for (uint32_t i = lane; i < tab_words; i += 64) {
+    const uint32_t v = i < nsym ? __builtin_amdgcn_raw_buffer_load_b32(w, (int)(rec + kWireScratchTable + 4 * i), 0, 0) : 0u;
+    __builtin_amdgcn_raw_buffer_store_b32(v, w, (int)(tab + 4 * i), 0, 0);
   }
-  if (threadIdx.x < kWireTileBlocks)
-    __builtin_amdgcn_raw_buffer_store_b32(head[threadIdx.x], w, (int)(toff + 4 * threadIdx.x), 0, 0);
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t bl = wave * 8 + j;
-    const bool live = tile * kWireTileBlocks + bl < nblocks;
-    const WireCode c{(head[bl] >> 8) & 0xfu, head[bl] & 0xffu, head[bl] >> 12};
-    const uint32_t dst = toff + kWireTileHeader + pre[bl];
-    uint32_t sm_lo = 0, sm_hi = 0, nmine = 0;
-    uint64_t acc = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t word = word_of(v[j], k);
-      const uint32_t sm = ((word >> 8) & 0x80u) | (word & 0x7fu);
-      if (k < 4) sm_lo |= sm << (8 * k);
-      else sm_hi |= sm << (8 * (k - 4));
-      bool escape;
-      acc |= (uint64_t)wire_code_of(exponent_of(word), c, &escape) << (k * c.width);
-      nmine += escape ? 1u : 0u;
-    }
-    uint32_t eoff = wave_scan(nmine, lane) - nmine;  // this lane's first escape, in word order
-    if (live) {
-      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-      __builtin_amdgcn_raw_buffer_store_b64(u32x2{sm_lo, sm_hi}, w, (int)(dst + 8 * lane), 0, 0);
-      for (uint32_t i = 0; i < c.width; ++i) plane[wave][lane * c.width + i] = (unsigned char)(acc >> (8 * i));
-      if (nmine) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          bool escape;
-          const uint32_t e = exponent_of(word_of(v[j], k));
-          (void)wire_code_of(e, c, &escape);
-          if (escape) escs[wave][min(eoff++, kWireBlockVals - 1)] = (unsigned char)e;
-        }
-      }
-      // zero padding after the escapes, up to the next 16 bytes
-      const uint32_t padded = (uint32_t)wire_align16(c.escapes);
-      for (uint32_t i = c.escapes + lane; i < padded; i += 64) escs[wave][i] = 0;
-    }
-    __syncthreads();
-    if (live) {
-      if (lane < 4 * c.width) {
-        const mo_u32x4 chunk = *(const MO_LDS mo_u32x4*)(&plane[wave][16 * lane]);
-        __builtin_amdgcn_raw_buffer_store_b128(chunk, w, (int)(dst + kWireBlockVals + 16 * lane), 0, 0);
-      }
-      if (16 * lane < c.escapes) {
-        const mo_u32x4 chunk = *(const MO_LDS mo_u32x4*)(&escs[wave][16 * lane]);
-        __builtin_amdgcn_raw_buffer_store_b128(chunk, w, (int)(dst + kWireBlockVals + 64 * c.width + 16 * lane), 0,
-                                               0);
-      }
-    }
-    __syncthreads();  // the LDS planes are rewritten by the next block
+  // final states
+  const uint32_t states = tab + 4 * tab_words;
+  __builtin_amdgcn_raw_buffer_store_b32(
+      __builtin_amdgcn_raw_buffer_load_b32(w, (int)(rec + kWireScratchStates + 4 * lane), 0, 0), w,
+      (int)(states + 4 * lane), 0, 0);
+  // the stream's words, zero-padded to 16 bytes
+  const uint32_t stream = states + 4 * kWireLanes, padded = (uint32_t)wire_align16(2 * nwords) / 2;
+  for (uint32_t i = lane; i < padded; i += 64) {
+    const unsigned short v =
+        i < nwords ? __builtin_amdgcn_raw_buffer_load_b16(w, (int)(rec + kWireScratchStream + 2 * (first + i)), 0, 0)
+                   : (unsigned short)0;
+    __builtin_amdgcn_raw_buffer_store_b16(v, w, (int)(stream + 2 * i), 0, 0);
   }
 }
 
-// Decode a coded stream of `raw_bytes` into `raw`. Grid: max(tiles, 1) workgroups; the first
-// also copies the raw tail. Reads go through a resource over [wire, wire + wire_bytes), writes
-// stay inside [raw, raw + raw_bytes) whatever the stream holds.
+// Decode a coded stream of `raw_bytes` into `raw`. Grid: max(ceil(tiles / 4), 1) workgroups, one
+// wave per tile; the first workgroup also copies the raw tail. 6.5 KiB of LDS a wave: the table
+// entries by rank, each slot's rank, a ring of the stream's next 512 words, and one group's
+// exponents: state l decodes the tile's words 64 j + l, so the exponents of 8 rounds are 1 KiB of
+// consecutive words, written out as one 16-byte store a lane. Reads go through
+// a resource over [wire, wire + wire_bytes), and writes stay inside [raw, raw + raw_bytes)
+// whatever the stream holds: a damaged header is clamped, and table values only index the
+// wave's own LDS arrays.
 extern "C" __global__ __launch_bounds__(mo::kThreads) void mo_wire_decode_kernel(const char* wire, uint64_t wire_bytes,
                                                                                   uint64_t raw_bytes, char* raw) {
   using namespace mo;
-  constexpr int kWaves = kThreads / 64;
-  __shared__ uint32_t head[kWireTileBlocks], pre[kWireTileBlocks];
-  __shared__ __attribute__((aligned(16))) unsigned char plane[kWaves][kWireBlockVals];
-  __shared__ __attribute__((aligned(16))) unsigned char escs[kWaves][kWireBlockVals];
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t nblocks = wire_blocks(raw_bytes);
-  const uint64_t tile = blockIdx.x;
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  constexpr uint32_t kSlots = 1u << kWireProbBits, kRing = 512;
+  __shared__ __attribute__((aligned(16))) unsigned char slot_rank[kWireWaves][kSlots];
+  __shared__ uint32_t ranks[kWireWaves][256];  // table entry -> exponent | (f - 1) << 8 | c << 20
+  __shared__ __attribute__((aligned(16))) unsigned short rings[kWireWaves][kRing];
+  __shared__ __attribute__((aligned(16))) unsigned char groups[kWireWaves][8 * kWireLanes];
+  const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const __amdgpu_buffer_rsrc_t w = wire_rsrc(wire, wire_bytes);
-  const uint32_t toff = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(kWireHeader + 4 * tile), 0, 0);
-  if (threadIdx.x < kWireTileBlocks) {
-    const uint32_t h = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(toff + 4 * threadIdx.x), 0, 0);
-    // clamp what a damaged header could hold: width 0-8, escapes 0-512
-    head[threadIdx.x] = (h & 0xffu) | (min((h >> 8) & 0xfu, 8u) << 8) | (min(h >> 12, kWireBlockVals) << 12);
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t acc = 0;
-    for (uint32_t k = 0; k < kWireTileBlocks; ++k) {
-      pre[k] = acc;
-      acc += wire_block_coded((head[k] >> 8) & 0xfu, head[k] >> 12);
-    }
-  }
-  __syncthreads();
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t bl = wave * 8 + j;
-    const uint64_t b = tile * kWireTileBlocks + bl;
-    const bool live = b < nblocks;
-    const WireCode c{(head[bl] >> 8) & 0xfu, head[bl] & 0xffu, head[bl] >> 12};
-    const uint32_t src = toff + kWireTileHeader + pre[bl];
-    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-    u32x2 sm = {0, 0};
-    if (live) {
-      sm = __builtin_amdgcn_raw_buffer_load_b64(w, (int)(src + 8 * lane), 0, 0);
-      if (lane < 4 * c.width)
-        *(MO_LDS mo_u32x4*)(&plane[wave][16 * lane]) =
-            __builtin_amdgcn_raw_buffer_load_b128(w, (int)(src + kWireBlockVals + 16 * lane), 0, 0);
-      if (16 * lane < c.escapes)
-        *(MO_LDS mo_u32x4*)(&escs[wave][16 * lane]) = __builtin_amdgcn_raw_buffer_load_b128(
-            w, (int)(src + kWireBlockVals + 64 * c.width + 16 * lane), 0, 0);
-    }
-    __syncthreads();
-    uint64_t acc = 0;
-    for (uint32_t i = 0; i < c.width; ++i) acc |= (uint64_t)plane[wave][lane * c.width + i] << (8 * i);
-    const uint32_t mask = (1u << c.width) - 1u;
-    const uint32_t esc_code = c.escapes && c.width && c.width < 8 ? mask : 0xffffffffu;
-    uint32_t nmine = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) nmine += ((uint32_t)(acc >> (k * c.width)) & mask) == esc_code ? 1u : 0u;
-    uint32_t eoff = wave_scan(nmine, lane) - nmine;
-    if (live) {
-      uint32_t out[4];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t s = ((k < 4 ? sm[0] : sm[1]) >> (8 * (k & 3))) & 0xffu;
-        const uint32_t code = (uint32_t)(acc >> (k * c.width)) & mask;
-        uint32_t e;
-        if (c.width == 8) e = code;
-        else if (code == esc_code) e = escs[wave][min(eoff++, kWireBlockVals - 1)];
-        else e = (c.base + code) & 0xffu;
-        const uint32_t word = ((s & 0x80u) << 8) | (e << 7) | (s & 0x7fu);
-        if (k & 1) out[k >> 1] |= word << 16;
-        else out[k >> 1] = word;
-      }
-      st16(raw + b * kWireBlockBytes + lane * 16, make_uint4(out[0], out[1], out[2], out[3]));
-    }
-    __syncthreads();
-  }
-  if (tile == 0) {
-    const uint64_t tail = raw_bytes % kWireBlockBytes, tail_dst = nblocks * kWireBlockBytes;
+  if (blockIdx.x == 0) {
+    const uint64_t tail = raw_bytes % kWireBlockBytes, tail_dst = wire_blocks(raw_bytes) * kWireBlockBytes;
     const uint64_t data_start = wire_data_start(raw_bytes);
     for (uint64_t i = threadIdx.x; i < tail; i += kThreads)
       st<kG>(raw + tail_dst + i, (uint8_t)__builtin_amdgcn_raw_buffer_load_b8(w, (int)(data_start + i), 0, 0));
+  }
+  const uint64_t tile = (uint64_t)blockIdx.x * kWireTilesPerGroup + wave;
+  if (tile >= wire_tiles(raw_bytes)) return;
+  const uint32_t n = wire_tile_words(raw_bytes, tile), J = n / kWireLanes;
+  char* const dst = raw + tile * kWireTileRaw;
+  const uint32_t toff = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(kWireHeader + 4 * tile), 0, 0);
+  const uint32_t head = __builtin_amdgcn_raw_buffer_load_b32(w, (int)toff, 0, 0);
+  const uint32_t body = toff + kWireTileHeader;
+  if ((head & 3u) != kWireModeRans) {
+    for (uint32_t c = lane; c < n / 8; c += 64) {
+      const mo_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(w, (int)(body + 16 * c), 0, 0);
+      st16(dst + 16 * (uint64_t)c, make_uint4(v.x, v.y, v.z, v.w));
+    }
+    return;
+  }
+  const uint32_t nsym = min((head >> 8) & 0x1ffu, 256u);
+  MO_LDS unsigned char* const sr = (MO_LDS unsigned char*)slot_rank[wave];
+  MO_LDS uint32_t* const rk = (MO_LDS uint32_t*)ranks[wave];
+  MO_LDS unsigned short* const ring = (MO_LDS unsigned short*)rings[wave];
+  // Table entries in rank order with their cumulative frequencies; each entry's first slot is
+  // marked with its rank (rank 0 starts at slot 0, where every slot's mark starts).
+  const uint32_t tab = body + n;
+  for (uint32_t i = lane; i < kSlots / 4; i += 64) *(MO_LDS uint32_t*)(sr + 4 * i) = 0;
+  wave_lds_fence();
+  uint32_t carry = 0;
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t r = 64 * k + lane;
+    const uint32_t e = r < nsym ? __builtin_amdgcn_raw_buffer_load_b32(w, (int)(tab + 4 * r), 0, 0) : 0u;
+    const uint32_t f = r < nsym ? min((e >> 8) & 0x1fffu, kSlots) : 0u;
+    const uint32_t incl = wave_scan(f, lane), c = carry + incl - f;
+    carry += (uint32_t)__shfl((int)incl, 63, 64);
+    rk[r] = (e & 0xffu) | (((f - 1) & 0xfffu) << 8) | ((c & 0xfffu) << 20);
+    if (f && c < kSlots) sr[c] = (unsigned char)r;
+  }
+  wave_lds_fence();
+  // Every slot's rank: the last mark at or before it (marks rise with the slot), 64 slots a
+  // round as a prefix maximum over the round's lanes and the rounds before.
+  uint32_t before = 0;
+  for (uint32_t row = 0; row < kSlots / 64; ++row) {
+    const uint32_t slot = 64 * row + lane;
+    const uint32_t cur = max(before, wave_scan_max_dpp(sr[slot]));
+    before = (uint32_t)__builtin_amdgcn_readlane((int)cur, 63);
+    sr[slot] = (unsigned char)cur;
+  }
+  // States, and the stream's first 512 words into the ring (word i at i % 512); `next` holds
+  // the 2 words this lane brings in at the next refill.
+  const uint32_t states = tab + (uint32_t)wire_align16(4 * nsym);
+  uint32_t x = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(states + 4 * lane), 0, 0);
+  const uint32_t stream = states + 4 * kWireLanes;
+#pragma unroll
+  for (uint32_t q = 0; q < 4; ++q)
+    *(MO_LDS uint32_t*)(ring + 128 * q + 2 * lane) =
+        __builtin_amdgcn_raw_buffer_load_b32(w, (int)(stream + 256 * q + 4 * lane), 0, 0);
+  uint32_t next = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(stream + 1024 + 4 * lane), 0, 0);
+  wave_lds_fence();
+  uint32_t ptr = 0, wb = 0;  // words read so far; the first word the ring still holds
+  // the group's sign-mantissa bytes (words 8 l .. 8 l + 7 of its 512), one group ahead
+  MO_LDS unsigned char* const grp = (MO_LDS unsigned char*)groups[wave];
+  const uint32_t ngroups = J / 8;
+  u32x2 sm_next = __builtin_amdgcn_raw_buffer_load_b64(w, (int)(body + 8 * lane), 0, 0);
+  for (uint32_t g = 0; g < ngroups; ++g) {
+    const u32x2 sm = sm_next;
+    sm_next = __builtin_amdgcn_raw_buffer_load_b64(w, (int)(body + 512 * (g + 1) + 8 * lane), 0, 0);  // a spare past the last
+#pragma unroll
+    for (uint32_t r = 0; r < 8; ++r) {
+      const uint32_t slot = x & (kSlots - 1);
+      const uint32_t t = rk[sr[slot]];
+      x = (((t >> 8) & 0xfffu) + 1) * (x >> kWireProbBits) + slot - (t >> 20);
+      const bool need = x < kWireStateLow;
+      const uint64_t bal = __ballot(need);
+      const uint32_t word = ring[(ptr + lanes_below(bal)) & (kRing - 1)];
+      x = need ? (x << 16) | word : x;
+      ptr += (uint32_t)__popcll(bal);
+      grp[64 * r + lane] = (unsigned char)t;
+      if (ptr - wb >= 128) {
+        // words [wb, wb + 128) are consumed: their ring quarter takes words [wb + 512, wb + 640)
+        *(MO_LDS uint32_t*)(ring + (wb & (kRing - 1)) + 2 * lane) = next;
+        wb += 128;
+        next = __builtin_amdgcn_raw_buffer_load_b32(w, (int)(stream + 2 * (wb + kRing) + 4 * lane), 0, 0);
+        wave_lds_fence();
+      }
+    }
+    wave_lds_fence();
+    const u32x2 ex = *(const MO_LDS u32x2*)(grp + 8 * lane);
+    uint32_t o[4];
+#pragma unroll
+    for (uint32_t k = 0; k < 8; k += 2) {
+      uint32_t pair = 0;
+#pragma unroll
+      for (uint32_t h = 0; h < 2; ++h) {
+        const uint32_t i = k + h;
+        const uint32_t s = (sm[i >> 2] >> (8 * (i & 3))) & 0xffu, e = (ex[i >> 2] >> (8 * (i & 3))) & 0xffu;
+        pair |= (((s & 0x80u) << 8) | (e << 7) | (s & 0x7fu)) << (16 * h);
+      }
+      o[k >> 1] = pair;
+    }
+    st16(dst + 1024 * (uint64_t)g + 16 * lane, make_uint4(o[0], o[1], o[2], o[3]));
+    wave_lds_fence();  // the group buffer is read before the next group writes it
   }
 }

@@ -234,7 +234,7 @@ struct Segment {
   bool prefetched = false;
   int restore_slot = -1;
   uint64_t restore_gen = 0;
-  // Wire-coded: the host copy (host_bytes long, wire_capacity(bytes)) holds the coded stream,
+  // Wire-coded: the host copy (host_bytes long, wire_max_coded(bytes)) holds the coded stream,
   // whose first u64 is its length; a fetch brings it into the restore slot's wire buffer and
   // the unpack decodes it into the slot first.
   bool wire = false;
@@ -316,7 +316,8 @@ struct Engine {
   std::vector<hipEvent_t> timing_pool;
   std::deque<PendingFree> pending;
   std::deque<PendingCount> counts;
-  uint64_t wire_slot_bytes = 0;  // each staging and restore slot's wire buffer, once allocated
+  uint64_t wire_slot_bytes = 0;     // each staging slot's wire buffer, once allocated
+  uint64_t wire_restore_bytes = 0;  // each restore slot's wire buffer, once allocated
   std::deque<Timing> timings;
   mo_stats st{};
 
@@ -552,13 +553,14 @@ struct Engine {
       const uint64_t cap = wire_capacity(seg.bytes);
       if (slot.wire_used + cap <= wire_slot_bytes) {
         char* w = slot.wire + slot.wire_used;
-        if (int rc = pool.alloc(cap, &seg.host)) return rc;
-        seg.host_bytes = cap;
+        const uint64_t most = wire_max_coded(seg.bytes);  // the stream; the working space stays on the device
+        if (int rc = pool.alloc(most, &seg.host)) return rc;
+        seg.host_bytes = most;
         // the coded length goes straight to the host copy's first u64, where the copy engine's
         // issuer reads it once the coding kernels have completed
         MO_HIP((hipError_t)wire_encode((uint64_t)(slot.dev + seg.stage_off), seg.bytes, (uint64_t)w, cap,
                                         (uint64_t)seg.host, stream));
-        MO_LINK(link->d2h_sized(seg.host, w, (const volatile uint64_t*)seg.host, cap, stream, slot.gate, &seg.d2h));
+        MO_LINK(link->d2h_sized(seg.host, w, (const volatile uint64_t*)seg.host, most, stream, slot.gate, &seg.d2h));
         slot.wire_used += (cap + 255) & ~uint64_t(255);
         seg.wire = true;
         seg.committed = true;
@@ -590,21 +592,25 @@ struct Engine {
   bool link_behind = false;
   int busy_wraps = 0;  // consecutive slot advances that found the slot's D2H on the engines
   bool wire_wanted(uint64_t bytes) {
-    if (!(cfg.flags & (MO_FLAG_WIRE_CODING | MO_FLAG_WIRE_AUTO)) || bytes < kWireMinBytes) return false;
+    if (!(cfg.flags & (MO_FLAG_WIRE_CODING | MO_FLAG_WIRE_AUTO)) || bytes < kWireMinBytes || bytes > kWireMaxRaw)
+      return false;
     if (!link->sized_copies()) return false;
     if (cfg.flags & MO_FLAG_WIRE_CODING) return true;
     return link_behind;
   }
 
   // Wire buffers, allocated on first use: one per staging slot (the coded streams of its
-  // segments) and one per restore slot (a fetched stream).
+  // segments, each followed by the coder's working space) and one per restore slot (a fetched
+  // stream, at most wire_max_coded of a slot).
   int ensure_wire() {
     if (wire_slot_bytes) return 0;
     const uint64_t bytes = ((wire_capacity(cfg.stage_slot_bytes) + cfg.stage_slot_bytes / 64 + (2ull << 20)) + 4095) &
                            ~uint64_t(4095);
+    const uint64_t fetched = (wire_max_coded(cfg.stage_slot_bytes) + 4095) & ~uint64_t(4095);
     for (auto& s : stage) MO_HIP(hipMalloc(&s.wire, bytes));
-    for (auto& r : restore) MO_HIP(hipMalloc(&r.wire, bytes));
+    for (auto& r : restore) MO_HIP(hipMalloc(&r.wire, fetched));
     wire_slot_bytes = bytes;
+    wire_restore_bytes = fetched;
     return 0;
   }
 
@@ -952,7 +958,8 @@ struct Engine {
     st.host_bytes_in_use = pool.in_use();
     st.host_bytes_peak = pool.peak();
     st.host_bytes_reserved = pool.reserved();
-    st.device_ring_bytes = (stage.size() + restore.size()) * (cfg.stage_slot_bytes + wire_slot_bytes);
+    st.device_ring_bytes = stage.size() * (cfg.stage_slot_bytes + wire_slot_bytes) +
+                           restore.size() * (cfg.stage_slot_bytes + wire_restore_bytes);
     *out = st;
   }
 

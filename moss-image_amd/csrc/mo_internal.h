@@ -66,7 +66,9 @@ int launch_equal(const void* a, const void* b, uint64_t nbytes, uint32_t* flag, 
 // `stream`, and also writes the coded size to pinned host memory at `host_total` (0: not).
 // wire_decode restores the raw bytes from a coded stream of at most `wire_bytes`. Both buffers
 // 16-byte aligned (wire_check).
-constexpr uint64_t kWireMaxRaw = 1ull << 31;
+// At most 512 MiB: the coder addresses the wire buffer, about 2.1x the raw bytes with its working
+// space, through 32-bit buffer offsets.
+constexpr uint64_t kWireMaxRaw = 1ull << 29;
 int wire_check(uint64_t raw, uint64_t raw_bytes, uint64_t wire, uint64_t wire_bytes, std::string& err);
 int wire_encode(uint64_t raw, uint64_t raw_bytes, uint64_t wire, uint64_t capacity, uint64_t host_total,
                 hipStream_t stream);

@@ -310,6 +310,7 @@ int wire_encode(uint64_t raw, uint64_t raw_bytes, uint64_t wire, uint64_t capaci
   DeviceModule m;
   if (int rc = module_of_device(&m)) return rc;
   const uint64_t tiles = wire_tiles(raw_bytes);
+  const uint32_t groups = (uint32_t)((tiles + kWireTilesPerGroup - 1) / kWireTilesPerGroup);  // one wave per tile
   const void* r = (const void*)raw;
   void* w = (void*)wire;
   uint64_t n = raw_bytes, cap = capacity;
@@ -317,7 +318,7 @@ int wire_encode(uint64_t raw, uint64_t raw_bytes, uint64_t wire, uint64_t capaci
   hipError_t e;
   if (tiles) {
     void* params[] = {&r, &n, &w, &cap};
-    if ((e = hipModuleLaunchKernel(m.wire_sizes, (uint32_t)tiles, 1, 1, kThreads, 1, 1, 0, stream, params, nullptr)) !=
+    if ((e = hipModuleLaunchKernel(m.wire_sizes, groups, 1, 1, kThreads, 1, 1, 0, stream, params, nullptr)) !=
         hipSuccess)
       return (int)e;
   }
@@ -329,7 +330,7 @@ int wire_encode(uint64_t raw, uint64_t raw_bytes, uint64_t wire, uint64_t capaci
   }
   if (tiles) {
     void* params[] = {&r, &n, &w, &cap};
-    if ((e = hipModuleLaunchKernel(m.wire_encode, (uint32_t)tiles, 1, 1, kThreads, 1, 1, 0, stream, params,
+    if ((e = hipModuleLaunchKernel(m.wire_encode, groups, 1, 1, kThreads, 1, 1, 0, stream, params,
                                    nullptr)) != hipSuccess)
       return (int)e;
   }
@@ -344,7 +345,8 @@ int wire_decode(uint64_t wire, uint64_t wire_bytes, uint64_t raw, uint64_t raw_b
   void* r = (void*)raw;
   uint64_t wb = wire_bytes, n = raw_bytes;
   void* params[] = {&w, &wb, &n, &r};
-  return (int)hipModuleLaunchKernel(m.wire_decode, (uint32_t)(tiles ? tiles : 1), 1, 1, kThreads, 1, 1, 0, stream,
+  const uint32_t groups = (uint32_t)((tiles + kWireTilesPerGroup - 1) / kWireTilesPerGroup);  // one wave per tile
+  return (int)hipModuleLaunchKernel(m.wire_decode, groups ? groups : 1, 1, 1, kThreads, 1, 1, 0, stream,
                                     params, nullptr);
 }
 

@@ -4,33 +4,38 @@
 //
 // A segment's payload is a byte string whose pieces start 256-byte aligned, so the bfloat16
 // values it mostly holds sit on the 2-byte grid. The coder reads it as 16-bit words w =
-// s(1) e(8) m(7): it keeps each word's sign and mantissa as one byte, and codes the 8-bit
-// exponent field per 512-word block in one of three ways, whichever is smallest:
-//   width 0       every exponent of the block equals `base`;
-//   width k 1..7  (the coder uses 1..5) a k-bit code per word: code c < 2^k - 1 (or any c when the block has no
-//                 escapes) stands for exponent base + c; code 2^k - 1 marks an escape, whose
-//                 8-bit exponent follows in the block's escape bytes, in word order;
-//   width 8       the exponent bytes as they are.
-// Words that are not bfloat16 (float32 low halves, integers, random bits) take width 8 and
-// cost 1/256 more than raw. Decoding restores every word bit for bit, NaN payloads included.
+// s(1) e(8) m(7), in tiles of up to 32 blocks of 512 words (32 KiB raw). A tile keeps each
+// word's sign and mantissa as one byte and codes the 8-bit exponent fields with interleaved rANS
+// (range asymmetric numeral systems): 64 coder states, state l taking the tile's words
+// l*J .. l*J + J - 1 (J = the tile's words / 64), 32-bit states kept in [2^16, 2^32), 16-bit
+// renormalisation words, and the tile's exponent frequencies normalised to 4096:
+//   f(e) = floor(count(e) * 4096 / words) for every exponent e present, at least 1, and the
+//   difference of their sum to 4096 added to the most frequent exponent (the smallest on ties).
+// Coding runs over j = J-1 .. 0: state x with symbol e (frequency f, cumulative frequency c)
+// first emits x & 0xffff and shifts x right by 16 when x >= f << 20, then becomes
+// (x / f) << 12 | (x % f) + c. The words one round j emits are stored in lane order, and the
+// rounds in ascending j; the decoder runs j = 0 .. J-1: e = the symbol whose slot range holds
+// x & 4095, x = f * (x >> 12) + (x & 4095) - c, then x = x << 16 | next word while x < 2^16.
+// A tile whose coding would not be smaller than its raw words is stored raw; so is a tile whose
+// normalisation would leave the most frequent exponent below 1 (not seen on real data).
 //
 // Layout (all offsets in bytes from the start of the coded stream, little-endian):
 //   [0, 16)            header: u64 total (coded bytes, header included), u32 raw bytes,
 //                      u32 tiles
 //   [16, 16 + 4 T)     u32 offset of each tile's data
 //   data_start         the raw tail (raw bytes % kWireBlockBytes bytes, copied as is)
-//   tiles_start        the tiles, each 16-byte aligned:
-//                        kWireTileBlocks u32 block headers (base | width << 8 | escapes << 12;
-//                        zero for blocks past the end), then each block's data:
-//                          kWireBlockVals sign-mantissa bytes (byte i: word i's bit 15 as
-//                          bit 7, its bits 0-6 as bits 0-6),
-//                          64 * width code bytes: lane l of the coding wave packs words
-//                          8l..8l+7 into `width` bytes at l * width, word 8l+k in bits
-//                          [k * width, (k + 1) * width) of that little-endian field,
-//                          the escapes' exponent bytes, zero-padded to a multiple of 16.
-// A tile holds 32 blocks of 512 words (1 KiB raw each). The wire buffer a coder writes into
-// also holds, after the largest stream, its working space: each block's header as the sizing
-// pass chose it (wire_capacity covers both).
+//   tiles_start        the tiles, each 16-byte aligned. A tile of n words:
+//                        u32 mode | nsym << 8, u32 stream words, u32 0, u32 0;
+//                        mode 1 (raw): the n words as they are;
+//                        mode 0 (rANS): n sign-mantissa bytes (byte i: word i's bit 15 as
+//                        bit 7, its bits 0-6 as bits 0-6), the frequency table (nsym u32
+//                        exponent | frequency << 8, ascending exponents; cumulative frequencies
+//                        follow in that order) zero-padded to 16 bytes, the 64 final states
+//                        (u32), the stream's 16-bit words zero-padded to 16 bytes.
+// The wire buffer a coder writes into also holds, after the largest stream, its working space:
+// per tile a 16-byte record (mode | nsym << 8, stream words, first stream word, coded size),
+// the frequency table, the final states and room for the largest stream, which the coding pass
+// fills from the end (wire_capacity covers both).
 // Plain constexpr code (callable from device code too), no HIP headers, like mo_kdesc.h.
 #pragma once
 
@@ -38,36 +43,50 @@
 
 namespace mo {
 
-constexpr uint32_t kWireBlockVals = 512;                              // words per block (one wave)
+constexpr uint32_t kWireBlockVals = 512;                              // words per block
 constexpr uint32_t kWireBlockBytes = 2 * kWireBlockVals;              // raw bytes per block
-constexpr uint32_t kWireTileBlocks = 32;                              // blocks per tile (one workgroup)
+constexpr uint32_t kWireTileBlocks = 32;                              // blocks per tile (one coding wave)
+constexpr uint32_t kWireTileVals = kWireBlockVals * kWireTileBlocks;  // 16 384 words per tile
 constexpr uint32_t kWireTileRaw = kWireBlockBytes * kWireTileBlocks;  // 32 KiB raw per tile
 constexpr uint32_t kWireHeader = 16;
-constexpr uint32_t kWireTileHeader = 4 * kWireTileBlocks;
+constexpr uint32_t kWireTileHeader = 16;
+constexpr uint32_t kWireLanes = 64;           // interleaved rANS states per tile
+constexpr uint32_t kWireProbBits = 12;        // frequencies sum to 4096
+constexpr uint32_t kWireStateLow = 1u << 16;  // states stay in [2^16, 2^32)
+constexpr uint32_t kWireModeRans = 0, kWireModeRaw = 1;
+constexpr uint32_t kWireTilesPerGroup = 4;   // one wave per tile, four waves a workgroup
 constexpr uint32_t kWireScanThreads = 1024;  // the one workgroup of the offset scan
-constexpr uint32_t kWireBins = 32;           // exponent offsets 0..30 from the block minimum; 31 = farther
+// Working space per tile: record, table (256 u32), states, stream (one word per exponent).
+constexpr uint32_t kWireScratchTable = 16;
+constexpr uint32_t kWireScratchStates = kWireScratchTable + 4 * 256;
+constexpr uint32_t kWireScratchStream = kWireScratchStates + 4 * kWireLanes;
+constexpr uint32_t kWireScratchTile = kWireScratchStream + 2 * kWireTileVals;
 
 constexpr uint64_t wire_align16(uint64_t x) { return (x + 15) & ~uint64_t(15); }
 constexpr uint64_t wire_blocks(uint64_t raw) { return raw / kWireBlockBytes; }
 constexpr uint64_t wire_tiles(uint64_t raw) {
   return (wire_blocks(raw) + kWireTileBlocks - 1) / kWireTileBlocks;
 }
+// Words of tile t (a multiple of 512).
+constexpr uint32_t wire_tile_words(uint64_t raw, uint64_t t) {
+  return kWireBlockVals *
+         (uint32_t)(wire_blocks(raw) - t * kWireTileBlocks < kWireTileBlocks ? wire_blocks(raw) - t * kWireTileBlocks
+                                                                              : kWireTileBlocks);
+}
 constexpr uint64_t wire_data_start(uint64_t raw) { return wire_align16(kWireHeader + 4 * wire_tiles(raw)); }
 constexpr uint64_t wire_tiles_start(uint64_t raw) {
   return wire_align16(wire_data_start(raw) + raw % kWireBlockBytes);
 }
-// Coded bytes of one block: sign-mantissa bytes, codes, padded escape bytes.
-constexpr uint32_t wire_block_coded(uint32_t width, uint32_t escapes) {
-  return kWireBlockVals + 64 * width + (uint32_t)wire_align16(escapes);
+constexpr uint32_t wire_raw_tile(uint32_t n) { return kWireTileHeader + 2 * n; }
+constexpr uint32_t wire_rans_tile(uint32_t n, uint32_t nsym, uint32_t nwords) {
+  return kWireTileHeader + n + (uint32_t)wire_align16(4 * nsym) + 4 * kWireLanes + (uint32_t)wire_align16(2 * nwords);
 }
-// Largest coded size of `raw` bytes (every block at width 8, which the coder never exceeds).
+// Largest coded size of `raw` bytes (every tile raw, which the coder never exceeds).
 constexpr uint64_t wire_max_coded(uint64_t raw) {
-  return wire_tiles_start(raw) + wire_tiles(raw) * (kWireTileHeader + (uint64_t)kWireTileBlocks * wire_block_coded(8, 0));
+  return wire_tiles_start(raw) + kWireTileHeader * wire_tiles(raw) + wire_blocks(raw) * kWireBlockBytes;
 }
-// The coder's working space after the largest stream: each block's header (u32), chosen once
-// by the sizing pass and read by the coding pass.
 constexpr uint64_t wire_scratch_offset(uint64_t raw) { return wire_align16(wire_max_coded(raw)); }
 // The wire buffer to provide for coding `raw` bytes: the largest stream plus the working space.
-constexpr uint64_t wire_capacity(uint64_t raw) { return wire_scratch_offset(raw) + 4 * wire_blocks(raw); }
+constexpr uint64_t wire_capacity(uint64_t raw) { return wire_scratch_offset(raw) + kWireScratchTile * wire_tiles(raw); }
 
 }  // namespace mo

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 10
+MO_ABI_VERSION = 11
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001

@@ -3,10 +3,11 @@
 Each case codes a device buffer, compares the coded stream byte for byte with the numpy model
 (``tests/wire_model.py``) on every byte the format defines, checks the coded size the scan
 kernel wrote to pinned host memory, decodes into a buffer with sentinel guard bytes on both
-sides, and compares the result bitwise with the input. Inputs cover every width (random bits,
-one exponent, Gaussian activations, all exponent classes with NaN payloads, infinities,
-signed zeros and subnormals, exponents that differ between the 8-word groups each lane of the
-coding wave reads), partial tiles and raw tails, and a 50 MiB Gaussian buffer.
+sides, and compares the result bitwise with the input. Inputs cover both tile modes (random
+bits stay raw; one exponent, Gaussian activations, all exponent classes with NaN payloads,
+infinities, signed zeros and subnormals, and exponents that change from one coder state's run
+of words to the next are rANS-coded), partial tiles of 1 to 31 blocks and raw tails, and a
+50 MiB Gaussian buffer.
 """
 
 from __future__ import annotations
@@ -64,7 +65,8 @@ def _content(kind: str, nbytes: int, seed: int) -> torch.Tensor:
 CASES = [
     ("random", 16), ("random", 1024), ("random", 1040), ("gauss", 32 * 1024), ("gauss", 32 * 1024 + 1024 + 16),
     ("flat", 64 * 1024), ("special", 3 * 32 * 1024 + 5 * 1024 + 496), ("gauss", (1 << 20) + 48),
-    ("random", 40 * 1024 + 3), ("gauss", 0), ("lanes", 64 * 1024 * 4 + 2 * 1024),
+    ("random", 40 * 1024 + 3), ("gauss", 0), ("lanes", 64 * 1024 * 4 + 2 * 1024), ("gauss", 3 * 1024 + 100),
+    ("special", 31 * 1024),
 ]
 
 
@@ -101,7 +103,7 @@ def test_encode_matches_model_and_decodes_bitwise(kind, nbytes) -> None:
 
 def test_large_gaussian_buffer_round_trip_and_ratio() -> None:
     """50 MiB of Gaussian bfloat16 (an activation-like buffer): bitwise round trip, and a coded
-    size within the model's, about 0.75 of the raw bytes."""
+    size of about 0.67 of the raw bytes (8 sign-mantissa bits and about 2.7 exponent bits a word)."""
 
     lib = _native.load()
     stream = torch.cuda.current_stream(DEV).cuda_stream
@@ -118,7 +120,7 @@ def test_large_gaussian_buffer_round_trip_and_ratio() -> None:
     torch.cuda.synchronize()
     coded = int(total[0])
     assert coded == int(wire[:8].cpu().view(torch.int64)[0])
-    assert coded < 0.8 * nbytes
+    assert coded < 0.69 * nbytes
     _native.check("mo_wire_decode", lib.mo_wire_decode(wire.data_ptr(), coded, out.data_ptr(), nbytes, stream))
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), src.view(torch.int16))
