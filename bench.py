@@ -1295,7 +1295,7 @@ def main() -> int:
     parser.add_argument("--layers", type=int, default=CONFIG3["num_layers"])
     parser.add_argument("--no-parity", action="store_true")
     parser.add_argument("--stage-slots", type=int, default=4)
-    parser.add_argument("--restore-slots", type=int, default=4)
+    parser.add_argument("--restore-slots", type=int, default=6)
     parser.add_argument("--slot-mib", type=int, default=128)
     parser.add_argument("--no-staged-restore", action="store_true")
     parser.add_argument("--d2h-engine", type=lambda v: int(v, 0), default=0,
