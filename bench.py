@@ -18,6 +18,8 @@ Prints ONE JSON line (stdout). Progress goes to stderr.
 
 Leg Q: the config-5 int8 weight-only GEMMs on the HIP MFMA kernels against the eager path.
 Leg BR: regime B on the first 16 blocks, where the reference hooks' pinned copies fit the host.
+Legs A4 and C5P: config 4 (2048^2 + 4096 text tokens, regime A) and config 5 packed (int8
+bases, LoRA r16, four buckets in one varlen traversal, regime A), 3 timed steps after 1 warm-up.
 Leg AH: regime A with 100 ms of host work after every step, on both host-link transports (the
 SDMA link's unpack waits on the host for its H2D; the HIP-stream link's never does).
 Parity: loss and LoRA gradients against hooks off in regimes A, B and B at 16 blocks.
@@ -37,6 +39,8 @@ import time
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
+# legs whose steps take seconds: timed over --steps-big steps
+BIG_LEGS = ("A4", "C5U", "C5P", "S5", "F3", "F3S")
 for _p in (ROOT / "moss-image_amd", ROOT):
     if str(_p) not in sys.path:
         sys.path.insert(0, str(_p))
@@ -1126,8 +1130,12 @@ def run(args) -> dict:
         torch.cuda.synchronize()
         log(f"regime {regime_name}: hooks see {len(manifest.records)} saves, payload {payload_unique / 1e9:.2f} GB "
             f"unique ({payload_copied / 1e9:.2f} GB as the reference copies it)")
-        steps = args.steps if regime_name == "A" else max(1, args.steps_b)
-        warmup = args.warmup if regime_name == "A" else max(1, args.warmup_b)
+        if regime_name == "A":
+            steps, warmup = args.steps, args.warmup
+        elif regime_name in BIG_LEGS:
+            steps, warmup = max(1, args.steps_big), max(1, args.warmup_big)
+        else:
+            steps, warmup = max(1, args.steps_b), max(1, args.warmup_b)
         host_work_s = args.host_work_ms / 1e3 if regime_name == "AH" else 0.0
         if regime_name == "BK":
             entry_extra = {"keep_last_blocks": args.keep_last_blocks}
@@ -1271,7 +1279,10 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--steps-b", type=int, default=5, help="timed steps of the legs other than A")
     parser.add_argument("--warmup-b", type=int, default=2)
-    parser.add_argument("--regimes", default="M,K,Q,A,B,BR,AH",
+    parser.add_argument("--steps-big", type=int, default=3,
+                        help="timed steps of the config-4/5 and full-parameter legs (2.3-4.7 s steps)")
+    parser.add_argument("--warmup-big", type=int, default=1)
+    parser.add_argument("--regimes", default="M,K,Q,A,B,BR,AH,A4,C5P",
                         help="M = config-2 block microbench, K = 28 MiB gathers/scatters back to back and after "
                         "other kernels (a GEMM with a large output, a fill, a read), Q = config-5 int8 GEMMs "
                         "(HIP vs eager), "
