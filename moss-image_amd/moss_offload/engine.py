@@ -57,7 +57,7 @@ class EngineConfig:
     # Lossless wire coding of staging segments on the SDMA link (MO_FLAG_WIRE_*): "off", "on"
     # (every segment of at least 256 KiB), "auto" (only segments that close while at least two
     # staging slots of D2H bytes are queued, i.e. while the link sets the pace). Coded segments
-    # cross the link in fewer bytes (bfloat16 activations: about 0.76) for HBM-bound coding
+    # cross the link in fewer bytes (bfloat16 activations: about 0.66) for HBM-bound coding
     # kernels and one wire buffer per staging and restore slot, allocated on first use.
     wire_coding: str = "auto"
     copy_kernel_blocks: int = 16
