@@ -607,8 +607,11 @@ struct Engine {
     const uint64_t bytes = ((wire_capacity(cfg.stage_slot_bytes) + cfg.stage_slot_bytes / 64 + (2ull << 20)) + 4095) &
                            ~uint64_t(4095);
     const uint64_t fetched = (wire_max_coded(cfg.stage_slot_bytes) + 4095) & ~uint64_t(4095);
-    for (auto& s : stage) MO_HIP(hipMalloc(&s.wire, bytes));
-    for (auto& r : restore) MO_HIP(hipMalloc(&r.wire, fetched));
+    // a failed allocation leaves the buffers made so far in place for the next attempt
+    for (auto& s : stage)
+      if (!s.wire) MO_HIP(hipMalloc(&s.wire, bytes));
+    for (auto& r : restore)
+      if (!r.wire) MO_HIP(hipMalloc(&r.wire, fetched));
     wire_slot_bytes = bytes;
     wire_restore_bytes = fetched;
     return 0;
