@@ -71,7 +71,7 @@ extern "C" {
 #define MO_FLAG_WIRE_CODING 0x200 /* code every staging segment of at least 256 KiB with the
                                      lossless wire coding (mo_wire_encode) before its D2H and
                                      decode it after its H2D: bfloat16 activations cross the
-                                     host link in about 0.75 of their bytes. SDMA link only
+                                     host link in about 0.66 of their bytes. SDMA link only
                                      (the coded length is read when the copy is issued);
                                      costs one wire buffer per staging and restore slot     */
 #define MO_FLAG_WIRE_AUTO 0x400   /* the same, only for segments that close while the D2H
@@ -179,14 +179,15 @@ int mo_scatter(const mo_tensor* tensors, int n, uint64_t payload, const uint64_t
 
 /* Wire coding of a payload (lossless; no counterpart in the reference, which copies raw bytes).
  * The engine codes staging segments with it before their D2H when MO_FLAG_WIRE_CODING (or
- * MO_FLAG_WIRE_AUTO) is set. Sixteen-bit words keep their sign and mantissa as a byte and
- * replace their 8-bit exponent by an offset of 0-8 bits from the smallest exponent of their
- * 512-word block; bfloat16 activations shrink to about 0.75 of their bytes. Format in
- * csrc/mo_wire.h. mo_wire_capacity: the largest coded size of raw_bytes (the wire buffer to
- * provide). mo_wire_encode codes raw_bytes at device `raw` into device `wire` (3 launches on
- * `stream`); the coded size is the stream's first u64 and is also written to pinned host memory
- * at `host_total` (0: not). mo_wire_decode restores raw_bytes bytes from a coded stream of at
- * most wire_bytes. Buffers 16-byte aligned, raw_bytes at most 2^31. */
+ * MO_FLAG_WIRE_AUTO) is set. Sixteen-bit words keep their sign and mantissa as a byte; the
+ * 8-bit exponents of each 32 KiB tile are coded with interleaved rANS (64 states, the tile's
+ * exponent frequencies normalised to 4096), and a tile that would not shrink is stored raw;
+ * bfloat16 activations shrink to about 0.66 of their bytes. Format in csrc/mo_wire.h.
+ * mo_wire_capacity: the largest coded size of raw_bytes plus the coder's working space (the
+ * wire buffer to provide). mo_wire_encode codes raw_bytes at device `raw` into device `wire`
+ * (3 launches on `stream`); the coded size is the stream's first u64 and is also written to
+ * pinned host memory at `host_total` (0: not). mo_wire_decode restores raw_bytes bytes from a
+ * coded stream of at most wire_bytes. Buffers 16-byte aligned, raw_bytes at most 2^29. */
 uint64_t mo_wire_capacity(uint64_t raw_bytes);
 int mo_wire_encode(uint64_t raw, uint64_t raw_bytes, uint64_t wire, uint64_t wire_capacity, uint64_t host_total,
                    uint64_t stream);
