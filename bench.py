@@ -1162,6 +1162,9 @@ def run(args) -> dict:
             configure_mode(wl_model, mode, regime)
             engine = mode_engine(device, mode) or get_engine(device)
             engine.config.keep_last_blocks = args.keep_last_blocks if regime_name == "BK" else 0
+            # wire buffers a previous leg allocated (coding ran there) are freed, so each leg's
+            # ring bytes are its own
+            engine.trim()
             # marks the start of each leg and mode in a kernel trace, and scales rocprofv3
             # FETCH_SIZE / WRITE_SIZE to bytes in a counter run
             calibration_copy(device, torch.cuda.current_stream(device).cuda_stream)

@@ -284,7 +284,9 @@ int mo_synchronize(mo_engine* engine);
 int mo_get_stats(mo_engine* engine, mo_stats* stats);
 int mo_reset_stats(mo_engine* engine);
 
-/* Release pinned chunks that hold no live payload. */
+/* Release pinned chunks that hold no live payload. With no group live, also free the wire
+ * buffers (after waiting for every copy and for the device; the next coded segment allocates
+ * them again). */
 int mo_trim(mo_engine* engine);
 
 /* Name of the host-link transport in use: "sdma" or "kernel". */

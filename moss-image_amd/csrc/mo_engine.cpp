@@ -934,6 +934,37 @@ struct Engine {
     return process_pending(false);
   }
 
+  // Pinned chunks that hold no live payload go back to the driver. With no group left (open or
+  // committed), the wire buffers are freed too, after every copy and every kernel on the device
+  // has finished (the next coded segment allocates them again); the restore slots then hold
+  // nothing.
+  int trim() {
+    if (int rc = process_pending(false)) return rc;
+    pool.trim();
+    if (!wire_slot_bytes || open_group || !groups.empty()) return 0;
+    MO_LINK(link->synchronize());
+    MO_HIP(hipDeviceSynchronize());
+    hipError_t first = hipSuccess;
+    for (auto& s : stage) {
+      const hipError_t e = s.wire ? hipFree(s.wire) : hipSuccess;
+      if (first == hipSuccess) first = e;
+      s.wire = nullptr;
+      s.wire_used = 0;
+    }
+    for (auto& r : restore) {
+      const hipError_t e = r.wire ? hipFree(r.wire) : hipSuccess;
+      if (first == hipSuccess) first = e;
+      r.wire = nullptr;
+      r.group = kNone;
+      r.consumed = true;
+      r.decoded = true;
+    }
+    wire_slot_bytes = 0;
+    wire_restore_bytes = 0;
+    MO_HIP(first);
+    return 0;
+  }
+
   int synchronize() {
     if (int rc = flush_packs()) return rc;
     MO_LINK(link->synchronize());
@@ -1322,7 +1353,7 @@ int mo_get_stats(mo_engine* engine, mo_stats* stats) {
 int mo_reset_stats(mo_engine* engine) { MO_ENGINE_CALL(engine, (engine->e.reset_stats(), 0)); }
 
 int mo_trim(mo_engine* engine) {
-  MO_ENGINE_CALL(engine, (engine->e.process_pending(false), engine->e.pool.trim(), 0));
+  MO_ENGINE_CALL(engine, engine->e.trim());
 }
 
 const char* mo_link_name(mo_engine* engine) {

@@ -473,8 +473,8 @@ def test_wire_coded_segments_round_trip(mode, staged) -> None:
     if mode == "on":
         assert st["wire_segments"] > 0
     if st["wire_segments"]:
-        # random-bit tensors code at width 8 (a little over raw); the coded size never exceeds
-        # the format's worst case
+        # random-bit tiles are stored raw (a little over raw with their headers); the coded size
+        # never exceeds the format's worst case
         assert 0 < st["wire_bytes"] <= st["wire_raw_bytes"] * 1.003 + 4096 * st["wire_segments"]
     assert st["bytes_unpacked"] == st["bytes_packed"]
     for _, gid, idx in handles:
@@ -482,6 +482,41 @@ def test_wire_coded_segments_round_trip(mode, staged) -> None:
     engine.synchronize()
     assert engine.stats()["host_bytes_in_use"] == 0
     engine.close()
+
+
+def test_trim_frees_wire_buffers_only_with_no_group_live() -> None:
+    """mo_trim keeps the wire buffers while a group is live (its restore still decodes
+    bitwise) and frees them once none is; the next coded segment allocates them again."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine(wire_coding="on")
+    stream = torch.cuda.current_stream(device).cuda_stream
+    rings = engine.stats()["device_ring_bytes"]  # no wire buffers yet
+    assert rings == (3 + 2) * 2 * MiB
+    g = torch.Generator(device="cpu").manual_seed(11)
+
+    def round_trip(trim_while_live: bool) -> None:
+        t = torch.randn(700_000, generator=g).to(torch.bfloat16).to(device)
+        gid, idx = engine.pack(t, stream)
+        engine.commit(stream)
+        engine.synchronize()
+        coded = engine.stats()["device_ring_bytes"]
+        assert coded > rings  # the segment was coded: wire buffers exist
+        if trim_while_live:
+            engine.trim()
+            assert engine.stats()["device_ring_bytes"] == coded
+        assert_bitwise(engine.restore(gid, idx, stream), t)
+        engine.drop(gid, idx)
+        engine.synchronize()
+        engine.trim()
+        assert engine.stats()["device_ring_bytes"] == rings
+
+    try:
+        round_trip(trim_while_live=True)
+        round_trip(trim_while_live=False)  # buffers allocated again after the trim
+        assert engine.stats()["wire_segments"] >= 2
+    finally:
+        engine.close()
 
 
 def test_wire_coding_is_skipped_on_the_hip_stream_link() -> None:
