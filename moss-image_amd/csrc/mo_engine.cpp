@@ -281,11 +281,14 @@ struct PendingFree {
 };
 
 // Coded bytes of a wire-coded copy, counted once the copy has completed (they are the first
-// u64 of the host copy, known only after the coding kernels ran).
+// u64 of the host copy, known only after the coding kernels ran). A D2H names its segment, whose
+// host copy then shrinks to the stream's length.
 struct PendingCount {
   const char* host;
   CopyRef copy;
   bool d2h;
+  uint64_t group = 0;
+  uint32_t seg = 0;
 };
 
 struct Timing {
@@ -514,10 +517,28 @@ struct Engine {
         uint64_t total = 0;
         memcpy(&total, c.host, sizeof(total));
         (c.d2h ? st.bytes_d2h : st.bytes_h2d) += total;
-        if (c.d2h) st.wire_bytes += total;
+        if (c.d2h) {
+          st.wire_bytes += total;
+          shrink_host(c, total);
+        }
       }
       counts.pop_front();
     }
+  }
+
+  // A coded segment's host copy was sized for its largest stream; once its D2H has landed the
+  // stream's length is known and the rest of the copy goes back to the pool. A fetch issued
+  // earlier copies only the stream's length, so it reads nothing past what is kept.
+  void shrink_host(const PendingCount& c, uint64_t total) {
+    Group* g = find(c.group);
+    if (!g || c.seg >= g->segs.size()) return;  // released meanwhile: freed whole
+    Segment& seg = g->segs[c.seg];
+    if (seg.host != c.host || !seg.wire || total > seg.host_bytes) return;
+    const uint64_t held = align_up(seg.host_bytes, kHostAlign);
+    const uint64_t keep = align_up(std::max<uint64_t>(total, 16), kHostAlign);
+    if (keep >= held) return;
+    pool.free(seg.host + keep, held - keep);
+    seg.host_bytes = keep;
   }
 
   int process_pending(bool wait) {
@@ -544,7 +565,8 @@ struct Engine {
   int close_segment(hipStream_t stream) {
     if (!open_group || open_seg < 0) return 0;
     if (int rc = flush_packs()) return rc;
-    Segment& seg = open_group->segs[open_seg];
+    const uint32_t si = (uint32_t)open_seg;
+    Segment& seg = open_group->segs[si];
     StageSlot& slot = stage[seg.stage_slot];
     seg.bytes = slot.used - seg.stage_off;
     open_seg = -1;
@@ -567,7 +589,7 @@ struct Engine {
         st.d2h_copies++;
         st.wire_segments++;
         st.wire_raw_bytes += seg.bytes;
-        counts.push_back(PendingCount{seg.host, seg.d2h, true});
+        counts.push_back(PendingCount{seg.host, seg.d2h, true, open_group->id, si});
         return 0;
       }
     }

@@ -500,8 +500,12 @@ def test_trim_frees_wire_buffers_only_with_no_group_live() -> None:
         gid, idx = engine.pack(t, stream)
         engine.commit(stream)
         engine.synchronize()
-        coded = engine.stats()["device_ring_bytes"]
+        st = engine.stats()
+        coded = st["device_ring_bytes"]
         assert coded > rings  # the segment was coded: wire buffers exist
+        # its host copy, sized for the largest stream, shrank to the stream once the D2H landed
+        assert st["wire_bytes"] > 0
+        assert st["host_bytes_in_use"] <= 0.72 * t.numel() * 2 + 4096
         if trim_while_live:
             engine.trim()
             assert engine.stats()["device_ring_bytes"] == coded
