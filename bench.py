@@ -960,6 +960,7 @@ def run(args) -> dict:
         kernel_timing=True,
         stage_slots=args.stage_slots,
         restore_slots=args.restore_slots,
+        prefetch_depth=args.prefetch_depth,
         stage_slot_bytes=args.slot_mib << 20,
         staged_restore=not args.no_staged_restore,
         kernel_copy=args.kernel_copy,
@@ -1309,7 +1310,9 @@ def main() -> int:
     parser.add_argument("--layers", type=int, default=CONFIG3["num_layers"])
     parser.add_argument("--no-parity", action="store_true")
     parser.add_argument("--stage-slots", type=int, default=4)
-    parser.add_argument("--restore-slots", type=int, default=6)
+    parser.add_argument("--restore-slots", type=int, default=8)
+    parser.add_argument("--prefetch-depth", type=int, default=8,
+                        help="groups the engine prefetches ahead of backward after each restored group")
     parser.add_argument("--slot-mib", type=int, default=128)
     parser.add_argument("--no-staged-restore", action="store_true")
     parser.add_argument("--d2h-engine", type=lambda v: int(v, 0), default=0,

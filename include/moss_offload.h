@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 11
+#define MO_ABI_VERSION 12
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -106,7 +106,7 @@ typedef struct mo_tensor {
 typedef struct mo_config {
   uint64_t stage_slot_bytes;    /* [128 MiB] device staging and restore slot size      */
   uint32_t stage_slots;         /* [4] slots in the forward staging ring               */
-  uint32_t restore_slots;       /* [6] slots in the backward restore ring              */
+  uint32_t restore_slots;       /* [8] slots in the backward restore ring              */
   uint64_t host_limit_bytes;    /* [0 = no limit] cap on pinned host memory             */
   uint64_t host_chunk_bytes;    /* [1 GiB] granularity of hipHostMalloc reservations   */
   uint32_t flags;               /* MO_FLAG_*                                          */
@@ -263,6 +263,12 @@ int mo_commit(mo_engine* engine, uint64_t stream, uint64_t* group);
  * so a later mo_unpack on `stream` finds them resident. Segments still intact in their staging
  * slot (and packed on `stream`) are skipped: unpack reads them there. Never blocks the host. */
 int mo_prefetch(mo_engine* engine, uint64_t group, uint64_t stream);
+
+/* Prefetch several groups, given in the order backward will need them: the first as
+ * mo_prefetch does; each later one only if every segment it still needs gets a free restore
+ * slot now (a farther group never takes a slot a nearer one will need); stops at the first
+ * that does not fit. No reference counterpart: the reference prefetches nothing. */
+int mo_prefetch_groups(mo_engine* engine, const uint64_t* groups, uint32_t n, uint64_t stream);
 
 /* Restore entries of a group: dst[i] is the device address for entry i (0 = skip it), laid out
  * with the strides the entry was packed with. H2D copies any missing segment, makes `stream`

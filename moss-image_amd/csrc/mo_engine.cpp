@@ -860,6 +860,27 @@ struct Engine {
     return 0;
   }
 
+  // Groups in the order backward will need them: the first as far as free slots allow (as
+  // prefetch), each later one only if every segment it still needs gets a free slot now, so a
+  // farther group never takes a slot a nearer one will need. Stops at the first that does not.
+  int prefetch_groups(const uint64_t* gids, uint32_t n, hipStream_t stream) {
+    if (n == 0) return 0;
+    if (int rc = prefetch(gids[0], stream)) return rc;
+    for (uint32_t k = 1; k < n; ++k) {
+      Group* g = find(gids[k]);
+      if (!g) return fail(MO_E_INVALID, "mo_prefetch_groups: unknown group " + std::to_string(gids[k]));
+      if (g->open) return 0;
+      uint32_t needed = 0, free_slots = 0;
+      for (uint32_t si = 0; si < g->segs.size(); ++si)
+        if (!resident(*g, si) && !staged(g->segs[si], stream)) ++needed;
+      for (const RestoreSlot& r : restore)
+        if (r.group == kNone || r.consumed) ++free_slots;
+      if (needed > free_slots) return 0;
+      if (int rc = prefetch(gids[k], stream)) return rc;
+    }
+    return 0;
+  }
+
   int unpack(uint64_t gid, const uint64_t* dst, uint32_t n, hipStream_t stream) {
     if (int rc = check_link()) return rc;
     link_behind = false;
@@ -1030,7 +1051,7 @@ struct Engine {
     if (c) cfg = *c;
     if (!cfg.stage_slot_bytes) cfg.stage_slot_bytes = 128ull << 20;
     if (!cfg.stage_slots) cfg.stage_slots = 4;
-    if (!cfg.restore_slots) cfg.restore_slots = 6;
+    if (!cfg.restore_slots) cfg.restore_slots = 8;
     if (!cfg.host_chunk_bytes) cfg.host_chunk_bytes = 1ull << 30;
     if (!cfg.copy_kernel_blocks) cfg.copy_kernel_blocks = 16;
     if (cfg.stage_slot_bytes < 2 * kMinPiece || cfg.stage_slot_bytes % kPieceAlign)
@@ -1338,6 +1359,11 @@ int mo_commit(mo_engine* engine, uint64_t stream, uint64_t* group) {
 
 int mo_prefetch(mo_engine* engine, uint64_t group, uint64_t stream) {
   MO_ENGINE_CALL(engine, engine->e.prefetch(group, (hipStream_t)stream));
+}
+
+int mo_prefetch_groups(mo_engine* engine, const uint64_t* groups, uint32_t n, uint64_t stream) {
+  if (n && !groups) return mo::fail(MO_E_INVALID, "mo_prefetch_groups: null group list");
+  MO_ENGINE_CALL(engine, engine->e.prefetch_groups(groups, n, (hipStream_t)stream));
 }
 
 int mo_unpack(mo_engine* engine, uint64_t group, const uint64_t* dst, uint32_t n, uint64_t stream) {

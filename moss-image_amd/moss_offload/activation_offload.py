@@ -407,7 +407,7 @@ class _ActivationOffload:
             # forward made repeatedly (e.g. one RoPE table checkpointed with every block): start
             # bringing them back now. Segments still in the staging ring are skipped.
             for gid in ([last] if last is not None else []) + sorted(self._shared - {last}, reverse=True):
-                self.engine.prefetch(gid, stream)
+                self.engine.prefetch(gid, stream, ahead=gid == last)
         self._shared.clear()
         return False
 

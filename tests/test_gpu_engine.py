@@ -484,6 +484,48 @@ def test_wire_coded_segments_round_trip(mode, staged) -> None:
     engine.close()
 
 
+def test_prefetch_groups_takes_a_farther_group_only_when_all_of_it_fits() -> None:
+    """mo_prefetch_groups: the nearest group as far as slots allow, a later one only when every
+    segment it needs gets a free slot; restores stay bitwise whatever was prefetched."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine(wire_coding="off", prefetch=False)  # 2 MiB slots: 3 staging, 2 restore
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(5)
+    slot_elems = MiB  # bfloat16 elements that fill one 2 MiB slot
+    try:
+        # one-slot groups g0-g3, a three-slot group g4, then g5-g8, which wrap the staging ring
+        # past every segment before them
+        sizes = [slot_elems] * 4 + [3 * slot_elems] + [slot_elems] * 4
+        handles, gids = [], []
+        for n in sizes:
+            t = torch.randn(n, generator=g).to(torch.bfloat16).to(device)
+            gid, idx = engine.pack(t, stream)
+            engine.commit(stream)
+            handles.append((t, gid, idx))
+            gids.append(gid)
+        engine.synchronize()
+        issued = lambda: engine.stats()["prefetch_issued"]  # noqa: E731
+        base = issued()
+        # g3 and g2 take the two restore slots; g1 finds none
+        engine._prefetch_groups([gids[3], gids[2], gids[1]], stream)
+        assert issued() - base == 2
+        _restore_and_check(engine, handles, device, [3, 2])
+        # g1 takes one of the two freed slots; g4 needs three and is left alone
+        base = issued()
+        engine._prefetch_groups([gids[1], gids[4]], stream)
+        assert issued() - base == 1
+        _restore_and_check(engine, handles, device, [1, 4, 0, 5, 6, 7, 8])
+        st = engine.stats()
+        assert st["prefetch_hits"] >= 3 and st["copy_failures"] == 0
+        for _, gid, idx in handles:
+            engine.drop(gid, idx)
+        engine.synchronize()
+        assert engine.stats()["host_bytes_in_use"] == 0
+    finally:
+        engine.close()
+
+
 def test_trim_frees_wire_buffers_only_with_no_group_live() -> None:
     """mo_trim keeps the wire buffers while a group is live (its restore still decodes
     bitwise) and frees them once none is; the next coded segment allocates them again."""
