@@ -18,8 +18,9 @@ Prints ONE JSON line (stdout). Progress goes to stderr.
 
 Leg Q: the config-5 int8 weight-only GEMMs on the HIP MFMA kernels against the eager path.
 Leg BR: regime B on the first 16 blocks, where the reference hooks' pinned copies fit the host.
-Legs A4 and C5P: config 4 (2048^2 + 4096 text tokens, regime A) and config 5 packed (int8
-bases, LoRA r16, four buckets in one varlen traversal, regime A), 3 timed steps after 1 warm-up.
+Legs A4, C5U and C5P: config 4 (2048^2 + 4096 text tokens, regime A) and config 5 (int8 bases,
+LoRA r16, four buckets, regime A) unpacked (four graphs before one backward) and packed (one
+varlen traversal), 3 timed steps after 1 warm-up.
 Leg AH: regime A with 100 ms of host work after every step, on both host-link transports (the
 SDMA link's unpack waits on the host for its H2D; the HIP-stream link's never does).
 Parity: loss and LoRA gradients against hooks off in regimes A, B and B at 16 blocks.
@@ -1286,7 +1287,7 @@ def main() -> int:
     parser.add_argument("--steps-big", type=int, default=3,
                         help="timed steps of the config-4/5 and full-parameter legs (2.3-4.7 s steps)")
     parser.add_argument("--warmup-big", type=int, default=1)
-    parser.add_argument("--regimes", default="M,K,Q,A,B,BR,AH,A4,C5P",
+    parser.add_argument("--regimes", default="M,K,Q,A,B,BR,AH,A4,C5U,C5P",
                         help="M = config-2 block microbench, K = 28 MiB gathers/scatters back to back and after "
                         "other kernels (a GEMM with a large output, a fill, a read), Q = config-5 int8 GEMMs "
                         "(HIP vs eager), "
