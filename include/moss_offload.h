@@ -130,7 +130,8 @@ typedef struct mo_stats {
   uint64_t bytes_packed, bytes_unpacked;  /* payload bytes through pack / unpack kernels */
   uint64_t bytes_d2h, bytes_h2d;          /* bytes over the host link                  */
   uint64_t pack_launches, unpack_launches, d2h_copies, h2d_copies;
-  uint64_t host_bytes_in_use, host_bytes_peak, host_bytes_reserved;
+  uint64_t host_bytes_in_use, host_bytes_peak, host_bytes_reserved;  /* pinned pool; the peak since
+                                                                         creation or mo_reset_stats */
   uint64_t stage_slot_waits;   /* staging slots reused (each ordered after its last D2H) */
   uint64_t host_blocks;        /* engine calls that blocked the host for a copy          */
   double host_block_ms;        /* time spent blocked in them                             */

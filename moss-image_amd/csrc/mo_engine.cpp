@@ -197,6 +197,7 @@ class HostPool {
 
   uint64_t in_use() const { return in_use_; }
   uint64_t peak() const { return peak_; }
+  void reset_peak() { peak_ = in_use_; }
   uint64_t reserved() const { return reserved_; }
 
  private:
@@ -1043,6 +1044,7 @@ struct Engine {
   void reset_stats() {
     process_timings(false);
     link->reset_stats();
+    pool.reset_peak();  // the pinned peak counts from here, like the other statistics
     st = mo_stats{};
   }
 
