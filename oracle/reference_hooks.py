@@ -181,11 +181,10 @@ def emulated_offload(model: nn.Module, recorder: Recorder | None = None):
 
 
 def bits(tensor: torch.Tensor) -> torch.Tensor:
-    """Integer view of a tensor's logical elements (bitwise comparison; -0.0 != +0.0, NaN == NaN)."""
+    """Integer view of a tensor's logical elements, in logical order (bitwise comparison:
+    -0.0 != +0.0, a NaN equals a NaN of the same payload only, and a bool is its stored byte)."""
 
     width = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}[tensor.element_size()]
-    if tensor.dtype == torch.bool:
-        return tensor.to(torch.uint8)
     return tensor.contiguous().view(width)
 
 
