@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 12
+#define MO_ABI_VERSION 13
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -116,6 +116,10 @@ typedef struct mo_config {
                                    halves, one per engine                              */
   uint32_t h2d_engine;          /* [0 = the lowest available not used by D2H] SDMA
                                    engine bits for H2D (two bits: split the same way)  */
+  uint64_t wire_device_limit;   /* [0 = no limit] cap on the device bytes of the wire
+                                   buffers; where they would pass it, or their
+                                   allocation fails, segments cross raw and the engine
+                                   tries again at the next forward                    */
 } mo_config;
 
 /* Where one packed tensor lives: its group (one block's saves) and index in the group. */
@@ -155,6 +159,9 @@ typedef struct mo_stats {
                                   and bytes_h2d count coded bytes for coded segments        */
   uint64_t device_ring_bytes;  /* device memory the engine holds: staging and restore slots,
                                   plus their wire buffers once wire coding has run          */
+  uint64_t wire_fallbacks;     /* segments meant for wire coding that crossed raw because the
+                                  wire buffers could not be allocated (or would pass
+                                  wire_device_limit)                                        */
 } mo_stats;
 
 typedef struct mo_engine mo_engine;

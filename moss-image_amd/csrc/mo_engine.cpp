@@ -27,6 +27,7 @@
 #include <vector>
 
 #include "../../include/moss_offload.h"
+#include "mo_deferred.h"
 #include "mo_internal.h"
 #include "mo_link.h"
 
@@ -272,25 +273,20 @@ struct RestoreSlot {
   bool consumed = true;  // scattered at least once since fetched (or empty)
   int gate = -1;
   char* wire = nullptr;  // a coded segment's stream as fetched (wire coding)
-  bool decoded = true;   // dev holds the fetched segment's raw bytes
+  bool decoded = true;   // dev holds the fetched segment's raw bytes (once `join` completes)
+  // Recorded on `used_on` after the slot's last decode and scatter: an unpack of the slot on
+  // another stream waits for it first. Compared by handle only, never used as a stream.
+  hipEvent_t join = nullptr;
+  hipStream_t used_on = nullptr;
 };
 
-struct PendingFree {
-  char* host;
-  uint64_t bytes;
-  CopyRef copies[2];
-};
-
-// Coded bytes of a wire-coded copy, counted once the copy has completed (they are the first
-// u64 of the host copy, known only after the coding kernels ran). A D2H names its segment, whose
-// host copy then shrinks to the stream's length.
-struct PendingCount {
-  const char* host;
-  CopyRef copy;
-  bool d2h;
-  uint64_t group = 0;
-  uint32_t seg = 0;
-};
+// Host ranges freed once their copies finish, and coded byte counts read once theirs finish
+// (mo_deferred.h). A count's bytes are the first u64 of the host copy, known only after the
+// coding kernels ran; a D2H names its segment, whose host copy then shrinks to the stream's
+// length.
+using Deferred = mo::DeferredHost<CopyRef>;
+using PendingFree = Deferred::Free;
+using PendingCount = Deferred::Count;
 
 struct Timing {
   hipEvent_t start, end;
@@ -318,8 +314,7 @@ struct Engine {
   uint64_t next_group = 0;
   uint64_t gen_counter = 0, tick = 0;
   std::vector<hipEvent_t> timing_pool;
-  std::deque<PendingFree> pending;
-  std::deque<PendingCount> counts;
+  Deferred deferred;  // host frees and coded-byte counts waiting for their copies
   uint64_t wire_slot_bytes = 0;     // each staging slot's wire buffer, once allocated
   uint64_t wire_restore_bytes = 0;  // each restore slot's wire buffer, once allocated
   std::deque<Timing> timings;
@@ -503,28 +498,39 @@ struct Engine {
   }
 
   // ---- deferred host frees ----
-  // Count the coded bytes of wire-coded copies that have completed (before any host free).
+  // Count the coded bytes of every wire-coded copy that has completed. With `wait`, first wait
+  // (at most 300 s) for all of them.
   void process_counts(bool wait) {
-    while (!counts.empty()) {
-      PendingCount& c = counts.front();
-      if (!idle(c.copy)) {
-        if (!wait) break;
-        const auto deadline = std::chrono::steady_clock::now() + std::chrono::seconds(300);
-        while (!idle(c.copy) && std::chrono::steady_clock::now() < deadline)
-          std::this_thread::sleep_for(std::chrono::microseconds(50));
-        if (!idle(c.copy)) break;
-      }
-      if (!c.copy->failed()) {
-        uint64_t total = 0;
-        memcpy(&total, c.host, sizeof(total));
-        (c.d2h ? st.bytes_d2h : st.bytes_h2d) += total;
-        if (c.d2h) {
-          st.wire_bytes += total;
-          shrink_host(c, total);
-        }
-      }
-      counts.pop_front();
+    if (wait) wait_copies(false);
+    deferred.settle_counts(idle, [this](const PendingCount& c) { count(c); });
+  }
+
+  void count(const PendingCount& c) {
+    if (c.copy && c.copy->failed()) return;
+    uint64_t total = 0;
+    memcpy(&total, c.host, sizeof(total));
+    (c.d2h ? st.bytes_d2h : st.bytes_h2d) += total;
+    if (c.d2h) {
+      st.wire_bytes += total;
+      shrink_host(c, total);
     }
+  }
+
+  // Poll until every copy the deferred work refers to has finished (only the counts' copies
+  // unless `frees`); false after 300 s.
+  bool wait_copies(bool frees) {
+    const auto deadline = std::chrono::steady_clock::now() + std::chrono::seconds(300);
+    auto busy = [&] {
+      if (frees) return !deferred.all_done(idle);
+      for (const PendingCount& c : deferred.counts)
+        if (!idle(c.copy)) return true;
+      return false;
+    };
+    while (busy()) {
+      if (std::chrono::steady_clock::now() > deadline) return false;
+      std::this_thread::sleep_for(std::chrono::microseconds(50));
+    }
+    return true;
   }
 
   // A coded segment's host copy was sized for its largest stream; once its D2H has landed the
@@ -542,24 +548,13 @@ struct Engine {
     seg.host_bytes = keep;
   }
 
+  // Settle the counts and free the host ranges whose copies have finished; with `wait`, all of
+  // them (at most 300 s).
   int process_pending(bool wait) {
-    process_counts(wait);
-    const auto deadline = std::chrono::steady_clock::now() + std::chrono::seconds(300);
-    for (auto it = pending.begin(); it != pending.end();) {
-      bool done = idle(it->copies[0]) && idle(it->copies[1]);
-      while (!done && wait) {
-        if (std::chrono::steady_clock::now() > deadline) return fail(MO_E_STATE, "copies did not finish in 300 s");
-        std::this_thread::sleep_for(std::chrono::microseconds(50));
-        done = idle(it->copies[0]) && idle(it->copies[1]);
-      }
-      if (done) {
-        pool.free(it->host, it->bytes);
-        it = pending.erase(it);
-      } else {
-        ++it;
-      }
-    }
-    return 0;
+    const bool finished = !wait || wait_copies(true);
+    deferred.settle(idle, [this](const PendingCount& c) { count(c); },
+                    [this](char* host, uint64_t bytes) { pool.free(host, bytes); });
+    return finished ? 0 : fail(MO_E_STATE, "copies did not finish in 300 s");
   }
 
   // ---- forward ----
@@ -571,8 +566,7 @@ struct Engine {
     StageSlot& slot = stage[seg.stage_slot];
     seg.bytes = slot.used - seg.stage_off;
     open_seg = -1;
-    if (wire_wanted(seg.bytes)) {
-      if (int rc = ensure_wire()) return rc;
+    if (wire_wanted(seg.bytes) && wire_ready()) {
       const uint64_t cap = wire_capacity(seg.bytes);
       if (slot.wire_used + cap <= wire_slot_bytes) {
         char* w = slot.wire + slot.wire_used;
@@ -590,7 +584,7 @@ struct Engine {
         st.d2h_copies++;
         st.wire_segments++;
         st.wire_raw_bytes += seg.bytes;
-        counts.push_back(PendingCount{seg.host, seg.d2h, true, open_group->id, si});
+        deferred.counts.push_back(PendingCount{seg.host, seg.d2h, true, open_group->id, si});
         return 0;
       }
     }
@@ -618,26 +612,46 @@ struct Engine {
     if (!(cfg.flags & (MO_FLAG_WIRE_CODING | MO_FLAG_WIRE_AUTO)) || bytes < kWireMinBytes || bytes > kWireMaxRaw)
       return false;
     if (!link->sized_copies()) return false;
-    if (cfg.flags & MO_FLAG_WIRE_CODING) return true;
-    return link_behind;
+    if (!(cfg.flags & MO_FLAG_WIRE_CODING) && !link_behind) return false;
+    if (wire_unavailable) {
+      st.wire_fallbacks++;
+      return false;
+    }
+    return true;
   }
 
   // Wire buffers, allocated on first use: one per staging slot (the coded streams of its
   // segments, each followed by the coder's working space) and one per restore slot (a fetched
   // stream, at most wire_max_coded of a slot).
-  int ensure_wire() {
-    if (wire_slot_bytes) return 0;
+  // They are an optimisation, so the step never fails for want of them: where they would pass
+  // cfg.wire_device_limit or an allocation fails (the HIP error is cleared, the buffers made so
+  // far stay for the next attempt), segments cross raw until the next forward tries again.
+  bool wire_unavailable = false;
+  bool wire_ready() {
+    if (wire_slot_bytes) return true;
     const uint64_t bytes = ((wire_capacity(cfg.stage_slot_bytes) + cfg.stage_slot_bytes / 64 + (2ull << 20)) + 4095) &
                            ~uint64_t(4095);
     const uint64_t fetched = (wire_max_coded(cfg.stage_slot_bytes) + 4095) & ~uint64_t(4095);
-    // a failed allocation leaves the buffers made so far in place for the next attempt
+    bool ok = !cfg.wire_device_limit || bytes * stage.size() + fetched * restore.size() <= cfg.wire_device_limit;
     for (auto& s : stage)
-      if (!s.wire) MO_HIP(hipMalloc(&s.wire, bytes));
+      if (ok && !s.wire && hipMalloc(&s.wire, bytes) != hipSuccess) {
+        s.wire = nullptr;
+        ok = false;
+      }
     for (auto& r : restore)
-      if (!r.wire) MO_HIP(hipMalloc(&r.wire, fetched));
+      if (ok && !r.wire && hipMalloc(&r.wire, fetched) != hipSuccess) {
+        r.wire = nullptr;
+        ok = false;
+      }
+    if (!ok) {
+      (void)hipGetLastError();
+      wire_unavailable = true;
+      st.wire_fallbacks++;
+      return false;
+    }
     wire_slot_bytes = bytes;
     wire_restore_bytes = fetched;
-    return 0;
+    return true;
   }
 
   int advance_slot(hipStream_t stream) {
@@ -826,7 +840,7 @@ struct Engine {
     if (seg.wire) {
       MO_LINK(link->h2d_sized(r.wire, seg.host, (const volatile uint64_t*)seg.host, seg.host_bytes, seg.d2h, r.gate,
                               &copy));
-      counts.push_back(PendingCount{seg.host, copy, false});
+      deferred.counts.push_back(PendingCount{seg.host, copy, false, 0, 0});
       r.decoded = false;
     } else {
       MO_LINK(link->h2d(r.dev, seg.host, seg.bytes, seg.d2h, r.gate, &copy));
@@ -834,6 +848,7 @@ struct Engine {
       r.decoded = true;
     }
     seg.h2d = std::move(copy);
+    r.used_on = nullptr;  // the H2D was ordered after the slot's consumed point
     r.group = g.id;
     r.seg = si;
     r.gen = ++gen_counter;
@@ -886,6 +901,7 @@ struct Engine {
     if (int rc = check_link()) return rc;
     link_behind = false;
     busy_wraps = 0;
+    wire_unavailable = false;  // the next forward may try to allocate the wire buffers again
     process_pending(false);
     Group* g = find(gid);
     if (!g) return fail(MO_E_INVALID, "mo_unpack: unknown group " + std::to_string(gid));
@@ -922,6 +938,9 @@ struct Engine {
       seg.prefetched = false;
       if (r) {
         MO_LINK(link->wait(r->gate, stream));
+        // Last decoded or read on another stream: this stream reads the slot after that work,
+        // and so the consumed point recorded below covers both streams' reads.
+        if (r->used_on && r->used_on != stream) MO_HIP(hipStreamWaitEvent(stream, r->join, 0));
         if (!r->decoded) {
           // the coded stream has landed (wait): decode it into the slot on this stream, ahead
           // of the unpack kernels that read the slot
@@ -947,6 +966,9 @@ struct Engine {
       st.unpack_launches += L.launches();
       if (r) {
         MO_LINK(link->consumed(r->gate, stream));
+        if (!r->join) MO_HIP(hipEventCreateWithFlags(&r->join, hipEventDisableTiming));
+        MO_HIP(hipEventRecord(r->join, stream));
+        r->used_on = stream;
         r->consumed = true;
         r->tick = ++tick;
       }
@@ -965,7 +987,7 @@ struct Engine {
       open_seg = -1;
     }
     for (Segment& seg : g->segs) {
-      if (seg.host) pending.push_back(PendingFree{seg.host, seg.host_bytes, {seg.d2h, seg.h2d}});
+      if (seg.host) deferred.frees.push_back(PendingFree{seg.host, seg.host_bytes, {seg.d2h, seg.h2d}});
       if (seg.restore_slot >= 0) {
         RestoreSlot& r = restore[seg.restore_slot];
         if (r.group == g->id && r.gen == seg.restore_gen) {
@@ -985,7 +1007,10 @@ struct Engine {
   int trim() {
     if (int rc = process_pending(false)) return rc;
     pool.trim();
-    if (!wire_slot_bytes || open_group || !groups.empty()) return 0;
+    bool any_wire = false;
+    for (const auto& s : stage) any_wire = any_wire || s.wire;
+    for (const auto& r : restore) any_wire = any_wire || r.wire;
+    if (!any_wire || open_group || !groups.empty()) return 0;
     MO_LINK(link->synchronize());
     MO_HIP(hipDeviceSynchronize());
     hipError_t first = hipSuccess;
@@ -1002,6 +1027,7 @@ struct Engine {
       r.group = kNone;
       r.consumed = true;
       r.decoded = true;
+      r.used_on = nullptr;
     }
     wire_slot_bytes = 0;
     wire_restore_bytes = 0;
@@ -1096,8 +1122,7 @@ struct Engine {
     (void)hipDeviceSynchronize();
     groups.clear();
     (void)process_pending(true);
-    pending.clear();
-    counts.clear();
+    deferred.clear();
     link.reset();
     for (auto& t : timings) {
       (void)hipEventDestroy(t.start);
@@ -1119,6 +1144,7 @@ struct Engine {
     for (auto& r : restore) {
       if (r.dev) (void)hipFree(r.dev);
       if (r.wire) (void)hipFree(r.wire);
+      if (r.join) (void)hipEventDestroy(r.join);
     }
     stage.clear();
     restore.clear();

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 12
+MO_ABI_VERSION = 13
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -62,6 +62,7 @@ class MoConfig(ctypes.Structure):
         ("copy_kernel_blocks", ctypes.c_uint32),
         ("d2h_engine", ctypes.c_uint32),
         ("h2d_engine", ctypes.c_uint32),
+        ("wire_device_limit", ctypes.c_uint64),
     ]
 
 
@@ -117,6 +118,7 @@ class MoStats(ctypes.Structure):
         ("wire_raw_bytes", ctypes.c_uint64),
         ("wire_bytes", ctypes.c_uint64),
         ("device_ring_bytes", ctypes.c_uint64),
+        ("wire_fallbacks", ctypes.c_uint64),
     ]
 
     def as_dict(self) -> dict:

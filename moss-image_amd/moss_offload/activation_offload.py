@@ -160,9 +160,9 @@ class _OffloadedTensor:
     reference. ``group is None`` marks a save with no elements.
     """
 
-    __slots__ = ("engine", "group", "entry", "device", "dtype", "shape", "stride", "payload_shape")
+    __slots__ = ("engine", "group", "entry", "device", "dtype", "shape", "stride", "payload_shape", "reader")
 
-    def __init__(self, engine, group, entry, device, dtype, shape, stride, payload_shape):
+    def __init__(self, engine, group, entry, device, dtype, shape, stride, payload_shape, reader=True):
         self.engine = engine
         self.group = group
         self.entry = entry
@@ -171,12 +171,13 @@ class _OffloadedTensor:
         self.shape = shape
         self.stride = stride
         self.payload_shape = payload_shape
+        self.reader = reader  # False: held by a recomputed save for its replay, not by autograd
 
     def __del__(self):
         engine = self.engine
         if engine is not None and self.group is not None:
             try:
-                engine.drop(self.group, self.entry)
+                engine.drop(self.group, self.entry, self.reader)
             except Exception:  # interpreter shutdown or engine already closed
                 pass
 
@@ -513,7 +514,7 @@ class _ActivationOffload:
         # before any reuse of that cast's memory once the engine lets go of it
         if stream != rec_stream:
             return None
-        target = self._own(handle)
+        target = self._own(handle, reader=True)
         if target is None:
             return None
         ticket = self.engine.equal(earlier, tensor, stream)
@@ -553,14 +554,15 @@ class _ActivationOffload:
             return None
         return handle, meta
 
-    def _own(self, handle):
-        """A reference of the derived handle's own to an input handle."""
+    def _own(self, handle, reader: bool = False):
+        """A reference of a derived or alias handle's own to an input handle: ``reader`` when its
+        restore goes to autograd (an alias's target), not when a replay only reads it."""
 
         if isinstance(handle, _OffloadedTensor) and handle.group is not None:
-            if not self.engine.acquire(handle.group, handle.entry):
+            if not self.engine.acquire(handle.group, handle.entry, reader=reader):
                 return None
             return _OffloadedTensor(handle.engine, handle.group, handle.entry, handle.device, handle.dtype,
-                                    handle.shape, handle.stride, handle.payload_shape)
+                                    handle.shape, handle.stride, handle.payload_shape, reader=reader)
         return handle  # a derived handle (owns its inputs) or a resident tensor
 
     def _derive(self, tensor: torch.Tensor) -> _DerivedTensor | None:
@@ -629,7 +631,7 @@ class _ActivationOffload:
             restored = torch.empty_strided(saved.payload_shape, saved.stride, dtype=saved.dtype, device=saved.device)
         else:
             stream = torch.cuda.current_stream(saved.device).cuda_stream
-            restored = saved.engine.restore(saved.group, saved.entry, stream)
+            restored = saved.engine.restore(saved.group, saved.entry, stream, saved.reader)
         return restored.as_strided(saved.shape, saved.stride)
 
 

@@ -30,6 +30,10 @@ import torch
 from . import _native
 
 
+LINKS = ("sdma", "hipdma")
+WIRE_CODINGS = {"off": 0, "on": _native.MO_FLAG_WIRE_CODING, "auto": _native.MO_FLAG_WIRE_AUTO}
+
+
 @dataclass
 class EngineConfig:
     """Sizes and switches of one device engine (see ``mo_config`` in moss_offload.h)."""
@@ -64,6 +68,10 @@ class EngineConfig:
     # cross the link in fewer bytes (bfloat16 activations: about 0.66) for HBM-bound coding
     # kernels and one wire buffer per staging and restore slot, allocated on first use.
     wire_coding: str = "auto"
+    # Cap on the device bytes of the wire buffers (0: none). Where the buffers would pass it, or
+    # their allocation fails, segments cross raw (stats "wire_fallbacks") and the engine tries
+    # again at the next forward; the step never fails for want of them.
+    wire_device_limit: int = 0
     copy_kernel_blocks: int = 16
     d2h_engine: int = 0
     h2d_engine: int = 0
@@ -99,6 +107,23 @@ class EngineConfig:
     # them only sends them out and straight back; keeping them trades device memory for link
     # time in both directions. Restores stay bitwise: a kept save is the saved tensor itself.
     keep_last_blocks: int = 0
+    # Each consumer of a deduplicated save (one payload saved by several autograd nodes) gets a
+    # tensor of its own, as the reference's restore does: while another consumer is still to
+    # take it, a take is a device copy, and the last consumer gets the restored tensor itself.
+    # False hands all of them the one restored tensor, as autograd does without hooks.
+    private_restores: bool = True
+
+    def __post_init__(self) -> None:
+        if self.link not in LINKS:
+            raise ValueError(f"link must be one of {LINKS}, got {self.link!r}")
+        if self.wire_coding not in WIRE_CODINGS:
+            raise ValueError(f"wire_coding must be one of {tuple(WIRE_CODINGS)}, got {self.wire_coding!r}")
+        for name in ("stage_slot_bytes", "stage_slots", "restore_slots", "host_limit_bytes", "host_chunk_bytes",
+                     "copy_kernel_blocks", "d2h_engine", "h2d_engine", "prefetch_depth", "keep_last_blocks",
+                     "wire_device_limit"):
+            value = getattr(self, name)
+            if isinstance(value, bool) or not isinstance(value, int) or value < 0:
+                raise ValueError(f"{name} must be a non-negative integer, got {value!r}")
 
     def native(self) -> _native.MoConfig:
         cfg = _native.MoConfig()
@@ -117,23 +142,21 @@ class EngineConfig:
             | (_native.MO_FLAG_PACK_NT_LOAD if self.pack_nt_load else 0)
             | (0 if self.unpack_nt_load else _native.MO_FLAG_UNPACK_CACHED_LOAD)
             | (0 if self.unpack_nt_store else _native.MO_FLAG_UNPACK_CACHED_STORE)
-            | {"off": 0, "on": _native.MO_FLAG_WIRE_CODING, "auto": _native.MO_FLAG_WIRE_AUTO}.get(self.wire_coding, 0)
+            | WIRE_CODINGS[self.wire_coding]
         )
-        if self.link not in ("sdma", "hipdma"):
-            raise ValueError(f"link must be 'sdma' or 'hipdma', got {self.link!r}")
-        if self.wire_coding not in ("off", "on", "auto"):
-            raise ValueError(f"wire_coding must be 'off', 'on' or 'auto', got {self.wire_coding!r}")
         cfg.copy_kernel_blocks = self.copy_kernel_blocks
         cfg.d2h_engine = self.d2h_engine
         cfg.h2d_engine = self.h2d_engine
+        cfg.wire_device_limit = self.wire_device_limit
         return cfg
 
 
 class _EntryState:
-    __slots__ = ("refs", "dtype", "payload_shape", "stride", "nbytes", "restored", "restored_version")
+    __slots__ = ("refs", "readers", "dtype", "payload_shape", "stride", "nbytes", "restored", "restored_version")
 
     def __init__(self, dtype, payload_shape, stride, nbytes):
         self.refs = 0
+        self.readers = 0  # references whose restore goes to an autograd consumer
         self.dtype = dtype
         self.payload_shape = payload_shape
         self.stride = stride
@@ -197,7 +220,7 @@ class OffloadEngine:
                 raise RuntimeError(f"engine entry index {idx} out of sync with group {gid}")
             entry = _EntryState(source.dtype, tuple(source.shape), tuple(source.stride()),
                                 source.numel() * (2 if narrow else source.element_size()))
-            entry.refs = 1
+            entry.refs = entry.readers = 1
             group.entries.append(entry)
             group.live += 1
             if self.config.batch_packs:
@@ -217,19 +240,21 @@ class OffloadEngine:
                 self._hold()
             return None if gid == _native.NO_GROUP else gid
 
-    def acquire(self, gid: int, idx: int) -> bool:
-        """Add a reference to a live entry (a deduplicated save). False if it is gone."""
+    def acquire(self, gid: int, idx: int, reader: bool = True) -> bool:
+        """Add a reference to a live entry (a deduplicated save, or with ``reader=False`` an
+        input that a recomputed save reads). False if it is gone."""
 
         with self._lock:
             group = self._groups.get(gid)
             if group is None or idx >= len(group.entries) or group.entries[idx].refs <= 0:
                 return False
             group.entries[idx].refs += 1
+            group.entries[idx].readers += 1 if reader else 0
             group.live += 1
             return True
 
-    def drop(self, gid: int, idx: int) -> None:
-        """Remove one reference; release the group when none is left."""
+    def drop(self, gid: int, idx: int, reader: bool = True) -> None:
+        """Remove one reference (as taken); release the group when none is left."""
 
         with self._lock:
             group = self._groups.get(gid)
@@ -237,6 +262,7 @@ class OffloadEngine:
                 return
             entry = group.entries[idx]
             entry.refs -= 1
+            entry.readers -= 1 if reader else 0
             group.live -= 1
             if entry.refs <= 0:
                 entry.restored = None
@@ -313,15 +339,17 @@ class OffloadEngine:
             _native.check("mo_equal_discard", self._lib.mo_equal_discard(self._handle, ticket))
 
     # ------------------------------------------------------------------ backward
-    def restore(self, gid: int, idx: int, stream: int) -> torch.Tensor:
-        """Return entry ``idx`` of group ``gid`` as a fresh device tensor of its packed layout."""
+    def restore(self, gid: int, idx: int, stream: int, reader: bool = True) -> torch.Tensor:
+        """Return entry ``idx`` of group ``gid`` as a device tensor of its packed layout: for an
+        autograd consumer (``reader``) one of its own, for an internal read (``reader=False``,
+        a recomputed save's input, read at once) possibly the one other readers get too."""
 
         with self._lock:
             group = self._groups.get(gid)
             if group is None:
                 raise RuntimeError(f"offloaded group {gid} was already released")
             entry = group.entries[idx]
-            cached = self._take_cached(entry)
+            cached = self._take_cached(entry, reader)
             if cached is not None:
                 return cached
             n = len(group.entries)
@@ -339,7 +367,7 @@ class OffloadEngine:
                 self._hold()
             if self.config.prefetch:
                 self._prefetch_after(gid, stream, max(1, self.config.prefetch_depth))
-            return self._take_cached(entry)
+            return self._take_cached(entry, reader)
 
     def prefetch(self, gid: int, stream: int, ahead: bool = False) -> None:
         """Queue H2D of group ``gid``'s segments into free restore slots; with ``ahead``, also of
@@ -369,17 +397,27 @@ class OffloadEngine:
             ids = (ctypes.c_uint64 * len(order))(*order)
             _native.check("mo_prefetch_groups", self._lib.mo_prefetch_groups(self._handle, ids, len(order), stream))
 
-    @staticmethod
-    def _take_cached(entry: _EntryState) -> torch.Tensor | None:
+    def _take_cached(self, entry: _EntryState, reader: bool) -> torch.Tensor | None:
+        """The cached restore of ``entry``, handed out once per reference.
+
+        The last reference takes the tensor itself. An autograd consumer while another is still
+        to come gets a device copy (``private_restores``), so that no consumer can see another's
+        in-place write, as with the reference's restore, which copies for each unpack. Internal
+        reads share the cached tensor; a take finds it changed (its version moved) only if a
+        consumer wrote it in place, and then the entry is restored again from its host copy."""
+
         tensor = entry.restored
         if tensor is None:
             return None
         if tensor._version != entry.restored_version:
-            # Someone modified the shared restored copy in place: restore afresh.
             entry.restored = None
             return None
         if entry.refs <= 1:
             entry.restored = None
+            return tensor
+        if reader and entry.readers > 1 and self.config.private_restores:
+            copy = torch.empty_strided(entry.payload_shape, entry.stride, dtype=entry.dtype, device=self.device)
+            return copy.copy_(tensor)
         return tensor
 
     def _predict_next(self, gid: int) -> int | None:

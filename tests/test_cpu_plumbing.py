@@ -253,11 +253,13 @@ class _StubEngine:
     def __init__(self):
         self.results = {}
         self.discarded = []
+        self.acquired = []  # (group, entry, reader) of every extra reference taken
 
-    def acquire(self, gid, idx):
+    def acquire(self, gid, idx, reader=True):
+        self.acquired.append((gid, idx, reader))
         return True
 
-    def drop(self, gid, idx):
+    def drop(self, gid, idx, reader=True):
         pass
 
     def equal(self, a, b, stream):
@@ -310,6 +312,8 @@ def test_recomputed_products_are_found_from_the_graph() -> None:
     a4 = 4.0 * t1
     d4 = ctx._derive(a4)
     assert isinstance(d4, _DerivedTensor) and d4.scalar == 4.0 and len(d4.inputs) == 1
+    # the replay only reads its input: its reference is not a reader's
+    assert ctx.engine.acquired[-1] == (1, 0, False) and not d4.inputs[0].reader
     ctx._remember(a4, d4)
     p = a4 * s
     dp = ctx._derive(p)
@@ -380,6 +384,8 @@ def test_equal_casts_are_aliased_only_after_the_bytes_compare_equal() -> None:
     alias = ctx._alias(first, _cast_origin(first), 0)
     assert isinstance(alias, _CheckedAlias) and alias.tensor is first and ctx._pending == [alias]
     assert alias.settle(False) and alias.tensor is None and alias.target.group == h.group
+    # the alias hands its target's restore to autograd: a reader's reference
+    assert ctx.engine.acquired[-1] == (7, 0, True) and alias.target.reader
     # a write between the casts that autograd does not see: the bytes differ, the save stays
     ctx = _derive_context()
     second = tokens.float()
@@ -414,6 +420,54 @@ def test_equal_casts_are_aliased_only_after_the_bytes_compare_equal() -> None:
     ctx._pending.clear()
     del alias
     assert ctx.engine.discarded == [1]
+
+
+def test_each_reader_of_a_deduplicated_entry_gets_its_own_tensor() -> None:
+    """``OffloadEngine._take_cached``: an entry restored once is handed out once per reference.
+    An autograd consumer while another reader is still to take it gets a copy of its own (the
+    reference's restore copies for every unpack, training/activation_offload.py:75-77); the last
+    reader gets the restored tensor itself; a replay's read shares it; a take after an in-place
+    write to the cached tensor finds it stale."""
+
+    from moss_offload.engine import EngineConfig, OffloadEngine, _EntryState
+
+    def engine(private):
+        e = OffloadEngine.__new__(OffloadEngine)
+        e.config, e.device = EngineConfig(private_restores=private), torch.device("cpu")
+        return e
+
+    padded = torch.arange(64, dtype=torch.float32).as_strided((3, 5), (8, 1))  # gaps between rows
+
+    def entry(readers, internal):
+        ent = _EntryState(torch.float32, (3, 5), (8, 1), 60)
+        ent.readers, ent.refs = readers, readers + internal
+        ent.restored = torch.empty_strided((3, 5), (8, 1))
+        ent.restored.copy_(padded)
+        ent.restored_version = ent.restored._version
+        return ent
+
+    e = engine(True)
+    ent = entry(readers=2, internal=1)
+    cached = ent.restored
+    first = e._take_cached(ent, reader=True)  # another reader is still to come: a copy
+    assert first is not cached and first.untyped_storage().data_ptr() != cached.untyped_storage().data_ptr()
+    assert first.stride() == (8, 1) and torch.equal(first, padded)
+    replay = e._take_cached(ent, reader=False)  # a replay's read shares the cached tensor
+    assert replay is cached
+    ent.readers, ent.refs = 1, 2  # the first reader's node ran and let go of its save
+    last = e._take_cached(ent, reader=True)
+    assert last is cached and ent.restored is cached  # still cached for the replay's reference
+    ent.refs = 1
+    assert e._take_cached(ent, reader=False) is cached and ent.restored is None
+    # an in-place write to a cached tensor is seen at the next take: restore again
+    ent = entry(readers=2, internal=0)
+    with torch.no_grad():
+        ent.restored.add_(1.0)
+    assert e._take_cached(ent, reader=True) is None and ent.restored is None
+    # private_restores=False: every reader shares the one restored tensor
+    e = engine(False)
+    ent = entry(readers=2, internal=0)
+    assert e._take_cached(ent, reader=True) is ent.restored
 
 
 def test_hook_features_probe_reports_each_graph_reading_feature() -> None:

@@ -580,3 +580,79 @@ def test_wire_coding_is_skipped_on_the_hip_stream_link() -> None:
     engine.drop(gid, idx)
     engine.synchronize()
     engine.close()
+
+
+def test_wire_buffers_past_the_device_limit_fall_back_to_raw_segments() -> None:
+    """Wire buffers are an optimisation: where they would pass ``wire_device_limit`` (or their
+    allocation fails) segments cross raw, the step goes on, and the next forward tries again."""
+
+    device = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(13)
+    engine = _engine(wire_coding="on", wire_device_limit=1)
+    try:
+        for forward in range(2):
+            handles = []
+            for _ in range(3):
+                t = torch.randn(600_000, generator=g).to(torch.bfloat16).to(device)
+                handles.append((t, *engine.pack(t, stream)))
+                engine.commit(stream)
+            _restore_and_check(engine, handles, device, range(len(handles) - 1, -1, -1))
+            for _, gid, idx in handles:
+                engine.drop(gid, idx)
+            engine.synchronize()
+            st = engine.stats()
+            assert st["wire_segments"] == 0 and st["wire_fallbacks"] >= 3 * (forward + 1), st["wire_fallbacks"]
+            assert st["device_ring_bytes"] == (3 + 2) * 2 * MiB  # no wire buffer was kept
+            assert st["bytes_d2h"] >= st["bytes_packed"] and st["copy_failures"] == 0
+    finally:
+        engine.close()
+    # a limit the buffers fit in codes as usual
+    engine = _engine(wire_coding="on", wire_device_limit=1 << 30)
+    try:
+        t = torch.randn(600_000, generator=g).to(torch.bfloat16).to(device)
+        gid, idx = engine.pack(t, stream)
+        engine.commit(stream)
+        assert_bitwise(engine.restore(gid, idx, stream), t)
+        engine.drop(gid, idx)
+        engine.synchronize()
+        assert engine.stats()["wire_segments"] == 1 and engine.stats()["wire_fallbacks"] == 0
+    finally:
+        engine.close()
+
+
+def test_resident_coded_slot_restored_on_a_second_stream() -> None:
+    """A wire-coded segment decoded into its restore slot by an unpack on one stream, then
+    unpacked again from the slot on another stream (a retained graph's second backward there):
+    the second stream is ordered after the first one's decode and scatter, and the slot's next
+    refill after both streams' reads."""
+
+    device = torch.device("cuda", 0)
+    main = torch.cuda.current_stream(device)
+    side = torch.cuda.Stream(device=device)
+    g = torch.Generator(device="cpu").manual_seed(17)
+    engine = _engine(wire_coding="on", staged_restore=False, prefetch=False)
+    try:
+        tensors = [torch.randn(450_000, generator=g).to(torch.bfloat16).to(device) for _ in range(4)]
+        handles = []
+        for t in tensors:
+            handles.append((t, *engine.pack(t, main.cuda_stream)))
+            engine.commit(main.cuda_stream)
+        engine.synchronize()
+        t, gid, idx = handles[-1]
+        first = engine.restore(gid, idx, main.cuda_stream)  # fetch, decode and scatter on main
+        side.wait_stream(main)  # the restored tensor's allocation is main's; the slot is not
+        with torch.cuda.stream(side):
+            second = engine.restore(gid, idx, side.cuda_stream)  # the resident slot, read on side
+            second_bits = second.clone()
+        main.wait_stream(side)
+        assert_bitwise(first, t)
+        assert_bitwise(second_bits, t)
+        # the other groups reuse the two restore slots after both reads
+        _restore_and_check(engine, handles, device, [2, 1, 0])
+        assert engine.stats()["wire_segments"] == 4
+        for _, gid_, idx_ in handles:
+            engine.drop(gid_, idx_)
+        engine.synchronize()
+    finally:
+        engine.close()
