@@ -41,7 +41,14 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 # legs whose steps take seconds: timed over --steps-big steps
-BIG_LEGS = ("A4", "C5U", "C5P", "S5", "F3", "F3S")
+BIG_LEGS = ("A4", "B4", "B4R", "C5U", "C5P", "S5", "F3", "F3S")
+# legs whose hooks-off and engine modes are timed in alternating rounds (--rounds-big), so that
+# drift over the run falls on both alike; their exposed time is reported per round
+INTERLEAVED = ("A4", "B4", "B4R", "C5U", "C5P")
+# torch's pinned host allocator (the reference hooks' pin_memory) fails after about 55.6 GiB on
+# the MI355X box (raw hipHostMalloc after about 65 GiB); a reference mode whose per-save pins
+# would pass this is not attempted
+PINNED_CAP_BYTES = 55 << 30
 for _p in (ROOT / "moss-image_amd", ROOT):
     if str(_p) not in sys.path:
         sys.path.insert(0, str(_p))
@@ -774,7 +781,7 @@ def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
         return start.elapsed_time(stop) / 1e3 / iters
 
     shapes = {}
-    block = {"hip": 0.0, "fused": 0.0, "eager": 0.0}
+    block = {"hip": 0.0, "fused": 0.0, "fused_lds": 0.0, "eager": 0.0}
     block_flop = 0.0
     for name, ((out_f, in_f), count) in C5_GEMMS.items():
         x = torch.randn(rows, in_f, device=device, generator=g).to(torch.bfloat16)
@@ -783,7 +790,12 @@ def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
         s = torch.empty(out_f, device=device).uniform_(1e-3, 2e-2, generator=g)
         assert qk.resolve_backend("auto", x, w, s, torch.bfloat16) == "hip"
         flop = 2.0 * rows * in_f * out_f
+        qk.set_kernel("lds")  # the large tile decoding the weight into LDS, for comparison
+        t_lds = {"fused_lds_fwd": timed(lambda: qk.int8_linear_forward(x, w, s, path="fused")),
+                 "fused_lds_bwd": timed(lambda: qk.int8_linear_backward(dy, w, s, x.shape, path="fused"))}
+        qk.set_kernel("registers")
         t = {
+            **t_lds,
             "hip_fwd": timed(lambda: qk.int8_linear_forward(x, w, s)),
             "hip_bwd": timed(lambda: qk.int8_linear_backward(dy, w, s, x.shape)),
             "fused_fwd": timed(lambda: qk.int8_linear_forward(x, w, s, path="fused")),
@@ -804,10 +816,12 @@ def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
         shapes[name] = rec
         block["hip"] += count * (t["hip_fwd"] + t["hip_bwd"])
         block["fused"] += count * (t["fused_fwd"] + t["fused_bwd"])
+        block["fused_lds"] += count * (t["fused_lds_fwd"] + t["fused_lds_bwd"])
         block["eager"] += count * (t["eager_fwd"] + t["eager_bwd"])
         block_flop += count * 2 * flop
         log(f"int8 GEMM {name} ({out_f}x{in_f}, {rows} rows): hip fwd {rec['hip_fwd_tflops']} bwd "
             f"{rec['hip_bwd_tflops']} | fused fwd {rec['fused_fwd_tflops']} bwd {rec['fused_bwd_tflops']} | "
+            f"fused (LDS decode) fwd {rec['fused_lds_fwd_tflops']} bwd {rec['fused_lds_bwd_tflops']} | "
             f"eager fwd {rec['eager_fwd_tflops']} bwd {rec['eager_bwd_tflops']} TFLOP/s")
         del x, dy, w, s, wd, yh, ye, gh, ge
     achieved = block_flop / block["hip"] / 1e12
@@ -816,6 +830,7 @@ def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
         "block_ms": {k: round(v * 1e3, 3) for k, v in block.items()},
         "block_speedup_vs_eager": round(block["eager"] / block["hip"], 4),
         "fused_block_speedup_vs_eager": round(block["eager"] / block["fused"], 4),
+        "fused_lds_block_speedup_vs_eager": round(block["eager"] / block["fused_lds"], 4),
         "library_rows": qk.LIBRARY_ROWS,
         "library_weight_elements": qk.LIBRARY_WEIGHT,
         "roofline": {"bound": "mfma",
@@ -1031,6 +1046,7 @@ def run(args) -> dict:
                                                  args.gradacc_threads)
         torch.cuda.empty_cache()
 
+    c4 = {}
     c5 = {}
     full = {}
 
@@ -1050,6 +1066,17 @@ def run(args) -> dict:
             return model, opt, inputs, config3_forward, "B"
         if name == "A4":
             return model, opt, make_inputs(device, C4_GRID, C4_TEXT, seed=4), config3_forward, "A"
+        if name in ("B4", "B4R"):
+            # config 4 (2048^2 + 4096 text) not checkpointed, so the host link sets the pace: on
+            # --b4-layers blocks, whose coded saves fit the pinned-memory cap, and on
+            # --b4-ref-layers, where the reference hooks' per-save pins fit it too
+            layers = model.layers
+            count = args.b4_layers if name == "B4" else args.b4_ref_layers
+            model.layers = torch.nn.ModuleList(list(layers)[:count])
+            cleanups.append(lambda: setattr(model, "layers", layers))
+            if "c4" not in c4:
+                c4["c4"] = make_inputs(device, C4_GRID, C4_TEXT, seed=4)
+            return model, opt, c4["c4"], config3_forward, "B"
         if name in ("C5U", "C5P"):
             if not c5:
                 c5["model"] = build_c5_model(device, args.layers, args.int8_backend)
@@ -1158,45 +1185,80 @@ def run(args) -> dict:
         modes = list(args.modes)
         if regime_name == "AH" and "engine" in modes:
             modes.insert(modes.index("engine") + 1, "engine_hipdma")
-        for mode in modes:
-            if regime_name == "BK" and mode == "reference":
-                continue  # the reference offloads every block
+        if regime_name == "BK" and "reference" in modes:
+            modes.remove("reference")  # the reference offloads every block
+        if "reference" in modes:
+            # the reference pins one host tensor per save, dups included, each rounded up to a
+            # power of two by torch's caching host allocator
+            pins = sum(1 << max(0, (r.payload_bytes - 1).bit_length()) for r in manifest.records
+                       if not r.resident and r.payload_bytes)
+            if pins > PINNED_CAP_BYTES:
+                modes.remove("reference")
+                entry["reference"] = {"skipped": f"needs {pins / 2**30:.1f} GiB of pinned host memory per step "
+                                      f"(one pin per save), over the {PINNED_CAP_BYTES / 2**30:.0f} GiB a process "
+                                      f"can pin on this box", "pinned_bytes_needed": pins}
+                log(f"{regime_name}/reference skipped: {entry['reference']['skipped']}")
+        rounds = max(1, args.rounds_big) if regime_name in INTERLEAVED else 1
+        times = {mode: [] for mode in modes}
+        peaks = {mode: 0 for mode in modes}
+        failed = {}
+
+        def enter(mode, first):
             configure_mode(wl_model, mode, regime)
             engine = mode_engine(device, mode) or get_engine(device)
             engine.config.keep_last_blocks = args.keep_last_blocks if regime_name == "BK" else 0
-            # wire buffers a previous leg allocated (coding ran there) are freed, so each leg's
-            # ring bytes are its own
-            engine.trim()
-            # marks the start of each leg and mode in a kernel trace, and scales rocprofv3
-            # FETCH_SIZE / WRITE_SIZE to bytes in a counter run
-            calibration_copy(device, torch.cuda.current_stream(device).cuda_stream)
-            engine.reset_stats()
-            moss_offload.reset_hook_counters()
-            if streamer is not None:
-                streamer.reset_stats()
-            failure = None
-            try:
-                seconds, peak = time_steps(wl_model, wl_opt, wl_inputs, steps, warmup, f"{regime_name}/{mode}", forward,
-                                           host_work_s)
-            except RuntimeError as exc:  # e.g. the reference hooks exhausting pinned host memory
-                import traceback
+            if first:
+                # wire buffers a previous leg allocated (coding ran there) are freed, so each
+                # leg's ring bytes are its own
+                engine.trim()
+                # marks the start of each leg and mode in a kernel trace, and scales rocprofv3
+                # FETCH_SIZE / WRITE_SIZE to bytes in a counter run
+                calibration_copy(device, torch.cuda.current_stream(device).cuda_stream)
+                engine.reset_stats()
+                moss_offload.reset_hook_counters()
+                if streamer is not None:
+                    streamer.reset_stats()
+            return engine
 
-                log(f"{regime_name}/{mode} failed: {exc}\n{traceback.format_exc(limit=-4)}")
-                failure = str(exc).splitlines()[0]
-            if failure is not None:
-                # the traceback held the failed step's graph, and with it every pinned copy it
-                # made; they are freed now, and the cached pinned blocks go back to the host
-                entry[mode] = {"error": failure}
-                wl_opt.zero_grad(set_to_none=True)
-                gc.collect()
-                torch.cuda.synchronize()
-                torch._C._host_emptyCache()
+        for rnd in range(rounds):
+            for mode in modes:
+                if mode in failed or (mode == "reference" and rnd > 0):  # one round of the baseline
+                    continue
+                enter(mode, rnd == 0)
+                try:
+                    seconds, peak = time_steps(wl_model, wl_opt, wl_inputs, steps, warmup if rnd == 0 else 0,
+                                               f"{regime_name}/{mode}" + (f" round {rnd + 1}/{rounds}" if rounds > 1 else ""),
+                                               forward, host_work_s)
+                except RuntimeError as exc:  # e.g. the reference hooks exhausting pinned host memory
+                    import traceback
+
+                    log(f"{regime_name}/{mode} failed: {exc}\n{traceback.format_exc(limit=-4)}")
+                    failed[mode] = str(exc).splitlines()[0]
+                    # the traceback held the failed step's graph, and with it every pinned copy it
+                    # made; they are freed now, and the cached pinned blocks go back to the host
+                    wl_opt.zero_grad(set_to_none=True)
+                    gc.collect()
+                    torch.cuda.synchronize()
+                    torch._C._host_emptyCache()
+                    continue
+                times[mode].append(seconds)
+                peaks[mode] = max(peaks[mode], peak)
+                if mode == "reference":
+                    torch._C._host_emptyCache()
+
+        for mode in modes:
+            if mode in failed:
+                entry[mode] = {"error": failed[mode]}
                 continue
-            record = {"s_per_it": seconds, "peak_device_bytes": peak}
+            engine = mode_engine(device, mode) or get_engine(device)
+            timed = times[mode]
+            record = {"s_per_it": sum(timed) / len(timed), "peak_device_bytes": peaks[mode]}
+            if len(timed) > 1:
+                record["s_per_it_rounds"] = timed
+            n = warmup + steps * len(timed)  # stats were reset before the first warmup step
             if streamer is not None:
                 torch.cuda.synchronize()
                 ss = streamer.stats()
-                n = steps + warmup
                 record["stream"] = {
                     "fills_per_step": ss["fills"] / n,
                     "bytes_per_step": ss["bytes"] / n,
@@ -1212,7 +1274,6 @@ def run(args) -> dict:
             if mode in ("engine", "engine_hipdma"):
                 engine.synchronize()
                 st = engine.stats()
-                n = steps + warmup  # reset before warmup: stats cover warmup + timed steps
                 record["link"] = engine.link_name()
                 record["hook_counters_per_step"] = {k: v / n for k, v in moss_offload.hook_counters().items()}
                 # the staging and restore rings (and their wire buffers once coding ran) are the
@@ -1220,7 +1281,7 @@ def run(args) -> dict:
                 rings = st["device_ring_bytes"]
                 record.update(
                     engine_ring_bytes=rings,
-                    peak_device_bytes_with_rings=peak + rings,
+                    peak_device_bytes_with_rings=peaks[mode] + rings,
                     d2h_bytes_per_step=st["bytes_d2h"] / n,
                     h2d_bytes_per_step=st["bytes_h2d"] / n,
                     d2h_copies_per_step=st["d2h_copies"] / n,
@@ -1238,6 +1299,7 @@ def run(args) -> dict:
                     unpack_bytes_per_launch=st["timed_unpack_bytes"] / max(st["timed_unpack_launches"], 1),
                     wire_segments_per_step=st["wire_segments"] / n,
                     wire_ratio=(st["wire_bytes"] / st["wire_raw_bytes"]) if st["wire_raw_bytes"] else None,
+                    wire_fallbacks=st["wire_fallbacks"],
                     pack_launches_per_step=st["timed_pack_launches"] / n,
                     unpack_launches_per_step=st["timed_unpack_launches"] / n,
                     pack_hbm_bytes_per_step=st["timed_pack_hbm_bytes"] / n,
@@ -1251,17 +1313,30 @@ def run(args) -> dict:
                     host_pinned_peak_bytes=st["host_bytes_peak"],
                 )
                 engine.trim()
-            if mode == "reference":
-                torch._C._host_emptyCache()
             entry[mode] = record
         none = entry.get("none", {}).get("s_per_it")
         for name in ("engine", "engine_hipdma"):
             eng = entry.get(name)
-            if none is not None and eng is not None and "s_per_it" in eng:
-                copy_s = eng["d2h_s_per_step"] + eng["h2d_s_per_step"]
-                exposed = eng["s_per_it"] - none
-                eng["hidden_fraction"] = min(1.0, max(0.0, 1.0 - exposed / copy_s)) if copy_s > 0 else None
-                eng["exposed_s"] = exposed
+            if none is None or eng is None or "s_per_it" not in eng:
+                continue
+            copy_s = eng["d2h_s_per_step"] + eng["h2d_s_per_step"]
+
+            def hidden(exposed):
+                return min(1.0, max(0.0, 1.0 - exposed / copy_s)) if copy_s > 0 else None
+
+            eng["exposed_s"] = eng["s_per_it"] - none
+            eng["hidden_fraction"] = hidden(eng["exposed_s"])
+            pairs = list(zip(times.get(name, []), times.get("none", [])))
+            if len(pairs) > 1:
+                # per round: the engine's steps against the hooks-off steps timed just before them
+                per_round = sorted(e - o for e, o in pairs)
+                mid = len(per_round) // 2
+                median = per_round[mid] if len(per_round) % 2 else (per_round[mid - 1] + per_round[mid]) / 2
+                eng["exposed_s_rounds"] = [e - o for e, o in pairs]
+                eng["exposed_s_median"] = median
+                eng["exposed_s_range"] = [per_round[0], per_round[-1]]
+                eng["hidden_fraction_median"] = hidden(median)
+                eng["hidden_fraction_range"] = [hidden(per_round[-1]), hidden(per_round[0])]
         ref = entry.get("reference")
         if none is not None and ref is not None and "s_per_it" in ref:
             ref["exposed_s"] = ref["s_per_it"] - none
@@ -1284,10 +1359,17 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--steps-b", type=int, default=5, help="timed steps of the legs other than A")
     parser.add_argument("--warmup-b", type=int, default=2)
-    parser.add_argument("--steps-big", type=int, default=3,
-                        help="timed steps of the config-4/5 and full-parameter legs (2.3-4.7 s steps)")
+    parser.add_argument("--steps-big", type=int, default=2,
+                        help="timed steps per round of the config-4/5 and full-parameter legs (2.1-4.7 s steps)")
+    parser.add_argument("--rounds-big", type=int, default=4,
+                        help="rounds of the interleaved legs (A4, B4, B4R, C5U, C5P): hooks off and engine take "
+                             "turns, --steps-big steps each; the reference hooks time one round")
     parser.add_argument("--warmup-big", type=int, default=1)
-    parser.add_argument("--regimes", default="M,K,Q,A,B,BR,AH,A4,C5U,C5P",
+    parser.add_argument("--b4-layers", type=int, default=24,
+                        help="blocks of the B4 leg (config 4 not checkpointed): its coded saves fit the pinned cap")
+    parser.add_argument("--b4-ref-layers", type=int, default=6,
+                        help="blocks of the B4R leg, where the reference hooks' per-save pins fit the cap too")
+    parser.add_argument("--regimes", default="M,K,Q,A,B,BR,AH,A4,B4,B4R,C5U,C5P",
                         help="M = config-2 block microbench, K = 28 MiB gathers/scatters back to back and after "
                         "other kernels (a GEMM with a large output, a fill, a read), Q = config-5 int8 GEMMs "
                         "(HIP vs eager), "
@@ -1297,7 +1379,9 @@ def main() -> int:
                         "streams), BK = regime B keeping the last "
                         "--keep-last-blocks blocks' saves resident, G = host gradient accumulation "
                         "(full-parameter config-3 dims, 2 micro-batches: device / engine / reference stash), "
-                        "A4 = config 4 (2048^2, regime A), C5U/C5P = config 5 unpacked / packed (regime A), "
+                        "A4 = config 4 (2048^2, regime A), B4/B4R = config 4 not checkpointed on --b4-layers / "
+                        "--b4-ref-layers blocks (the host link sets the pace), "
+                        "C5U/C5P = config 5 unpacked / packed (regime A), "
                         "S5 = config 5 packed with every block streamed from pinned host masters, "
                         "F3/F3S = full-parameter training at config-3 dims, resident / every block on the trainable ring")
     parser.add_argument("--micro-iters", type=int, default=1000)

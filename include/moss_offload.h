@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 13
+#define MO_ABI_VERSION 15
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -285,6 +285,17 @@ int mo_prefetch_groups(mo_engine* engine, const uint64_t* groups, uint32_t n, ui
 int mo_unpack(mo_engine* engine, uint64_t group, const uint64_t* dst, uint32_t n,
               uint64_t stream);
 
+/* Restore groups[0] as mo_unpack does (its entries' addresses are dst[0 .. counts[0])), then
+ * each further groups[k] (the next counts[k] addresses) only if every segment it needs can be
+ * read now without waiting for a copy: resident in a restore slot with its H2D landed, or still
+ * in its staging slot. unpacked[k] is set to 1 for each group restored. The first group's last
+ * segment and the further groups are scattered together, in as few kernel launches as their
+ * pieces allow (small groups, such as the inputs of checkpointed blocks, then share one large
+ * launch). No reference counterpart: the reference restores one saved tensor per unpack
+ * (activation_offload.py:136-147). */
+int mo_unpack_groups(mo_engine* engine, const uint64_t* groups, const uint64_t* dst,
+                     const uint32_t* counts, uint32_t n, uint64_t stream, uint32_t* unpacked);
+
 /* Drop a group: its pinned host memory returns to the pool once every copy using it ended. */
 int mo_release(mo_engine* engine, uint64_t group);
 
@@ -417,10 +428,24 @@ int mo_int8_linear_forward(uint64_t x, uint64_t w, uint64_t scale, uint64_t bias
                            uint32_t in_features, uint32_t out_features, uint64_t stream);
 
 /* dx[rows][in] = dy[rows][out] . decode(w): the input gradient of the frozen int8 linear (no
- * weight gradient). Same layouts and constraints. Replaces _int8_linear_backward_kernel
+ * weight gradient). Same layouts and constraints. `workspace` (device, 16-byte aligned, at
+ * least mo_int8_backward_workspace_bytes; 0 = none) receives the transposed int8 weight, which
+ * the large-tile kernel reads with the reduction contiguous; without one the large tile decodes
+ * the weight through LDS instead (slower, same results). Replaces _int8_linear_backward_kernel
  * (quant_kernels.py:160-209). */
 int mo_int8_linear_backward(uint64_t dy, uint64_t w, uint64_t scale, uint64_t dx, uint32_t rows,
-                            uint32_t in_features, uint32_t out_features, uint64_t stream);
+                            uint32_t in_features, uint32_t out_features, uint64_t workspace,
+                            uint64_t workspace_bytes, uint64_t stream);
+uint64_t mo_int8_backward_workspace_bytes(uint32_t in_features, uint32_t out_features);
+
+/* Which kernel takes the large (256 x 256) tiles of the two calls above, process-wide:
+ * MO_INT8_KERNEL_REGISTERS (default; reduction a multiple of 64): each wave decodes its columns'
+ * int8 weights in registers into the MFMA operand, and the LDS carries only the activations;
+ * MO_INT8_KERNEL_LDS: the weight tile is decoded into LDS and shared by the waves. Both give
+ * the same results bit for bit; the switch exists to measure one against the other. No
+ * reference counterpart (the reference has one Triton kernel per direction). */
+enum { MO_INT8_KERNEL_REGISTERS = 0, MO_INT8_KERNEL_LDS = 1 };
+int mo_int8_set_kernel(uint32_t kernel);
 
 /* ---- host gradient accumulation (training/fused_adafactor.py:327-369) -------------------- */
 

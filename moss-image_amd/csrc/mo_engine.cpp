@@ -897,74 +897,35 @@ struct Engine {
     return 0;
   }
 
-  int unpack(uint64_t gid, const uint64_t* dst, uint32_t n, hipStream_t stream) {
+  // Restore group gids[0] into dst[0 .. counts[0]) (an entry with a zero address is skipped),
+  // fetching what is missing; then each further group gids[k], into the next counts[k]
+  // addresses, if every segment it needs can be read right now without a wait: resident in a
+  // restore slot with its H2D landed, or still in its staging slot. unpacked[k] says which were.
+  // The first group's segments are scattered one by one, each flushed and its slot released
+  // before the next segment may fetch (and so take a slot); its last segment's pieces and the
+  // further groups' go out together, in as few launches as the pieces allow. The further
+  // groups never fetch, so no slot with a scatter still pending is ever refilled.
+  int unpack_groups(const uint64_t* gids, const uint64_t* dst, const uint32_t* counts, uint32_t n,
+                    hipStream_t stream, uint32_t* unpacked) {
     if (int rc = check_link()) return rc;
     link_behind = false;
     busy_wraps = 0;
     wire_unavailable = false;  // the next forward may try to allocate the wire buffers again
     process_pending(false);
-    Group* g = find(gid);
-    if (!g) return fail(MO_E_INVALID, "mo_unpack: unknown group " + std::to_string(gid));
-    if (n != g->entries.size())
-      return fail(MO_E_INVALID, "mo_unpack: group " + std::to_string(gid) + " has " +
-                                    std::to_string(g->entries.size()) + " entries, got " + std::to_string(n));
-    if (g->open) {
-      uint64_t id;
-      if (int rc = commit(stream, &id)) return rc;
+    for (uint32_t k = 0; k < n; ++k) {
+      unpacked[k] = 0;
+      const Group* g = find(gids[k]);
+      if (!g) return fail(MO_E_INVALID, "mo_unpack: unknown group " + std::to_string(gids[k]));
+      if (counts[k] != g->entries.size())
+        return fail(MO_E_INVALID, "mo_unpack: group " + std::to_string(gids[k]) + " has " +
+                                      std::to_string(g->entries.size()) + " entries, got " + std::to_string(counts[k]));
     }
-    std::string err;
-    for (uint32_t si = 0; si < g->segs.size(); ++si) {
-      Segment& seg = g->segs[si];
-      bool any = false;
-      for (const Piece& p : seg.pieces) any = any || dst[p.entry] != 0;
-      if (!any) continue;
-      RestoreSlot* r = nullptr;
-      const char* src = nullptr;
-      if (resident(*g, si)) {
-        if (seg.prefetched) st.prefetch_hits++;
-        r = &restore[seg.restore_slot];
-      } else if (staged(seg, stream)) {
-        // Still in the staging slot, stream-ordered after its pack kernels: no H2D.
-        src = stage[seg.stage_slot].dev + seg.stage_off;
-        st.staged_hits++;
-        st.bytes_staged += seg.bytes;
-      } else {
-        const int k = pick_slot(*g, si, false);
-        if (k < 0) return fail(MO_E_STATE, "mo_unpack: no restore slot available");
-        if (int rc = fetch(*g, si, k)) return rc;
-        st.restore_fetches++;
-        r = &restore[k];
-      }
-      seg.prefetched = false;
-      if (r) {
-        MO_LINK(link->wait(r->gate, stream));
-        // Last decoded or read on another stream: this stream reads the slot after that work,
-        // and so the consumed point recorded below covers both streams' reads.
-        if (r->used_on && r->used_on != stream) MO_HIP(hipStreamWaitEvent(stream, r->join, 0));
-        if (!r->decoded) {
-          // the coded stream has landed (wait): decode it into the slot on this stream, ahead
-          // of the unpack kernels that read the slot
-          MO_HIP((hipError_t)wire_decode((uint64_t)r->wire, seg.host_bytes, (uint64_t)r->dev, seg.bytes, stream));
-          r->decoded = true;
-        }
-        src = r->dev;
-      }
-      KernelTimer timer(this, false);
-      Launcher L(false, stream, &timer);
-      for (const Piece& p : seg.pieces) {
-        if (!dst[p.entry]) continue;
-        KDesc kd;
-        const Canon& c = g->entries[p.entry].canon;
-        if (dst[p.entry] % c.eb != 0) return fail(MO_E_INVALID, "mo_unpack: misaligned destination");
-        if (int rc = make_kdesc(c, dst[p.entry], p.first, p.nbytes, (uint64_t)(src + p.seg_off), kd, err))
-          return fail(rc, "mo_unpack: " + err);
-        kd.cache = unpack_cache();
-        L.add(kd);
-        st.bytes_unpacked += p.nbytes;
-      }
-      if (int rc = L.flush()) return hip_fail(rc, "unpack kernel launch");
-      st.unpack_launches += L.launches();
-      if (r) {
+    KernelTimer timer(this, false);
+    Launcher L(false, stream, &timer);
+    std::vector<RestoreSlot*> pending;  // slots whose scatter is added but not yet released
+    auto release_pending = [&]() -> int {
+      const int rc = L.flush();
+      for (RestoreSlot* r : pending) {
         MO_LINK(link->consumed(r->gate, stream));
         if (!r->join) MO_HIP(hipEventCreateWithFlags(&r->join, hipEventDisableTiming));
         MO_HIP(hipEventRecord(r->join, stream));
@@ -972,8 +933,98 @@ struct Engine {
         r->consumed = true;
         r->tick = ++tick;
       }
+      pending.clear();
+      return rc ? hip_fail(rc, "unpack kernel launch") : 0;
+    };
+    int rc = 0;
+    uint64_t off = 0;
+    for (uint32_t k = 0; k < n && !rc; off += counts[k], ++k) {
+      Group* g = find(gids[k]);
+      if (k > 0 && !ready_now(*g, dst + off, stream)) continue;
+      if (g->open) {
+        uint64_t id;
+        if ((rc = commit(stream, &id))) break;
+      }
+      for (uint32_t si = 0; si < g->segs.size() && !rc; ++si) {
+        if (k == 0 && !pending.empty() && (rc = release_pending())) break;
+        rc = scatter_segment(*g, si, dst + off, stream, k == 0, L, pending);
+      }
+      if (!rc) unpacked[k] = 1;
     }
-    return 0;
+    const int rc2 = release_pending();
+    st.unpack_launches += L.launches();
+    return rc ? rc : rc2;
+  }
+
+  // Whether every segment of `g` with a destination in `dst` can be scattered on `stream` now
+  // without waiting for a copy.
+  bool ready_now(const Group& g, const uint64_t* dst, hipStream_t stream) const {
+    if (g.open) return false;
+    for (uint32_t si = 0; si < g.segs.size(); ++si) {
+      const Segment& seg = g.segs[si];
+      bool any = false;
+      for (const Piece& p : seg.pieces) any = any || dst[p.entry] != 0;
+      if (!any || staged(seg, stream)) continue;
+      if (!resident(g, si) || !idle(seg.h2d)) return false;
+    }
+    return true;
+  }
+
+  // Add the pieces of segment `si` of `g` that have a destination to `L`, after making its
+  // bytes readable on `stream`: from the staging slot, or from a restore slot (fetched first if
+  // `fetch` allows, waited for, decoded if coded). The restore slot goes to `pending`.
+  int scatter_segment(Group& g, uint32_t si, const uint64_t* dst, hipStream_t stream, bool fetch_allowed,
+                      Launcher& L, std::vector<RestoreSlot*>& pending) {
+    Segment& seg = g.segs[si];
+    bool any = false;
+    for (const Piece& p : seg.pieces) any = any || dst[p.entry] != 0;
+    if (!any) return 0;
+    RestoreSlot* r = nullptr;
+    const char* src = nullptr;
+    if (resident(g, si)) {
+      if (seg.prefetched) st.prefetch_hits++;
+      r = &restore[seg.restore_slot];
+    } else if (staged(seg, stream)) {
+      // Still in the staging slot, stream-ordered after its pack kernels: no H2D.
+      src = stage[seg.stage_slot].dev + seg.stage_off;
+      st.staged_hits++;
+      st.bytes_staged += seg.bytes;
+    } else {
+      if (!fetch_allowed) return fail(MO_E_STATE, "mo_unpack: a further group's segment is not resident");
+      const int k = pick_slot(g, si, false);
+      if (k < 0) return fail(MO_E_STATE, "mo_unpack: no restore slot available");
+      if (int rc = fetch(g, si, k)) return rc;
+      st.restore_fetches++;
+      r = &restore[k];
+    }
+    seg.prefetched = false;
+    if (r) {
+      MO_LINK(link->wait(r->gate, stream));
+      // Last decoded or read on another stream: this stream reads the slot after that work,
+      // and so the consumed point recorded after the scatter covers both streams' reads.
+      if (r->used_on && r->used_on != stream) MO_HIP(hipStreamWaitEvent(stream, r->join, 0));
+      if (!r->decoded) {
+        // the coded stream has landed (wait): decode it into the slot on this stream, ahead
+        // of the unpack kernels that read the slot
+        MO_HIP((hipError_t)wire_decode((uint64_t)r->wire, seg.host_bytes, (uint64_t)r->dev, seg.bytes, stream));
+        r->decoded = true;
+      }
+      src = r->dev;
+    }
+    std::string err;
+    for (const Piece& p : seg.pieces) {
+      if (!dst[p.entry]) continue;
+      KDesc kd;
+      const Canon& c = g.entries[p.entry].canon;
+      if (dst[p.entry] % c.eb != 0) return fail(MO_E_INVALID, "mo_unpack: misaligned destination");
+      if (int rc = make_kdesc(c, dst[p.entry], p.first, p.nbytes, (uint64_t)(src + p.seg_off), kd, err))
+        return fail(rc, "mo_unpack: " + err);
+      kd.cache = unpack_cache();
+      L.add(kd);
+      st.bytes_unpacked += p.nbytes;
+    }
+    if (r) pending.push_back(r);
+    return L.status() ? hip_fail(L.status(), "unpack kernel launch") : 0;
   }
 
   int release(uint64_t gid) {
@@ -1396,7 +1447,18 @@ int mo_prefetch_groups(mo_engine* engine, const uint64_t* groups, uint32_t n, ui
 
 int mo_unpack(mo_engine* engine, uint64_t group, const uint64_t* dst, uint32_t n, uint64_t stream) {
   if (n > 0 && !dst) return mo::fail(MO_E_INVALID, "mo_unpack: null destination array");
-  MO_ENGINE_CALL(engine, engine->e.unpack(group, dst, n, (hipStream_t)stream));
+  uint32_t unpacked = 0;
+  MO_ENGINE_CALL(engine, engine->e.unpack_groups(&group, dst, &n, 1, (hipStream_t)stream, &unpacked));
+}
+
+int mo_unpack_groups(mo_engine* engine, const uint64_t* groups, const uint64_t* dst, const uint32_t* counts,
+                     uint32_t n, uint64_t stream, uint32_t* unpacked) {
+  if (n == 0) return mo::fail(MO_E_INVALID, "mo_unpack_groups: no group");
+  if (!groups || !counts || !unpacked) return mo::fail(MO_E_INVALID, "mo_unpack_groups: null array");
+  uint64_t total = 0;
+  for (uint32_t k = 0; k < n; ++k) total += counts[k];
+  if (total > 0 && !dst) return mo::fail(MO_E_INVALID, "mo_unpack_groups: null destination array");
+  MO_ENGINE_CALL(engine, engine->e.unpack_groups(groups, dst, counts, n, (hipStream_t)stream, unpacked));
 }
 
 int mo_release(mo_engine* engine, uint64_t group) { MO_ENGINE_CALL(engine, engine->e.release(group)); }

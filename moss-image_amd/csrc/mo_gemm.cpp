@@ -9,6 +9,7 @@
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <string>
@@ -36,8 +37,14 @@ struct GemmModule {
   int cus = 0;
   // [backward][small][tail]
   Kernel k[2][2][2];
-  hipFunction_t decode = nullptr;  // mo_int8_decode_kernel
+  hipFunction_t decode = nullptr;     // mo_int8_decode_kernel
+  hipFunction_t ws_fwd = nullptr;     // mo_int8_ws_fwd: weight in registers, column scales
+  hipFunction_t ws_kscale = nullptr;  // mo_int8_ws_kscale: the same on a transposed weight, per-k scales
+  hipFunction_t transpose = nullptr;  // mo_int8_transpose_kernel
 };
+
+// Which kernel takes the large-tile rows of a launch plan (mo_int8_set_kernel).
+std::atomic<uint32_t> g_kernel{MO_INT8_KERNEL_REGISTERS};
 
 std::mutex g_mu;
 std::map<int, GemmModule> g_modules;
@@ -67,6 +74,10 @@ int gemm_module(GemmModule* out) {
         }
     if ((e = hipModuleGetFunction(&m.decode, m.module, "mo_int8_decode_kernel")) != hipSuccess)
       return mo::set_hip_error((int)e, "hipModuleGetFunction (int8 decode)");
+    if ((e = hipModuleGetFunction(&m.ws_fwd, m.module, "mo_int8_ws_fwd")) != hipSuccess ||
+        (e = hipModuleGetFunction(&m.ws_kscale, m.module, "mo_int8_ws_kscale")) != hipSuccess ||
+        (e = hipModuleGetFunction(&m.transpose, m.module, "mo_int8_transpose_kernel")) != hipSuccess)
+      return mo::set_hip_error((int)e, "hipModuleGetFunction (int8 weight-in-registers kernels)");
     it = g_modules.emplace(device, m).first;
   }
   *out = it->second;
@@ -129,6 +140,9 @@ int launch(const Kernel& k, void** params, uint32_t rows, uint32_t cols, uint64_
   return 0;
 }
 
+// The weight-in-registers kernels: 256 x 256 tiles, four waves.
+Kernel registers_kernel(hipFunction_t fn) { return Kernel{fn, 256, kLarge}; }
+
 }  // namespace
 
 extern "C" {
@@ -163,8 +177,9 @@ int mo_int8_linear_forward(uint64_t x, uint64_t w, uint64_t scale, uint64_t bias
   Part parts[2];
   const int n = plan(rows, out_features, m.cus, parts);
   const int tail = in_features % 64 != 0;
+  const bool registers = !tail && g_kernel.load() == MO_INT8_KERNEL_REGISTERS;
   for (int p = 0; p < n; ++p) {
-    const Kernel& k = m.k[0][parts[p].small][tail];
+    const Kernel k = !parts[p].small && registers ? registers_kernel(m.ws_fwd) : m.k[0][parts[p].small][tail];
     const void* A = (const void*)(x + (uint64_t)parts[p].row0 * in_features * 2);
     const void* B = (const void*)w;
     const void* S = (const void*)scale;
@@ -178,18 +193,39 @@ int mo_int8_linear_forward(uint64_t x, uint64_t w, uint64_t scale, uint64_t bias
   return 0;
 }
 
+uint64_t mo_int8_backward_workspace_bytes(uint32_t in_features, uint32_t out_features) {
+  return (uint64_t)in_features * out_features;
+}
+
 int mo_int8_linear_backward(uint64_t dy, uint64_t w, uint64_t scale, uint64_t dx, uint32_t rows, uint32_t in_features,
-                            uint32_t out_features, uint64_t stream) {
+                            uint32_t out_features, uint64_t workspace, uint64_t workspace_bytes, uint64_t stream) {
   if (int rc = check(dy, w, scale, dx, rows, in_features, out_features)) return rc;
+  if (workspace % 16) return mo::set_error(MO_E_INVALID, "workspace pointer must be 16-byte aligned");
   GemmModule m;
   if (int rc = gemm_module(&m)) return rc;
   Part parts[2];
   const int n = plan(rows, in_features, m.cus, parts);
   const int tail = out_features % 64 != 0;
+  const bool registers = !tail && g_kernel.load() == MO_INT8_KERNEL_REGISTERS && workspace &&
+                         workspace_bytes >= mo_int8_backward_workspace_bytes(in_features, out_features);
+  bool transposed = false;
   for (int p = 0; p < n; ++p) {
-    const Kernel& k = m.k[1][parts[p].small][tail];
+    const bool ws = !parts[p].small && registers;
+    if (ws && !transposed) {
+      // the weight with the reduction (out) contiguous, for the weight-in-registers kernel
+      const void* src = (const void*)w;
+      void* dst = (void*)workspace;
+      uint32_t r = out_features, c = in_features;
+      void* tparams[] = {&src, &dst, &r, &c};
+      const uint64_t threads = (uint64_t)(out_features / 16) * (in_features / 4);
+      const hipError_t e = hipModuleLaunchKernel(m.transpose, (uint32_t)((threads + 255) / 256), 1, 1, 256, 1, 1, 0,
+                                                 (hipStream_t)stream, tparams, nullptr);
+      if (e != hipSuccess) return mo::set_hip_error((int)e, "int8 transpose launch");
+      transposed = true;
+    }
+    const Kernel k = ws ? registers_kernel(m.ws_kscale) : m.k[1][parts[p].small][tail];
     const void* A = (const void*)(dy + (uint64_t)parts[p].row0 * out_features * 2);
-    const void* B = (const void*)w;
+    const void* B = ws ? (const void*)workspace : (const void*)w;
     const void* S = (const void*)scale;
     void* C = (void*)(dx + (uint64_t)parts[p].row0 * in_features * 2);
     int M = (int)parts[p].rows, NC = (int)in_features, R = (int)out_features;
@@ -197,6 +233,13 @@ int mo_int8_linear_backward(uint64_t dy, uint64_t w, uint64_t scale, uint64_t dx
     void* params[] = {&A, &B, &S, &C, &M, &NC, &R, &tiles_m};
     if (int rc = launch(k, params, parts[p].rows, in_features, stream)) return rc;
   }
+  return 0;
+}
+
+int mo_int8_set_kernel(uint32_t kernel) {
+  if (kernel != MO_INT8_KERNEL_REGISTERS && kernel != MO_INT8_KERNEL_LDS)
+    return mo::set_error(MO_E_INVALID, "unknown int8 kernel selection");
+  g_kernel.store(kernel);
   return 0;
 }
 

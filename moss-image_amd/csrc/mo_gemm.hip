@@ -34,7 +34,10 @@
 // run of a few row and column tiles in that XCD's L2.
 // MFMA 32x32x16 bf16 lane layout (checked on the device): A lane l holds row l%32,
 // k = 8*(l/32)+j; B lane l holds column l%32, k = 8*(l/32)+j; D register r of lane l holds
-// row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// row 8*(r/4) + 4*(l/32) + r%4, column l%32. Within a step of 64, slice q gives lane half h the
+// reduction indices 32 h + 8 q + j (LDS chunk 4 h + q of a row), in every kernel of this file,
+// so that all tiles add the same products in the same order and a launch plan that splits the
+// rows between tiles does not change results.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -165,8 +168,8 @@ __device__ __forceinline__ void gemm_body(const __bf16* __restrict__ A, const in
   for (int p = 0; p < 2; ++p)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      rd_a[p][q] = swz(wm * G::kRowsW + 32 * p + lr, 2 * q + h);
-      rd_b[p][q] = swz(wc * G::kColsW + 32 * p + lr, 2 * q + h);
+      rd_a[p][q] = swz(wm * G::kRowsW + 32 * p + lr, 4 * h + q);
+      rd_b[p][q] = swz(wc * G::kColsW + 32 * p + lr, 4 * h + q);
     }
   int wr_b[8];  // forward: [0..1] = chunks 2 f_part + 0/1 of column f_col (i adds kFcols rows);
                 // transposed: [c] = column kTn t_ng + c, chunk t_rg
@@ -376,6 +379,275 @@ __device__ __forceinline__ void gemm_body(const __bf16* __restrict__ A, const in
   }
 }
 
+// ---- weight in registers ----
+// C[M][N] = A[M][K] . W'^T with Bq [N][K] int8 (the reduction contiguous), W' = decode(Bq), fp32
+// accumulation, bf16 output (+ bias). Scales per column (forward: Bq is the weight, scale[N]) or,
+// with kScaleK, per reduction index (input gradient: Bq is the transposed weight, scale[K]).
+// K % 64 == 0; rows past M and columns past N read zeros and store nothing.
+//
+// A workgroup owns a 256 x 256 tile with four waves side by side: wave w owns all 256 rows and
+// columns 64 w .. 64 w + 63, as 8 x 2 MFMA 32x32x16 tiles (256 accumulators). A goes global ->
+// LDS by the buffer-load DMA path, double-buffered and swizzled as in gemm_body; each wave reads
+// every row of it. B never enters LDS: each lane loads the int8 bytes of its two columns
+// straight into registers and decodes them there into the MFMA's B fragment, so every column is
+// decoded by one wave only and the LDS carries A alone (A fragment reads, 8 KiB a wave and
+// slice, plus the DMA).
+// Reduction order: in a step of 64, lane half h (lanes 32 h ..) takes k = 32 h + 8 q + j in
+// slice q (j = 0..7), for A's fragments and B's alike. A lane's weight bytes of a step are then
+// 32 contiguous bytes of its column: two 16-byte halves, half p serving slices 2 p and 2 p + 1.
+// Within step s, slice q reads the A fragments and decodes the B fragments of slice q + 1 (of
+// step s + 1 when q = 3) while slice q's MFMAs run. Half 0 of a column's bytes of step s is
+// free once slice 1 is decoded (during slice 0), half 1 once slice 3 is (during slice 2): half 0
+// of step s + 2 is loaded in slice 1 and half 1 in slice 3, into the register set of step s
+// (two sets by step parity). A has three LDS buffers (96 KiB): the tile of step s + 2 (and with
+// kScaleK its 64 scales) is DMA'd in slice 0 of step s into the buffer step s - 1 used, so a
+// DMA has six slices to land. After slice 2 each wave waits for everything but the loads of
+// step s + 2, then the workgroup meets at the one barrier of the step: slice 3 already reads
+// the next step's buffer, and every wave is done with step s - 1's before its refill.
+template <bool kScaleK>
+__device__ __forceinline__ void ws_body(const __bf16* __restrict__ A, const int8_t* __restrict__ Bq,
+                                        const float* __restrict__ scale, const __bf16* __restrict__ bias,
+                                        __bf16* __restrict__ C, int M, int N, int K, int tiles_m) {
+  constexpr int kBM = 256, kBN = 256, kWaves = 4, kDma = kBM / 8 / kWaves;  // 8 x 1 KiB A blocks per wave
+  // three buffers as distinct objects, chosen at compile time: the compiler can then tell the
+  // buffer a DMA writes from the ones being read, and waits only for the DMA that was asked for
+  __shared__ __attribute__((aligned(16))) __bf16 lds_a0[kBM * kBR];
+  __shared__ __attribute__((aligned(16))) __bf16 lds_a1[kBM * kBR];
+  __shared__ __attribute__((aligned(16))) __bf16 lds_a2[kBM * kBR];
+  __shared__ __attribute__((aligned(16))) float lds_s0[kBR];
+  __shared__ __attribute__((aligned(16))) float lds_s1[kBR];
+  __shared__ __attribute__((aligned(16))) float lds_s2[kBR];
+  auto abuf = [&](auto i) -> MO_LDS __bf16* {
+    constexpr int I = decltype(i)::value;
+    return (MO_LDS __bf16*)(I == 0 ? lds_a0 : I == 1 ? lds_a1 : lds_a2);
+  };
+  auto sbuf = [&](auto i) -> MO_LDS float* {
+    constexpr int I = decltype(i)::value;
+    return (MO_LDS float*)(I == 0 ? lds_s0 : I == 1 ? lds_s1 : lds_s2);
+  };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 31, h = lane >> 5;
+
+  // ---- tile numbering: XCD-aware, then grouped (as gemm_body) ----
+  const int tiles = gridDim.x;
+  const int tiles_c = tiles / tiles_m;
+  int t;
+  {
+    const int b = blockIdx.x, xcd = b % kXcds, idx = b / kXcds;
+    const int per = tiles / kXcds, rem = tiles % kXcds;
+    t = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+  }
+  const int group_tiles = kGroupM * tiles_c;
+  const int first_m = (t / group_tiles) * kGroupM;
+  const int gm = min(tiles_m - first_m, kGroupM);
+  const int in_group = t % group_tiles;
+  const int m0 = (first_m + in_group % gm) * kBM;
+  const int c0 = (in_group / gm) * kBN;
+
+  const rsrc_t ra_src = make_rsrc(A + (size_t)m0 * K, (uint32_t)(min(M - m0, kBM) * K * 2));
+  const rsrc_t rb_src = make_rsrc(Bq + (size_t)c0 * K, (uint32_t)(min(N - c0, kBN) * K));
+  const rsrc_t rs_src = make_rsrc(scale, (uint32_t)((kScaleK ? K : N) * 4));
+
+  // A by DMA: wave w fills 1 KiB blocks w * kDma + j (8 rows each), as gemm_body.
+  uint32_t a_off[kDma];
+#pragma unroll
+  for (int j = 0; j < kDma; ++j) {
+    const int row = (wave * kDma + j) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
+    a_off[j] = (uint32_t)(row * K + 8 * c) * 2;
+  }
+  // A fragment of slice q, row tile i: row 32 i + lr, chunk 4 h + q (i + 2 keeps the swizzle)
+  int rd_a[2][4];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) rd_a[p][q] = swz(32 * p + lr, 4 * h + q);
+  // B: column tile ct of the wave holds column 64 w + 32 ct + lr of the tile
+  uint32_t b_off[2];
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) b_off[ct] = (uint32_t)((64 * wave + 32 * ct + lr) * K + 32 * h);
+  float sf[2] = {0.f, 0.f};  // forward: bf16-rounded column scales
+  if (!kScaleK) {
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int n = c0 + 64 * wave + 32 * ct + lr;
+      sf[ct] = bf16_round(__builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rs_src, n < N ? n * 4 : (int)kOob, 0, 0)));
+    }
+  }
+
+  auto dma = [&](MO_LDS __bf16* As, MO_LDS float* Ss, int r0) {
+    const rsrc_t src = r0 < K ? ra_src : make_rsrc(A, 0u);
+#pragma unroll
+    for (int j = 0; j < kDma; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (MO_LDS void*)(As + (wave * kDma + j) * 512), 16, a_off[j],
+                                               r0 * 2, 0, 0);
+    if (kScaleK)  // the step's 64 scales, the same bytes from every wave
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r0 < K ? rs_src : make_rsrc(A, 0u), (MO_LDS void*)Ss, 4, lane * 4,
+                                               r0 * 4, 0, 0);
+  };
+  constexpr int kDmaOps = kDma + (kScaleK ? 1 : 0);
+
+  // weight bytes: raw[set][ct][half], loaded for step r0 / 64 (past K: zeros)
+  u32x4 raw[2][2][2];
+  auto load_half = [&](auto set, auto half, int r0) {
+    constexpr int S = decltype(set)::value, P = decltype(half)::value;
+    const rsrc_t src = r0 < K ? rb_src : make_rsrc(Bq, 0u);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+      raw[S][ct][P] = __builtin_amdgcn_raw_buffer_load_b128(src, (int)(b_off[ct] + 16 * P), r0, 0);
+  };
+
+  bf16x8 fa[2][8], fb[2][2];  // fragments of two slices
+  auto read_a = [&](const MO_LDS __bf16* As, int q, int slot) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) fa[slot][i] = *(const MO_LDS bf16x8*)(As + rd_a[i & 1][q] + (i >> 1) * 64 * kBR);
+  };
+  // B fragments of slice q from register set S (scales of that step in Ss when kScaleK)
+  auto decode_b = [&](auto set, const MO_LDS float* Ss, int q, int slot) {
+    constexpr int S = decltype(set)::value;
+    float sk[8];
+    if (kScaleK) {
+      const float4 lo = *(const MO_LDS float4*)(Ss + 32 * h + 8 * q);
+      const float4 hi = *(const MO_LDS float4*)(Ss + 32 * h + 8 * q + 4);
+      sk[0] = lo.x, sk[1] = lo.y, sk[2] = lo.z, sk[3] = lo.w, sk[4] = hi.x, sk[5] = hi.y, sk[6] = hi.z, sk[7] = hi.w;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sk[j] = bf16_round(sk[j]);
+    }
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const u32x4 v = q < 2 ? raw[S][ct][0] : raw[S][ct][1];
+      const uint32_t w0 = v[2 * (q & 1)], w1 = v[2 * (q & 1) + 1];
+      bf16x8 f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) f[j] = decode(j < 4 ? w0 : w1, j & 3, kScaleK ? sk[j] : sf[ct]);
+      fb[slot][ct] = f;
+    }
+  };
+
+  f32x16 acc[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) acc[i][ct] = f32x16{};
+
+  // Instruction interleave of one slice: an MFMA, then one of the next slice's 8 A fragment
+  // reads behind each of the first 8 MFMAs, the decode VALU (about 40 ops, 56 with per-k
+  // scales) spread over all 16, the DMA (with its M0 writes) in slice 0 and the weight loads in
+  // slices 1 and 3.
+  auto schedule = [&](int q) {
+    constexpr int kMfma = 0x008, kValu = 0x002, kDsRead = 0x100, kVmem = 0x020, kSalu = 0x004;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+      if (m < 8) __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+      if (kScaleK && m == 0) __builtin_amdgcn_sched_group_barrier(kDsRead, 2, 0);
+      if (q == 0 && m >= 1 && m < 1 + kDmaOps) {
+        __builtin_amdgcn_sched_group_barrier(kSalu, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(kVmem, 1, 0);
+      }
+      if ((q == 1 || q == 3) && m == 10) __builtin_amdgcn_sched_group_barrier(kVmem, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(kValu, kScaleK ? 4 : 3, 0);
+    }
+  };
+
+  // Step s over buffer b (A and scales of step s), b1 = buffer of step s + 1, b2 = buffer step
+  // s + 2 is DMA'd into; weights of step s in set Cur, of step s + 1 in set Nxt; r0 = 64 s.
+  auto step = [&](auto b, auto b1, auto b2, int r0, auto cur, auto nxt) {
+    using H0 = std::integral_constant<int, 0>;
+    using H1 = std::integral_constant<int, 1>;
+    const MO_LDS __bf16* Ac = abuf(b);
+    const MO_LDS __bf16* An = abuf(b1);
+    const MO_LDS float* Sc = sbuf(b);
+    const MO_LDS float* Sn = sbuf(b1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int cq = q & 1, nq = cq ^ 1;
+      if (q < 3) {
+        read_a(Ac, q + 1, nq);
+        decode_b(cur, Sc, q + 1, nq);
+      } else {
+        read_a(An, 0, nq);  // after the barrier: the next step's A and scales are in LDS
+        decode_b(nxt, Sn, 0, nq);
+      }
+      if (q == 0) dma(abuf(b2), sbuf(b2), r0 + 2 * kBR);
+      if (q == 1) load_half(cur, H0{}, r0 + 2 * kBR);
+      if (q == 3) load_half(cur, H1{}, r0 + 2 * kBR);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+          acc[i][ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cq][i], fb[cq][ct], acc[i][ct], 0, 0, 0);
+      schedule(q);
+      __builtin_amdgcn_sched_barrier(0);
+      if (q == 2) {
+        // landed: all but step s + 2's DMA (slice 0) and half-0 loads (slice 1), so step s + 1's
+        // A, scales and both weight halves; then the whole workgroup (every wave is done with
+        // the buffer step s + 3 will refill)
+        __builtin_amdgcn_s_waitcnt(wait_vm(kDmaOps + 2, 0));
+        __syncthreads();
+      }
+    }
+  };
+
+  using set0 = std::integral_constant<int, 0>;
+  using set1 = std::integral_constant<int, 1>;
+  using H0 = std::integral_constant<int, 0>;
+  using H1 = std::integral_constant<int, 1>;
+  typedef const MO_LDS __bf16* clp;
+  typedef const MO_LDS float* csp;
+  const int steps = K / kBR;
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  using B2 = std::integral_constant<int, 2>;
+  // prologue: steps 0 and 1 (A, scales and weights); step 0 must have landed
+  dma(abuf(B0{}), sbuf(B0{}), 0);
+  load_half(set0{}, H0{}, 0);
+  load_half(set0{}, H1{}, 0);
+  dma(abuf(B1{}), sbuf(B1{}), kBR);
+  load_half(set1{}, H0{}, kBR);
+  load_half(set1{}, H1{}, kBR);
+  __builtin_amdgcn_s_waitcnt(wait_vm(kDmaOps + 4, 0));
+  __syncthreads();
+  read_a((clp)lds_a0, 0, 0);
+  decode_b(set0{}, (csp)lds_s0, 0, 0);
+  // Steps in sixes: two register sets by step parity, three LDS buffers by step modulo 3. Steps
+  // past K (up to five at the end) read zeros and add nothing.
+  for (int s = 0; s < steps; s += 6) {
+    step(B0{}, B1{}, B2{}, (s + 0) * kBR, set0{}, set1{});
+    step(B1{}, B2{}, B0{}, (s + 1) * kBR, set1{}, set0{});
+    step(B2{}, B0{}, B1{}, (s + 2) * kBR, set0{}, set1{});
+    step(B0{}, B1{}, B2{}, (s + 3) * kBR, set1{}, set0{});
+    step(B1{}, B2{}, B0{}, (s + 4) * kBR, set0{}, set1{});
+    step(B2{}, B0{}, B1{}, (s + 5) * kBR, set1{}, set0{});
+  }
+
+  // ---- epilogue: bias, bf16, store (rows past M and columns past N fall outside) ----
+  const rsrc_t rc_src = make_rsrc(C + (size_t)m0 * N, (uint32_t)(min(M - m0, kBM) * N * 2));
+  const rsrc_t rbias_src = make_rsrc(bias, bias ? (uint32_t)N * 2 : 0u);
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) {
+    const int col = c0 + 64 * wave + 32 * ct + lr;
+    const bool col_ok = col < N;
+    const float b = (float)__builtin_bit_cast(
+        __bf16, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rbias_src, col_ok ? col * 2 : (int)kOob, 0, 0));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const __bf16 v = (__bf16)(acc[i][ct][r] + b);
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), rc_src,
+                                              col_ok ? (int)((uint32_t)(row * N + col) * 2) : (int)kOob, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
 // Configurations: forward 256 x 256 over 2 x 4 waves (two waves a SIMD); input gradient
 // 256 x 256 over 2 x 2 waves; both directions 128 x 128 over 2 x 2 waves for grids too small
 // or too ragged for the large tile.
@@ -397,6 +669,17 @@ using Small = Cfg<128, 128, 2, 2>;
                                                                  int R, int tiles_m) {                         \
     mo_gemm::gemm_body<G, true, FULL, VPM>(A, Bq, scale, nullptr, C, M, NC, R, tiles_m);                       \
   }
+
+extern "C" __global__ __launch_bounds__(256) void mo_int8_ws_fwd(const __bf16* A, const int8_t* Bq, const float* scale,
+                                                                   const __bf16* bias, __bf16* C, int M, int N, int K,
+                                                                   int tiles_m) {
+  mo_gemm::ws_body<false>(A, Bq, scale, bias, C, M, N, K, tiles_m);
+}
+extern "C" __global__ __launch_bounds__(256) void mo_int8_ws_kscale(const __bf16* A, const int8_t* Bq,
+                                                                     const float* scale, __bf16* C, int M, int N,
+                                                                     int K, int tiles_m) {
+  mo_gemm::ws_body<true>(A, Bq, scale, nullptr, C, M, N, K, tiles_m);
+}
 
 // full: R % 64 == 0; _tail: any multiple of 16
 MO_GEMM_FWD(mo_int8_linear_fwd_large, mo_gemm::FwdLarge, true, 6)
@@ -443,4 +726,32 @@ extern "C" __global__ __launch_bounds__(256) void mo_int8_decode_kernel(const in
   u32x4* dst = (u32x4*)(out + (size_t)i * 16);
   dst[0] = lo;
   dst[1] = hi;
+}
+
+// Wt[in][out] = W[out][in]^T for the input gradient on the weight-in-registers kernel, which
+// needs the reduction (out) contiguous. A lane moves a 16 x 4 block: 16 rows of W (out) x 4
+// columns (in), loaded as one dword per row (consecutive lanes: consecutive columns, so each
+// load instruction reads contiguous 256-byte row pieces), and written as 4 rows of Wt x 16 bytes.
+// rows % 16 == 0, cols % 16 == 0.
+extern "C" __global__ __launch_bounds__(256) void mo_int8_transpose_kernel(const int8_t* w, int8_t* wt,
+                                                                          uint32_t rows, uint32_t cols) {
+  const uint32_t col_groups = cols / 4;
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (i >= (uint64_t)(rows / 16) * col_groups) return;
+  const uint32_t rg = (uint32_t)(i / col_groups), cg = (uint32_t)(i % col_groups);
+  uint32_t v[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) v[r] = *(const uint32_t*)(w + ((size_t)(16 * rg + r) * cols + 4 * cg));
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    mo_gemm::u32x4 out;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) word |= ((v[4 * k + b] >> (8 * c)) & 0xFFu) << (8 * b);
+      out[k] = word;
+    }
+    *(mo_gemm::u32x4*)(wt + ((size_t)(4 * cg + c) * rows + 16 * rg)) = out;
+  }
 }

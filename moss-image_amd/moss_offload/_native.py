@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 13
+MO_ABI_VERSION = 15
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -35,6 +35,8 @@ MO_FLAG_UNPACK_CACHED_STORE = 0x100
 MO_FLAG_WIRE_CODING = 0x200
 MO_FLAG_WIRE_AUTO = 0x400
 MO_TENSOR_BF16_HIGH = 0x1
+MO_INT8_KERNEL_REGISTERS = 0
+MO_INT8_KERNEL_LDS = 1
 
 NO_GROUP = (1 << 64) - 1
 
@@ -195,6 +197,10 @@ SIGNATURES: dict[str, tuple] = {
     "mo_prefetch": (ctypes.c_int, [ctypes.c_void_p, _u64, _u64]),
     "mo_prefetch_groups": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(_u64), ctypes.c_uint32, _u64]),
     "mo_unpack": (ctypes.c_int, [ctypes.c_void_p, _u64, _P(_u64), ctypes.c_uint32, _u64]),
+    "mo_unpack_groups": (
+        ctypes.c_int,
+        [ctypes.c_void_p, _P(_u64), _P(_u64), _P(ctypes.c_uint32), ctypes.c_uint32, _u64, _P(ctypes.c_uint32)],
+    ),
     "mo_release": (ctypes.c_int, [ctypes.c_void_p, _u64]),
     "mo_group_info": (
         ctypes.c_int,
@@ -240,7 +246,9 @@ SIGNATURES: dict[str, tuple] = {
     "mo_int8_linear_forward": (ctypes.c_int, [_u64, _u64, _u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32,
                                               ctypes.c_uint32, _u64]),
     "mo_int8_linear_backward": (ctypes.c_int, [_u64, _u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32,
-                                               ctypes.c_uint32, _u64]),
+                                               ctypes.c_uint32, _u64, _u64, _u64]),
+    "mo_int8_backward_workspace_bytes": (_u64, [ctypes.c_uint32, ctypes.c_uint32]),
+    "mo_int8_set_kernel": (ctypes.c_int, [ctypes.c_uint32]),
 }
 
 _lock = threading.Lock()

@@ -83,6 +83,12 @@ class EngineConfig:
     # checkpointed block's inputs) this lets the trainer's thread run that many blocks ahead of
     # the GPU without waiting for an H2D.
     prefetch_depth: int = 8
+    # When autograd asks for a group, the groups backward needs next are scattered in the same
+    # kernel launch if their bytes are already on the device (H2D landed, or still staged),
+    # up to this many payload bytes in all: a checkpointed block's inputs (about 30 MB at
+    # 1024^2) are too small for one launch to reach the HBM copy rate, several together are
+    # not. Their restored tensors wait in the cache until asked for. 0: one group per unpack.
+    restore_ahead_bytes: int = 96 << 20
     dedupe: bool = True
     # Gather kernels of consecutive saves are launched together, one kernel per staging segment
     # when it closes (before its D2H), instead of one per save: fewer, larger launches that run
@@ -120,7 +126,7 @@ class EngineConfig:
             raise ValueError(f"wire_coding must be one of {tuple(WIRE_CODINGS)}, got {self.wire_coding!r}")
         for name in ("stage_slot_bytes", "stage_slots", "restore_slots", "host_limit_bytes", "host_chunk_bytes",
                      "copy_kernel_blocks", "d2h_engine", "h2d_engine", "prefetch_depth", "keep_last_blocks",
-                     "wire_device_limit"):
+                     "wire_device_limit", "restore_ahead_bytes"):
             value = getattr(self, name)
             if isinstance(value, bool) or not isinstance(value, int) or value < 0:
                 raise ValueError(f"{name} must be a non-negative integer, got {value!r}")
@@ -352,22 +358,53 @@ class OffloadEngine:
             cached = self._take_cached(entry, reader)
             if cached is not None:
                 return cached
-            n = len(group.entries)
-            dst = (ctypes.c_uint64 * n)()
-            for j, other in enumerate(group.entries):
-                if j != idx and (other.refs <= 0 or other.restored is not None):
-                    continue
-                tensor = torch.empty_strided(other.payload_shape, other.stride, dtype=other.dtype, device=self.device)
-                other.restored = tensor
-                other.restored_version = tensor._version
-                if other.nbytes:
-                    dst[j] = tensor.data_ptr()
-            _native.check("mo_unpack", self._lib.mo_unpack(self._handle, gid, dst, n, stream))
+            groups = [group] + self._ahead(gid)
+            counts = (ctypes.c_uint32 * len(groups))(*(len(g.entries) for g in groups))
+            dst = (ctypes.c_uint64 * sum(counts))()
+            made, base = [], 0
+            for k, g in enumerate(groups):
+                mine = []
+                for j, other in enumerate(g.entries):
+                    if (k or j != idx) and (other.refs <= 0 or other.restored is not None):
+                        continue
+                    tensor = torch.empty_strided(other.payload_shape, other.stride, dtype=other.dtype,
+                                                 device=self.device)
+                    mine.append((other, tensor))
+                    if other.nbytes:
+                        dst[base + j] = tensor.data_ptr()
+                made.append(mine)
+                base += len(g.entries)
+            unpacked = (ctypes.c_uint32 * len(groups))()
+            gids = (ctypes.c_uint64 * len(groups))(*(g.gid for g in groups))
+            _native.check("mo_unpack_groups", self._lib.mo_unpack_groups(self._handle, gids, dst, counts, len(groups),
+                                                                         stream, unpacked))
+            for k, mine in enumerate(made):
+                if unpacked[k]:  # the first group always is
+                    for other, tensor in mine:
+                        other.restored = tensor
+                        other.restored_version = tensor._version
             if self._held:  # unpacking the open group commits it
                 self._hold()
             if self.config.prefetch:
                 self._prefetch_after(gid, stream, max(1, self.config.prefetch_depth))
             return self._take_cached(entry, reader)
+
+    def _ahead(self, gid: int) -> list[_GroupState]:
+        """Groups backward needs after ``gid``, nearest first, whose live entries not yet
+        restored hold at most ``restore_ahead_bytes`` in all."""
+
+        budget = self.config.restore_ahead_bytes
+        out = []
+        if budget <= 0:
+            return out
+        for nxt in self._predict_chain(gid, max(1, self.config.prefetch_depth)):
+            g = self._groups[nxt]
+            size = sum(e.nbytes for e in g.entries if e.refs > 0 and e.restored is None)
+            if size > budget:
+                break
+            budget -= size
+            out.append(g)
+        return out
 
     def prefetch(self, gid: int, stream: int, ahead: bool = False) -> None:
         """Queue H2D of group ``gid``'s segments into free restore slots; with ``ahead``, also of

@@ -169,12 +169,25 @@ def int8_linear_backward(gradient: torch.Tensor, weight: torch.Tensor, scale: to
     if _library(rows, weight, path):
         torch.mm(matrix, decode_hip(weight, scale), out=out)
         return out.reshape(input_shape)
+    # the transposed int8 weight for the large tiles (freed to the caching allocator after the
+    # call; stream order keeps it alive for the kernels)
+    nbytes = lib.mo_int8_backward_workspace_bytes(in_features, out_features)
+    workspace = torch.empty(nbytes, dtype=torch.int8, device=gradient.device)
     _native.check(
         "mo_int8_linear_backward",
         lib.mo_int8_linear_backward(matrix.data_ptr(), weight.data_ptr(), scale.data_ptr(), out.data_ptr(), rows,
-                                    in_features, out_features, _stream(gradient)),
+                                    in_features, out_features, workspace.data_ptr(), nbytes, _stream(gradient)),
     )
     return out.reshape(input_shape)
+
+
+def set_kernel(kernel: str) -> None:
+    """Which kernel takes the large tiles of the fused path, process-wide: ``registers`` (default:
+    weights decoded in registers, activations through LDS) or ``lds`` (the weight tile decoded
+    into LDS). Same results bit for bit; for measuring one against the other."""
+
+    code = {"registers": _native.MO_INT8_KERNEL_REGISTERS, "lds": _native.MO_INT8_KERNEL_LDS}[kernel]
+    _native.check("mo_int8_set_kernel", _native.load().mo_int8_set_kernel(code))
 
 
 # ---- the reference module's interface (training/quant_kernels.py), same names and meaning ----

@@ -656,3 +656,65 @@ def test_resident_coded_slot_restored_on_a_second_stream() -> None:
         engine.synchronize()
     finally:
         engine.close()
+
+
+def test_small_groups_restored_ahead_share_one_scatter_launch() -> None:
+    """mo_unpack_groups through ``restore``: when a group is asked for, the next groups backward
+    needs join its scatter launch if their bytes are on the device already (prefetched and
+    landed), within ``restore_ahead_bytes``; a group whose H2D was never issued is left for its
+    own unpack. Every restore is bitwise, whichever launch wrote it."""
+
+    device = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(19)
+    # 8 MiB slots: each 1.5 MB group is one segment; 6 restore slots hold the prefetched ones
+    cfg = EngineConfig(stage_slot_bytes=8 * MiB, stage_slots=2, restore_slots=6, host_chunk_bytes=32 * MiB,
+                       wire_coding="off", staged_restore=False, prefetch=False, restore_ahead_bytes=5 * MiB)
+    engine = OffloadEngine(device, cfg)
+    try:
+        handles = []
+        for k in range(8):
+            group = [torch.randn(n, generator=g).to(device) for n in (300_000, 70_000, 5)]
+            members = [(t, *engine.pack(t, stream)) for t in group]
+            engine.commit(stream)
+            handles.append(members)
+        engine.synchronize()
+        gids = [members[0][1] for members in handles]
+        # groups 7..3 prefetched and landed; 2..0 never fetched
+        engine._prefetch_groups(gids[7:2:-1], stream)
+        engine.synchronize()
+        torch.cuda.synchronize(device)
+        base = engine.stats()["unpack_launches"]
+        t, gid, idx = handles[7][0]
+        assert_bitwise(engine.restore(gid, idx, stream), t)
+        # group 7 plus groups 6, 5 and 4 (3 x 1.48 MB within 5 MiB; group 3 would pass it): one launch
+        assert engine.stats()["unpack_launches"] - base == 1
+        for k in (6, 5, 4):
+            assert all(engine._groups[gids[k]].entries[j].restored is not None for j in range(3))
+        assert engine._groups[gids[3]].entries[0].restored is None
+        taken = {(7, 0)}
+        for k in (7, 6, 5, 4):
+            for j, (t, gid, idx) in enumerate(handles[k]):
+                if (k, j) not in taken:
+                    assert_bitwise(engine.restore(gid, idx, stream), t)
+                    taken.add((k, j))
+        assert engine.stats()["unpack_launches"] - base == 1  # 6, 5, 4 came from the cache
+        # group 3 is resident and landed, groups 2 and 1 were never fetched: 3 alone
+        t, gid, idx = handles[3][0]
+        assert_bitwise(engine.restore(gid, idx, stream), t)
+        taken.add((3, 0))
+        assert engine.stats()["unpack_launches"] - base == 2
+        assert engine._groups[gids[2]].entries[0].restored is None
+        for k in (3, 2, 1, 0):
+            for j, (t, gid, idx) in enumerate(handles[k]):
+                if (k, j) not in taken:
+                    assert_bitwise(engine.restore(gid, idx, stream), t)
+        st = engine.stats()
+        assert st["bytes_unpacked"] == st["bytes_packed"] and st["copy_failures"] == 0
+        for members in handles:
+            for _, gid, idx in members:
+                engine.drop(gid, idx)
+        engine.synchronize()
+        assert engine.stats()["host_bytes_in_use"] == 0
+    finally:
+        engine.close()

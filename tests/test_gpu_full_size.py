@@ -240,6 +240,33 @@ def test_config4_regime_a_2048_matches_no_offload(config3_model) -> None:
     _regime(config3_model, "B")
 
 
+def test_config4_regime_b_2048_matches_no_offload(config3_model) -> None:
+    """Config 4 not checkpointed (2048^2 + 4096 text tokens, the reference's plain-block branch,
+    training/model.py:708-709), where the host link sets the pace: about 6.3 GB of saves per
+    block. On 12 blocks (their coded saves fit the host's pinned-memory cap with room to
+    spare): every restore bitwise, the loss bitwise and the LoRA gradients within 1e-3."""
+
+    from moss_offload import engine as engine_mod
+
+    device = torch.device("cuda", 0)
+    inputs = bench.make_inputs(device, bench.C4_GRID, bench.C4_TEXT, seed=4)
+    layers = config3_model.layers
+    config3_model.layers = nn.ModuleList(list(layers)[:12])
+    try:
+        _regime(config3_model, "B")
+        expected = _step(config3_model, inputs, bench.config3_forward, moss_offload.activation_cpu_offload, False)
+        engine_mod.get_engine(device).reset_stats()
+        actual, counters, checked = _engine_step(config3_model, inputs)
+        st = engine_mod.get_engine(device).stats()
+    finally:
+        config3_model.layers = layers
+    _compare(actual, expected, "config 4 regime B, 12 blocks")
+    print(f"config 4 regime B: {counters}, restores checked {checked}, D2H {st['bytes_d2h'] / 1e9:.1f} GB, "
+          f"H2D {st['bytes_h2d'] / 1e9:.1f} GB, wire segments {st['wire_segments']}", flush=True)
+    assert checked > counters["offloaded"] // 2 and counters.get("narrowed", 0) >= 12
+    assert st["wire_segments"] > 0  # the link fell behind and the engine coded
+
+
 def _bit_sum(tensor):
     width = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}[tensor.element_size()]
     return tensor.detach().contiguous().view(width).sum(dtype=torch.int64)

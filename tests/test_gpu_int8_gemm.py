@@ -95,7 +95,8 @@ def test_backward_matches_fp64_reference(rows, in_f, out_f) -> None:
 # 256 large tiles), the large tile plus a small-tile launch for the rows of a partial last round
 # (17792 x 3072: 840 tiles), the small tile alone (small shapes above); each with a reduction
 # length that is and is not a multiple of 64.
-PLAN_SHAPES = [(4096, 4096, 4096), (4096, 1040, 4096), (17792, 3072, 3072), (17792, 1040, 3072)]
+PLAN_SHAPES = [(4096, 4096, 4096), (4096, 1040, 4096), (17792, 3072, 3072), (17792, 1040, 3072),
+               (4000, 4096, 4000)]  # the last: large tiles only, with ragged rows and columns
 
 
 @pytest.mark.parametrize("rows,in_f,out_f", PLAN_SHAPES)
@@ -109,7 +110,7 @@ def test_forward_launch_plans_match_fp64_reference(rows, in_f, out_f) -> None:
 
 
 @pytest.mark.parametrize("rows,in_f,out_f", [(4096, 4096, 4096), (4096, 4096, 1040), (17792, 3072, 3072),
-                                             (17792, 3072, 1040)])
+                                             (17792, 3072, 1040), (4000, 4000, 4096)])
 def test_backward_launch_plans_match_fp64_reference(rows, in_f, out_f) -> None:
     _, w, scale, _ = _operands(1, in_f, out_f, seed=rows + 5 * in_f + out_f)
     g = torch.Generator().manual_seed(rows + 1)
@@ -266,3 +267,25 @@ def test_library_path_is_the_eager_path_bit_for_bit(rows, in_f, out_f) -> None:
                        quant_kernels.int8_linear_forward(small, w, scale, b, path="fused").view(torch.int16))
     with pytest.raises(ValueError):
         quant_kernels.int8_linear_forward(x, w, scale, b, path="triton")
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", [(17792, 3072, 3072), (17792, 3072, 24576), (17792, 12288, 3072),
+                                             (4000, 4096, 4000)])
+def test_register_and_lds_kernels_agree_bitwise(rows, in_f, out_f) -> None:
+    """The large tile's two kernels (weights decoded in registers, or into LDS) add the same
+    products in the same order: forward and input gradient are equal bit for bit."""
+
+    x, w, scale, b = _operands(rows, in_f, out_f, seed=rows + in_f + out_f, bias=True)
+    g = torch.Generator().manual_seed(5)
+    dy = torch.randn(rows, out_f, generator=g).to(torch.bfloat16).to(DEV)
+    results = {}
+    try:
+        for kernel in ("lds", "registers"):
+            quant_kernels.set_kernel(kernel)
+            y = quant_kernels.int8_linear_forward(x, w, scale, b, path="fused")
+            dx = quant_kernels.int8_linear_backward(dy, w, scale, torch.Size((rows, in_f)), path="fused")
+            results[kernel] = (y, dx)
+    finally:
+        quant_kernels.set_kernel("registers")
+    for a, e in zip(results["registers"], results["lds"]):
+        assert torch.equal(a.view(torch.int16), e.view(torch.int16))
