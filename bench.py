@@ -336,6 +336,25 @@ def host_work(seconds: float) -> None:
         pass
 
 
+# engine statistics that are levels at the time of reading, not counts: summed over a mode's
+# rounds they would mean nothing, so the last reading stands
+ENGINE_LEVELS = ("groups_live", "entries_live", "host_bytes_in_use", "host_bytes_reserved", "device_ring_bytes",
+                 "py_groups_live")
+
+
+def add_counts(total: dict, reading: dict, latest=(), peak=()) -> None:
+    """Add one reading of counters to ``total``: sums, except the ``latest`` keys (the last
+    reading) and the ``peak`` keys (the largest)."""
+
+    for key, value in reading.items():
+        if key in latest or key not in total:
+            total[key] = value
+        elif key in peak:
+            total[key] = max(total[key], value)
+        else:
+            total[key] += value
+
+
 def time_steps(model, opt, inputs, steps: int, warmup: int, label: str, forward=config3_forward,
                host_work_s: float = 0.0):
     import torch
@@ -978,6 +997,7 @@ def run(args) -> dict:
         restore_slots=args.restore_slots,
         prefetch_depth=args.prefetch_depth,
         stage_slot_bytes=args.slot_mib << 20,
+        **({} if args.restore_ahead_mib is None else {"restore_ahead_bytes": args.restore_ahead_mib << 20}),
         staged_restore=not args.no_staged_restore,
         kernel_copy=args.kernel_copy,
         link=args.link,
@@ -1201,6 +1221,8 @@ def run(args) -> dict:
         rounds = max(1, args.rounds_big) if regime_name in INTERLEAVED else 1
         times = {mode: [] for mode in modes}
         peaks = {mode: 0 for mode in modes}
+        counted = {mode: 0 for mode in modes}  # steps (warmup included) the statistics below cover
+        engine_stats, hook_stats, stream_stats = {}, {}, {}
         failed = {}
 
         def enter(mode, first):
@@ -1214,17 +1236,30 @@ def run(args) -> dict:
                 # marks the start of each leg and mode in a kernel trace, and scales rocprofv3
                 # FETCH_SIZE / WRITE_SIZE to bytes in a counter run
                 calibration_copy(device, torch.cuda.current_stream(device).cuda_stream)
-                engine.reset_stats()
-                moss_offload.reset_hook_counters()
-                if streamer is not None:
-                    streamer.reset_stats()
+            # every mode and round starts from zero (the modes share the engine), and what it
+            # counted is added to its own totals right after it ran
+            engine.reset_stats()
+            moss_offload.reset_hook_counters()
+            if streamer is not None:
+                streamer.reset_stats()
             return engine
+
+        def collect(mode, engine, nsteps):
+            counted[mode] += nsteps
+            add_counts(hook_stats.setdefault(mode, {}), moss_offload.hook_counters())
+            if streamer is not None:
+                torch.cuda.synchronize()
+                add_counts(stream_stats.setdefault(mode, {}), streamer.stats())
+            if mode in ("engine", "engine_hipdma"):
+                engine.synchronize()
+                add_counts(engine_stats.setdefault(mode, {}), engine.stats(), latest=ENGINE_LEVELS,
+                           peak=("host_bytes_peak",))
 
         for rnd in range(rounds):
             for mode in modes:
                 if mode in failed or (mode == "reference" and rnd > 0):  # one round of the baseline
                     continue
-                enter(mode, rnd == 0)
+                engine = enter(mode, rnd == 0)
                 try:
                     seconds, peak = time_steps(wl_model, wl_opt, wl_inputs, steps, warmup if rnd == 0 else 0,
                                                f"{regime_name}/{mode}" + (f" round {rnd + 1}/{rounds}" if rounds > 1 else ""),
@@ -1243,6 +1278,7 @@ def run(args) -> dict:
                     continue
                 times[mode].append(seconds)
                 peaks[mode] = max(peaks[mode], peak)
+                collect(mode, engine, steps + (warmup if rnd == 0 else 0))
                 if mode == "reference":
                     torch._C._host_emptyCache()
 
@@ -1255,10 +1291,9 @@ def run(args) -> dict:
             record = {"s_per_it": sum(timed) / len(timed), "peak_device_bytes": peaks[mode]}
             if len(timed) > 1:
                 record["s_per_it_rounds"] = timed
-            n = warmup + steps * len(timed)  # stats were reset before the first warmup step
+            n = counted[mode]
             if streamer is not None:
-                torch.cuda.synchronize()
-                ss = streamer.stats()
+                ss = stream_stats[mode]
                 record["stream"] = {
                     "fills_per_step": ss["fills"] / n,
                     "bytes_per_step": ss["bytes"] / n,
@@ -1273,9 +1308,9 @@ def run(args) -> dict:
                 }
             if mode in ("engine", "engine_hipdma"):
                 engine.synchronize()
-                st = engine.stats()
+                st = engine_stats[mode]
                 record["link"] = engine.link_name()
-                record["hook_counters_per_step"] = {k: v / n for k, v in moss_offload.hook_counters().items()}
+                record["hook_counters_per_step"] = {k: v / n for k, v in hook_stats[mode].items()}
                 # the staging and restore rings (and their wire buffers once coding ran) are the
                 # engine's own hipMalloc, outside torch's allocator and so outside peak_device_bytes
                 rings = st["device_ring_bytes"]
@@ -1311,6 +1346,11 @@ def run(args) -> dict:
                     prefetch_hits=st["prefetch_hits"],
                     restore_fetches=st["restore_fetches"],
                     host_pinned_peak_bytes=st["host_bytes_peak"],
+                    restores_per_step=st["py_ahead_restores"] / n,
+                    groups_restored_ahead_per_step=st["py_ahead_restored"] / n,
+                    groups_offered_ahead_per_step=st["py_ahead_offered"] / n,
+                    ahead_not_resident_per_step=st["ahead_not_resident"] / n,
+                    ahead_in_flight_per_step=st["ahead_in_flight"] / n,
                 )
                 engine.trim()
             entry[mode] = record
@@ -1399,6 +1439,8 @@ def main() -> int:
     parser.add_argument("--prefetch-depth", type=int, default=8,
                         help="groups the engine prefetches ahead of backward after each restored group")
     parser.add_argument("--slot-mib", type=int, default=128)
+    parser.add_argument("--restore-ahead-mib", type=int, default=None,
+                        help="payload MiB of further groups one unpack may restore (default: the engine's)")
     parser.add_argument("--no-staged-restore", action="store_true")
     parser.add_argument("--d2h-engine", type=lambda v: int(v, 0), default=0,
                         help="SDMA engine bits for D2H (0: two engines, copies split in halves)")

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 15
+#define MO_ABI_VERSION 16
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -162,6 +162,9 @@ typedef struct mo_stats {
   uint64_t wire_fallbacks;     /* segments meant for wire coding that crossed raw because the
                                   wire buffers could not be allocated (or would pass
                                   wire_device_limit)                                        */
+  uint64_t ahead_restored;     /* further groups of mo_unpack_groups restored               */
+  uint64_t ahead_not_resident; /* further groups left: a segment was not in a restore slot  */
+  uint64_t ahead_in_flight;    /* further groups left: a segment's H2D had not landed       */
 } mo_stats;
 
 typedef struct mo_engine mo_engine;

@@ -940,7 +940,13 @@ struct Engine {
     uint64_t off = 0;
     for (uint32_t k = 0; k < n && !rc; off += counts[k], ++k) {
       Group* g = find(gids[k]);
-      if (k > 0 && !ready_now(*g, dst + off, stream)) continue;
+      if (k > 0) {
+        const int why = not_ready(*g, dst + off, stream);
+        if (why == 1) st.ahead_not_resident++;
+        if (why == 2) st.ahead_in_flight++;
+        if (why) continue;
+        st.ahead_restored++;
+      }
       if (g->open) {
         uint64_t id;
         if ((rc = commit(stream, &id))) break;
@@ -956,18 +962,21 @@ struct Engine {
     return rc ? rc : rc2;
   }
 
-  // Whether every segment of `g` with a destination in `dst` can be scattered on `stream` now
-  // without waiting for a copy.
-  bool ready_now(const Group& g, const uint64_t* dst, hipStream_t stream) const {
-    if (g.open) return false;
+  // 0 when every segment of `g` with a destination in `dst` can be scattered on `stream` now
+  // without waiting for a copy; else 1 (open, or a segment not in a restore slot) or 2 (a
+  // segment's H2D still running).
+  int not_ready(const Group& g, const uint64_t* dst, hipStream_t stream) const {
+    if (g.open) return 1;
+    int why = 0;
     for (uint32_t si = 0; si < g.segs.size(); ++si) {
       const Segment& seg = g.segs[si];
       bool any = false;
       for (const Piece& p : seg.pieces) any = any || dst[p.entry] != 0;
       if (!any || staged(seg, stream)) continue;
-      if (!resident(g, si) || !idle(seg.h2d)) return false;
+      if (!resident(g, si)) return 1;
+      if (!idle(seg.h2d)) why = 2;
     }
-    return true;
+    return why;
   }
 
   // Add the pieces of segment `si` of `g` that have a destination to `L`, after making its

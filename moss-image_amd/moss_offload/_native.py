@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 15
+MO_ABI_VERSION = 16
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -121,6 +121,9 @@ class MoStats(ctypes.Structure):
         ("wire_bytes", ctypes.c_uint64),
         ("device_ring_bytes", ctypes.c_uint64),
         ("wire_fallbacks", ctypes.c_uint64),
+        ("ahead_restored", ctypes.c_uint64),
+        ("ahead_not_resident", ctypes.c_uint64),
+        ("ahead_in_flight", ctypes.c_uint64),
     ]
 
     def as_dict(self) -> dict:

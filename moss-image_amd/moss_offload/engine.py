@@ -206,6 +206,8 @@ class OffloadEngine:
         self._held: deque[tuple[int, torch.Tensor, int]] = deque()
         self._calls = ctypes.c_uint64()
         self._launched = ctypes.c_uint64()
+        # restores that asked for groups ahead, the groups offered, the groups restored ahead
+        self._ahead_counts = {"restores": 0, "offered": 0, "restored": 0}
 
     # ------------------------------------------------------------------ forward
     def pack(self, source: torch.Tensor, stream: int, narrow: bool = False) -> tuple[int, int]:
@@ -378,6 +380,9 @@ class OffloadEngine:
             gids = (ctypes.c_uint64 * len(groups))(*(g.gid for g in groups))
             _native.check("mo_unpack_groups", self._lib.mo_unpack_groups(self._handle, gids, dst, counts, len(groups),
                                                                          stream, unpacked))
+            self._ahead_counts["restores"] += 1
+            self._ahead_counts["offered"] += len(groups) - 1
+            self._ahead_counts["restored"] += sum(unpacked[k] for k in range(1, len(groups)))
             for k, mine in enumerate(made):
                 if unpacked[k]:  # the first group always is
                     for other, tensor in mine:
@@ -483,11 +488,14 @@ class OffloadEngine:
             _native.check("mo_get_stats", self._lib.mo_get_stats(self._handle, ctypes.byref(out)))
             result = out.as_dict()
             result["py_groups_live"] = len(self._groups)
+            for key, value in self._ahead_counts.items():
+                result[f"py_ahead_{key}"] = value
             return result
 
     def reset_stats(self) -> None:
         with self._lock:
             _native.check("mo_reset_stats", self._lib.mo_reset_stats(self._handle))
+            self._ahead_counts = dict.fromkeys(self._ahead_counts, 0)
 
     def trim(self) -> None:
         with self._lock:

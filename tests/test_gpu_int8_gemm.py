@@ -269,8 +269,11 @@ def test_library_path_is_the_eager_path_bit_for_bit(rows, in_f, out_f) -> None:
         quant_kernels.int8_linear_forward(x, w, scale, b, path="triton")
 
 
+# Besides the config-5 shapes: 8000 x 1024 x 5008 (forward) and 8000 x 5008 x 1024 (input
+# gradient) run the register kernel alone on 640 large tiles with ragged rows and columns, over
+# a reduction of 16 steps that its six-step loop pads to 18.
 @pytest.mark.parametrize("rows,in_f,out_f", [(17792, 3072, 3072), (17792, 3072, 24576), (17792, 12288, 3072),
-                                             (4000, 4096, 4000)])
+                                             (4000, 4096, 4000), (8000, 1024, 5008), (8000, 5008, 1024)])
 def test_register_and_lds_kernels_agree_bitwise(rows, in_f, out_f) -> None:
     """The large tile's two kernels (weights decoded in registers, or into LDS) add the same
     products in the same order: forward and input gradient are equal bit for bit."""
