@@ -1435,8 +1435,8 @@ def main() -> int:
     parser.add_argument("--layers", type=int, default=CONFIG3["num_layers"])
     parser.add_argument("--no-parity", action="store_true")
     parser.add_argument("--stage-slots", type=int, default=4)
-    parser.add_argument("--restore-slots", type=int, default=8)
-    parser.add_argument("--prefetch-depth", type=int, default=8,
+    parser.add_argument("--restore-slots", type=int, default=16)
+    parser.add_argument("--prefetch-depth", type=int, default=16,
                         help="groups the engine prefetches ahead of backward after each restored group")
     parser.add_argument("--slot-mib", type=int, default=128)
     parser.add_argument("--restore-ahead-mib", type=int, default=None,

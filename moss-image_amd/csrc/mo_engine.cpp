@@ -1139,7 +1139,7 @@ struct Engine {
     if (c) cfg = *c;
     if (!cfg.stage_slot_bytes) cfg.stage_slot_bytes = 128ull << 20;
     if (!cfg.stage_slots) cfg.stage_slots = 4;
-    if (!cfg.restore_slots) cfg.restore_slots = 8;
+    if (!cfg.restore_slots) cfg.restore_slots = 16;
     if (!cfg.host_chunk_bytes) cfg.host_chunk_bytes = 1ull << 30;
     if (!cfg.copy_kernel_blocks) cfg.copy_kernel_blocks = 16;
     if (cfg.stage_slot_bytes < 2 * kMinPiece || cfg.stage_slot_bytes % kPieceAlign)

@@ -40,13 +40,18 @@ class EngineConfig:
 
     stage_slot_bytes: int = 128 << 20
     stage_slots: int = 4
-    # eight restore slots: a non-checkpointed block's coded saves span about five slots at
+    # sixteen restore slots: a non-checkpointed block's coded saves span about five slots at
     # 128 MiB, and with four the H2D of a block's later segments waited for its earlier
-    # segments' unpacks to run on the GPU (regime B 0.708 -> 0.645 s/it at six); with a
-    # checkpointed block's one small segment per group, eight slots and prefetch_depth 8 let
-    # the trainer's thread run about seven blocks ahead of the GPU in backward (100 ms of host
-    # work per step: 41 -> 10 ms exposed; regime A and B unchanged)
-    restore_slots: int = 8
+    # segments' unpacks to run on the GPU (regime B 0.708 -> 0.645 s/it at six). With a
+    # checkpointed block's one small segment per group, the slots bound how far ahead of the
+    # GPU the backward's H2D can run: the trainer's thread runs several blocks ahead of the GPU,
+    # and a slot is free only once the GPU has scattered its previous group. At eight, about a
+    # third of the groups a restore could take along (restore_ahead_bytes) were still in
+    # flight when asked for; at sixteen (prefetch_depth 16) none were, the unpack launches of a
+    # 1024^2 checkpointed step grew from 48 to 132 MB (4.85 -> 5.78 TB/s) and the trainer's
+    # thread blocked for an H2D 12 instead of 93 times per leg. The cost is 1 GiB more device
+    # memory at 128 MiB slots (a checkpoint-only trainer can take 32 MiB slots instead).
+    restore_slots: int = 16
     host_limit_bytes: int = 0
     host_chunk_bytes: int = 1 << 30
     timing: bool = False
@@ -82,13 +87,14 @@ class EngineConfig:
     # (mo_prefetch_groups: a farther group only when all of it fits). With small groups (a
     # checkpointed block's inputs) this lets the trainer's thread run that many blocks ahead of
     # the GPU without waiting for an H2D.
-    prefetch_depth: int = 8
+    prefetch_depth: int = 16
     # When autograd asks for a group, the groups backward needs next are scattered in the same
     # kernel launch if their bytes are already on the device (H2D landed, or still staged),
     # up to this many payload bytes in all: a checkpointed block's inputs (about 30 MB at
     # 1024^2) are too small for one launch to reach the HBM copy rate, several together are
-    # not. Their restored tensors wait in the cache until asked for. 0: one group per unpack.
-    restore_ahead_bytes: int = 96 << 20
+    # not (96 MiB: 93 MB launches at 5.43 TB/s; 192 MiB: 132 MB at 5.78 TB/s). Their restored
+    # tensors wait in the cache until asked for. 0: one group per unpack.
+    restore_ahead_bytes: int = 192 << 20
     dedupe: bool = True
     # Gather kernels of consecutive saves are launched together, one kernel per staging segment
     # when it closes (before its D2H), instead of one per save: fewer, larger launches that run
