@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 16
+#define MO_ABI_VERSION 17
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -120,6 +120,12 @@ typedef struct mo_config {
                                    buffers; where they would pass it, or their
                                    allocation fails, segments cross raw and the engine
                                    tries again at the next forward                    */
+  uint64_t commit_batch_bytes;  /* [0 = off] a segment closed by mo_commit waits, with its
+                                   gathers, for later commits until this many bytes of
+                                   such segments (or the staging slot) are full; then one
+                                   launch gathers them all and their D2Hs follow. No
+                                   reference counterpart (the reference copies each save
+                                   at its hook)                                         */
 } mo_config;
 
 /* Where one packed tensor lives: its group (one block's saves) and index in the group. */
@@ -236,7 +242,9 @@ int mo_destroy(mo_engine* engine);
  *
  * The gather kernels of consecutive calls on one stream are batched: they are launched, in
  * stream order, as one kernel per staging segment when the segment closes (its slot fills, or
- * mo_commit / mo_unpack of the group closes it), before a call on another stream, and at
+ * mo_commit / mo_unpack of the group closes it; with commit_batch_bytes, commits' segments
+ * gather together up to that many bytes or the slot's end, and any unpack, prefetch, release
+ * or synchronize launches them first), before a call on another stream, and at
  * mo_synchronize or mo_pack_flush. The caller therefore keeps the memory of every tensor it
  * passed valid (not freed, not written) until mo_pack_progress reports the call as launched;
  * after that the usual stream-ordered reuse applies. MO_FLAG_EAGER_PACK launches every call's
@@ -247,7 +255,8 @@ int mo_pack(mo_engine* engine, const mo_tensor* tensors, int n, uint64_t stream,
  * of its gather kernels enqueued. No reference counterpart: the reference copies at once. */
 int mo_pack_progress(mo_engine* engine, uint64_t* calls, uint64_t* launched);
 
-/* Launch every pending gather kernel now (on the stream of the calls that made them). */
+/* Launch every pending gather kernel now (on the stream of the calls that made them), and
+ * issue the D2H of every committed segment that was waiting for them. */
 int mo_pack_flush(mo_engine* engine);
 
 /* Byte equality of nbytes at device addresses a and b (both 16-byte aligned), checked by a

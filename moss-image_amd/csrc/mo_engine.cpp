@@ -434,6 +434,8 @@ struct Engine {
   uint64_t pack_launched = 0;  // every call numbered <= this has all its kernels enqueued
   bool in_pack = false;        // a flush inside a call leaves that call's later pieces pending
 
+  // Launch the pending gathers, then issue the D2H of the committed segments that waited for
+  // them (commit_batch_bytes), in commit order.
   int flush_packs() {
     if (pend) {
       const int rc = pend->flush();
@@ -442,8 +444,25 @@ struct Engine {
       if (rc) return hip_fail(rc, "pack kernel launch");
     }
     pack_launched = in_pack ? pack_calls - 1 : pack_calls;
+    std::vector<Closing> waiting;
+    waiting.swap(closing);
+    closing_bytes = 0;
+    for (const Closing& c : waiting) {
+      Group* g = find(c.group);
+      if (!g) continue;  // release() flushes first, so this does not happen
+      if (int rc = issue_d2h(*g, c.seg, c.stream)) return rc;
+    }
     return 0;
   }
+
+  // Segments closed by mo_commit whose gathers (and so D2H) wait for later commits.
+  struct Closing {
+    uint64_t group;
+    uint32_t seg;
+    hipStream_t stream;
+  };
+  std::vector<Closing> closing;
+  uint64_t closing_bytes = 0;
 
   // The open group is released before its D2H: its pending gathers never need to run.
   void discard_packs() {
@@ -558,14 +577,33 @@ struct Engine {
   }
 
   // ---- forward ----
-  int close_segment(hipStream_t stream) {
+  // Close the open segment and send it: launch the pending gathers, then its D2H. With
+  // `deferrable` (a commit), while the link is not behind and no coding is asked for, the
+  // segment may instead wait, gathers and all, for later commits' (commit_batch_bytes); a
+  // later flush sends them together. *deferred says which happened.
+  int close_segment(hipStream_t stream, bool deferrable = false, bool* deferred = nullptr) {
+    if (deferred) *deferred = false;
     if (!open_group || open_seg < 0) return 0;
-    if (int rc = flush_packs()) return rc;
     const uint32_t si = (uint32_t)open_seg;
     Segment& seg = open_group->segs[si];
-    StageSlot& slot = stage[seg.stage_slot];
-    seg.bytes = slot.used - seg.stage_off;
+    seg.bytes = stage[seg.stage_slot].used - seg.stage_off;
     open_seg = -1;
+    if (deferrable && cfg.commit_batch_bytes && pend && pend_stream == stream && !link_behind &&
+        !(cfg.flags & MO_FLAG_WIRE_CODING) && closing_bytes + seg.bytes < cfg.commit_batch_bytes) {
+      closing.push_back(Closing{open_group->id, si, stream});
+      closing_bytes += seg.bytes;
+      if (deferred) *deferred = true;
+      return 0;
+    }
+    if (int rc = flush_packs()) return rc;
+    return issue_d2h(*open_group, si, stream);
+  }
+
+  // The D2H of a closed segment whose gathers are launched (coded first if the link is behind).
+  int issue_d2h(Group& g, uint32_t si, hipStream_t stream) {
+    Segment& seg = g.segs[si];
+    StageSlot& slot = stage[seg.stage_slot];
+    const uint64_t gid = g.id;
     if (wire_wanted(seg.bytes) && wire_ready()) {
       const uint64_t cap = wire_capacity(seg.bytes);
       if (slot.wire_used + cap <= wire_slot_bytes) {
@@ -584,7 +622,7 @@ struct Engine {
         st.d2h_copies++;
         st.wire_segments++;
         st.wire_raw_bytes += seg.bytes;
-        deferred.counts.push_back(PendingCount{seg.host, seg.d2h, true, open_group->id, si});
+        deferred.counts.push_back(PendingCount{seg.host, seg.d2h, true, gid, si});
         return 0;
       }
     }
@@ -655,6 +693,11 @@ struct Engine {
   }
 
   int advance_slot(hipStream_t stream) {
+    // segments waiting for their gathers (commit_batch_bytes) go out before the ring moves on:
+    // the slot reached next may hold some of them, and its wait below covers only copies
+    // already issued
+    if (!closing.empty())
+      if (int rc = flush_packs()) return rc;
     stage_cur = (stage_cur + 1) % (int)stage.size();
     StageSlot& s = stage[stage_cur];
     st.stage_slot_waits++;
@@ -776,9 +819,13 @@ struct Engine {
 
   int commit(hipStream_t stream, uint64_t* gid) {
     *gid = kNone;
-    if (!open_group) return flush_packs();
-    if (int rc = close_segment(stream)) return rc;
-    if (int rc = flush_packs()) return rc;  // a group with no segment yet
+    // no open group: nothing to close; committed segments that wait keep waiting
+    if (!open_group) return closing.empty() ? flush_packs() : 0;
+    bool waits = false;
+    if (int rc = close_segment(stream, true, &waits)) return rc;
+    // a group with no segment yet launches what is pending, unless commits are gathering
+    if (!waits && closing.empty())
+      if (int rc = flush_packs()) return rc;
     open_group->open = false;
     *gid = open_group->id;
     open_group = nullptr;
@@ -861,6 +908,8 @@ struct Engine {
   }
 
   int prefetch(uint64_t gid, hipStream_t stream) {
+    if (!closing.empty())
+      if (int rc = flush_packs()) return rc;
     process_pending(false);
     Group* g = find(gid);
     if (!g) return fail(MO_E_INVALID, "mo_prefetch: unknown group " + std::to_string(gid));
@@ -908,6 +957,8 @@ struct Engine {
   int unpack_groups(const uint64_t* gids, const uint64_t* dst, const uint32_t* counts, uint32_t n,
                     hipStream_t stream, uint32_t* unpacked) {
     if (int rc = check_link()) return rc;
+    if (!closing.empty())  // segments waiting for their gathers go out before any is read
+      if (int rc = flush_packs()) return rc;
     link_behind = false;
     busy_wraps = 0;
     wire_unavailable = false;  // the next forward may try to allocate the wire buffers again
@@ -1039,6 +1090,11 @@ struct Engine {
   int release(uint64_t gid) {
     Group* g = find(gid);
     if (!g) return fail(MO_E_INVALID, "mo_release: unknown group " + std::to_string(gid));
+    if (!closing.empty()) {
+      // Committed segments wait for gathers pending beside this group's: launch them all (the
+      // open group's too, while their sources still live) and send the waiting segments.
+      if (int rc = flush_packs()) return rc;
+    }
     if (g == open_group) {
       // No D2H was issued: abandon the staging space and the gathers not launched yet
       // (their sources may be freed as soon as this returns).
@@ -1483,7 +1539,7 @@ int mo_group_info(mo_engine* engine, uint64_t group, uint32_t* entries, uint64_t
   if (d2h_complete) {
     int done = g->open ? 0 : 1;
     for (auto& seg : g->segs)
-      if (!mo::idle(seg.d2h)) done = 0;
+      if (!seg.committed || !mo::idle(seg.d2h)) done = 0;  // not committed: waits for its gathers
     *d2h_complete = done;
   }
   return 0;

@@ -403,6 +403,10 @@ class _ActivationOffload:
             self._poll()
         stream = torch.cuda.current_stream(self.device).cuda_stream
         last = self.engine.commit(stream)
+        # the forward is over: gathers still waiting for later commits run now, their segments
+        # go to the host, and the engine lets go of their sources (which would otherwise keep
+        # the forward's graph alive until the next engine call)
+        self.engine.flush()
         if self.engine.config.prefetch and exc[0] is None:
             # Backward starts with the last group, and with every group holding a save the
             # forward made repeatedly (e.g. one RoPE table checkpointed with every block): start

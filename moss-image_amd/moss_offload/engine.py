@@ -104,6 +104,13 @@ class EngineConfig:
     # nearer the HBM copy rate. The engine keeps each save's source tensor alive until its
     # kernel is launched (at most one staging slot of saves). False: launch at every save.
     batch_packs: bool = True
+    # A checkpointed block's saves (one group, about 30 MB at 1024^2) are gathered by one
+    # launch too small to reach the HBM copy rate. A group's segment closed by its commit
+    # waits instead, gathers and all, for the next groups' until this many bytes (or the
+    # staging slot's end); then one launch gathers them all and their D2Hs follow in order.
+    # Any restore, prefetch, release or synchronize sends the waiting segments first. Off
+    # while wire coding is on (the link sets the pace there). 0: every commit sends its own.
+    commit_batch_bytes: int = 128 << 20
     # A float32 save that is the untouched output of a bfloat16 -> float32 cast (every element's
     # low 16 bits are zero) crosses the link as its high halves: the same bits in half the bytes
     # (MO_TENSOR_BF16_HIGH). The hook decides from the autograd graph; False copies it whole.
@@ -135,7 +142,7 @@ class EngineConfig:
             raise ValueError(f"wire_coding must be one of {tuple(WIRE_CODINGS)}, got {self.wire_coding!r}")
         for name in ("stage_slot_bytes", "stage_slots", "restore_slots", "host_limit_bytes", "host_chunk_bytes",
                      "copy_kernel_blocks", "d2h_engine", "h2d_engine", "prefetch_depth", "keep_last_blocks",
-                     "wire_device_limit", "restore_ahead_bytes"):
+                     "wire_device_limit", "restore_ahead_bytes", "commit_batch_bytes"):
             value = getattr(self, name)
             if isinstance(value, bool) or not isinstance(value, int) or value < 0:
                 raise ValueError(f"{name} must be a non-negative integer, got {value!r}")
@@ -163,6 +170,7 @@ class EngineConfig:
         cfg.d2h_engine = self.d2h_engine
         cfg.h2d_engine = self.h2d_engine
         cfg.wire_device_limit = self.wire_device_limit
+        cfg.commit_batch_bytes = self.commit_batch_bytes
         return cfg
 
 
@@ -215,6 +223,7 @@ class OffloadEngine:
         self._held: deque[tuple[int, torch.Tensor, int]] = deque()
         self._calls = ctypes.c_uint64()
         self._launched = ctypes.c_uint64()
+        self._committed_calls = 0  # pack calls made before the last commit (their groups are committed)
         # restores that asked for groups ahead, the groups offered, the groups restored ahead
         self._ahead_counts = {"restores": 0, "offered": 0, "restored": 0}
 
@@ -255,6 +264,7 @@ class OffloadEngine:
                 group.committed = True
             if self._held:
                 self._hold()
+            self._committed_calls = self._calls.value if self._held else self._committed_calls
             return None if gid == _native.NO_GROUP else gid
 
     def acquire(self, gid: int, idx: int, reader: bool = True) -> bool:
@@ -290,11 +300,13 @@ class OffloadEngine:
                     del self._live[pos]
                 _native.check("mo_release", self._lib.mo_release(self._handle, gid))
                 if self._held:
-                    # releasing the open group drops its pending gathers: their sources were
-                    # never read, so a later in-place change to them is no error
-                    self._hold(check=False)
+                    # Releasing the open group drops its pending gathers: their sources were
+                    # never read, so a later in-place change to them is no error. Gathers of
+                    # committed groups that waited (commit_batch_bytes) ran in the release, and
+                    # are checked.
+                    self._hold(check_upto=self._committed_calls)
 
-    def _hold(self, source: torch.Tensor | None = None, check: bool = True) -> None:
+    def _hold(self, source: torch.Tensor | None = None, check_upto: int | None = None) -> None:
         """Keep ``source`` (of the pack call just made) alive while its gather is pending, and
         let go of the sources whose gathers the engine has launched. Launched kernels are
         stream-ordered before anything that later reuses their memory.
@@ -304,7 +316,8 @@ class OffloadEngine:
         saved tensor, which it skips while saved-tensor hooks are installed) would be offloaded
         with its new bytes, where a copy at the save keeps the old ones. That raises here: the
         same program without offloading fails autograd's check in backward, and
-        ``batch_packs=False`` copies at the save."""
+        ``batch_packs=False`` copies at the save. ``check_upto``: check only the sources of pack
+        calls numbered at most that (the others' gathers were dropped, not run)."""
 
         _native.check("mo_pack_progress", self._lib.mo_pack_progress(
             self._handle, ctypes.byref(self._calls), ctypes.byref(self._launched)))
@@ -312,8 +325,8 @@ class OffloadEngine:
             self._held.append((self._calls.value, source, source._version))
         launched = self._launched.value
         while self._held and self._held[0][0] <= launched:
-            _, tensor, version = self._held.popleft()
-            if check and tensor._version != version:
+            call, tensor, version = self._held.popleft()
+            if (check_upto is None or call <= check_upto) and tensor._version != version:
                 raise RuntimeError(
                     "a tensor saved for backward was modified in place before the offload engine "
                     "gathered it (autograd would reject this without offloading); "

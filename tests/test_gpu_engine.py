@@ -23,6 +23,8 @@ MiB = 1 << 20
 
 
 def _engine(**kw) -> OffloadEngine:
+    # each commit sends its own segments unless a test asks for commit batching
+    kw.setdefault("commit_batch_bytes", 0)
     cfg = EngineConfig(stage_slot_bytes=2 * MiB, stage_slots=3, restore_slots=2, host_chunk_bytes=8 * MiB, **kw)
     return OffloadEngine(torch.device("cuda", 0), cfg)
 
@@ -713,6 +715,80 @@ def test_small_groups_restored_ahead_share_one_scatter_launch() -> None:
         assert st["bytes_unpacked"] == st["bytes_packed"] and st["copy_failures"] == 0
         for members in handles:
             for _, gid, idx in members:
+                engine.drop(gid, idx)
+        engine.synchronize()
+        assert engine.stats()["host_bytes_in_use"] == 0
+    finally:
+        engine.close()
+
+
+def _d2h_complete(engine, gid: int) -> bool:
+    import ctypes
+
+    done = ctypes.c_int(-1)
+    assert engine._lib.mo_group_info(engine._handle, gid, None, None, ctypes.byref(done)) == 0
+    return bool(done.value)
+
+
+def test_commits_gather_together_up_to_commit_batch_bytes() -> None:
+    """commit_batch_bytes: a committed group's segment waits, gathers and all, for later
+    commits until the batch would pass the limit; then one launch gathers the waiting groups
+    and their D2Hs follow. A restore, a release and a filled staging slot send what waits
+    first. Every restore is bitwise; a waiting group reports its D2H as not complete."""
+
+    device = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(23)
+    # 2 MB groups; an 8 MiB slot holds four of them
+    cfg = EngineConfig(stage_slot_bytes=8 * MiB, stage_slots=3, restore_slots=4, host_chunk_bytes=32 * MiB,
+                       commit_batch_bytes=5 * MiB, wire_coding="off", prefetch=False)
+    engine = OffloadEngine(device, cfg)
+    try:
+        groups = []
+
+        def add_group():
+            t = torch.randn(500_000, generator=g).to(device)
+            gid, idx = engine.pack(t, stream)
+            engine.commit(stream)
+            groups.append((t, gid, idx))
+            return gid
+
+        base = engine.stats()["pack_launches"]
+        g0 = add_group()
+        g1 = add_group()
+        # 4 MB wait: nothing gathered, nothing sent, their sources held
+        assert engine.stats()["pack_launches"] - base == 0
+        assert engine.stats()["d2h_copies"] == 0 and engine._held
+        assert not _d2h_complete(engine, g0) and not _d2h_complete(engine, g1)
+        add_group()  # 6 MB would pass 5 MiB: the three go out in one launch
+        assert engine.stats()["pack_launches"] - base == 1
+        assert engine.stats()["d2h_copies"] == 3 and not engine._held
+        g3 = add_group()  # waits again
+        assert engine.stats()["d2h_copies"] == 3
+        # the fifth group does not fit the slot's last 0.39 MB: the ring moves on, which sends
+        # group 3 first; group 4 then waits in the next slot
+        g4 = add_group()
+        assert engine.stats()["d2h_copies"] == 4 and not _d2h_complete(engine, g4)
+        g5 = add_group()  # waits beside group 4
+        assert engine.stats()["d2h_copies"] == 4 and not _d2h_complete(engine, g5)
+        # a release of a waiting group sends the waiting segments first, then drops it
+        t5, _, idx5 = groups[5]
+        engine.drop(g5, idx5)
+        assert engine.stats()["d2h_copies"] == 6 and not engine._held
+        g6 = add_group()  # waits
+        assert engine.stats()["d2h_copies"] == 6 and not _d2h_complete(engine, g6)
+        # restores, newest first, each bitwise (a restore sends what waits first)
+        for t, gid, idx in reversed(groups):
+            if gid == g5:
+                continue
+            assert_bitwise(engine.restore(gid, idx, stream), t)
+        engine.synchronize()
+        assert all(_d2h_complete(engine, gid) for _, gid, _ in groups if gid != g5)
+        assert _d2h_complete(engine, g3)
+        st = engine.stats()
+        assert st["bytes_unpacked"] == st["bytes_packed"] - t5.numel() * 4 and st["copy_failures"] == 0
+        for _, gid, idx in groups:
+            if gid != g5:
                 engine.drop(gid, idx)
         engine.synchronize()
         assert engine.stats()["host_bytes_in_use"] == 0
