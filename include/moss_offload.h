@@ -170,7 +170,7 @@ typedef struct mo_stats {
                                   wire_device_limit)                                        */
   uint64_t ahead_restored;     /* further groups of mo_unpack_groups restored               */
   uint64_t ahead_not_resident; /* further groups left: a segment was not in a restore slot  */
-  uint64_t ahead_in_flight;    /* further groups left: a segment's H2D had not landed       */
+  uint64_t ahead_in_flight;    /* further groups left: a segment's H2D had not started      */
 } mo_stats;
 
 typedef struct mo_engine mo_engine;
@@ -299,9 +299,10 @@ int mo_unpack(mo_engine* engine, uint64_t group, const uint64_t* dst, uint32_t n
 
 /* Restore groups[0] as mo_unpack does (its entries' addresses are dst[0 .. counts[0])), then
  * each further groups[k] (the next counts[k] addresses) only if every segment it needs can be
- * read now without waiting for a copy: resident in a restore slot with its H2D landed, or still
- * in its staging slot. unpacked[k] is set to 1 for each group restored. The first group's last
- * segment and the further groups are scattered together, in as few kernel launches as their
+ * read now with at most a short wait: resident in a restore slot with its H2D landed or handed
+ * to the copy engine, or still in its staging slot. unpacked[k] is set to 1 for each group
+ * restored. The first group's last segment and the further groups are scattered together, in
+ * as few kernel launches as their
  * pieces allow (small groups, such as the inputs of checkpointed blocks, then share one large
  * launch). No reference counterpart: the reference restores one saved tensor per unpack
  * (activation_offload.py:136-147). */

@@ -1013,9 +1013,11 @@ struct Engine {
     return rc ? rc : rc2;
   }
 
-  // 0 when every segment of `g` with a destination in `dst` can be scattered on `stream` now
-  // without waiting for a copy; else 1 (open, or a segment not in a restore slot) or 2 (a
-  // segment's H2D still running).
+  // 0 when every segment of `g` with a destination in `dst` can be scattered on `stream` now,
+  // with at most a short wait: staged, or resident with its H2D landed or started (on the
+  // SDMA link: handed to the engine, so the wait is at most the transfer of what is queued
+  // ahead of it; on HIP streams: the GPU waits); else 1 (open, or a segment not in a restore
+  // slot) or 2 (a segment's H2D still waiting for the GPU to free its slot).
   int not_ready(const Group& g, const uint64_t* dst, hipStream_t stream) const {
     if (g.open) return 1;
     int why = 0;
@@ -1025,7 +1027,7 @@ struct Engine {
       for (const Piece& p : seg.pieces) any = any || dst[p.entry] != 0;
       if (!any || staged(seg, stream)) continue;
       if (!resident(g, si)) return 1;
-      if (!idle(seg.h2d)) why = 2;
+      if (seg.h2d && !seg.h2d->started()) why = 2;
     }
     return why;
   }

@@ -116,6 +116,8 @@ struct SdmaCopy : CopyState {
   bool dma_stamped = true;  // every part completed with stamps
   bool done() const override { return finished.load(std::memory_order_acquire); }
   bool failed() const override { return fail.load(std::memory_order_acquire); }
+  // handed to the engines: its compute-stream event and copy dependencies have passed
+  bool started() const override { return done() || issued.load(std::memory_order_acquire); }
 };
 using SdmaRef = std::shared_ptr<SdmaCopy>;
 
@@ -757,6 +759,8 @@ struct StreamCopy : CopyState {
     return true;
   }
   bool failed() const override { return false; }
+  // enqueued on a copy stream, which a consumer waits for on the GPU (hipStreamWaitEvent)
+  bool started() const override { return true; }
 };
 using StreamRef = std::shared_ptr<StreamCopy>;
 

@@ -37,6 +37,9 @@ struct CopyState {
   // The copy finished (or failed) and the transport holds no more references to it.
   virtual bool done() const = 0;
   virtual bool failed() const = 0;
+  // The copy no longer waits for anything but the transport itself: waiting for it takes at
+  // most the transfer time of what is queued ahead of it on its engine.
+  virtual bool started() const { return done(); }
 };
 using CopyRef = std::shared_ptr<CopyState>;
 

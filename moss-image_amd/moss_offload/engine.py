@@ -92,7 +92,8 @@ class EngineConfig:
     # the GPU without waiting for an H2D.
     prefetch_depth: int = 16
     # When autograd asks for a group, the groups backward needs next are scattered in the same
-    # kernel launch if their bytes are already on the device (H2D landed, or still staged),
+    # kernel launch if their bytes are on the device or on their way (H2D landed or handed to
+    # the copy engine, or still staged),
     # up to this many payload bytes in all: a checkpointed block's inputs (about 30 MB at
     # 1024^2) are too small for one launch to reach the HBM copy rate, several together are
     # not (96 MiB: 93 MB launches at 5.43 TB/s; 192 MiB: 132 MB at 5.78 TB/s). Their restored
