@@ -63,7 +63,9 @@ def _attention_core(query, key, value, cu_seqlens):
     if cu_seqlens is None:
         return F.scaled_dot_product_attention(query, key, value)
     if value.device.type == "cuda":
-        lengths = (cu_seqlens[1:] - cu_seqlens[:-1]).tolist()
+        lengths = getattr(cu_seqlens, "host_lengths", None)
+        if lengths is None:  # a cu_seqlens built elsewhere (or restored by the offload hooks)
+            lengths = (cu_seqlens[1:] - cu_seqlens[:-1]).tolist()
         parts = zip(query.split(lengths, 2), key.split(lengths, 2), value.split(lengths, 2))
         return torch.cat([F.scaled_dot_product_attention(q, k, v) for q, k, v in parts], 2)
     lengths = cu_seqlens[1:] - cu_seqlens[:-1]
@@ -261,7 +263,12 @@ def checkpointed_layer_indices(depth: int, fraction: float) -> frozenset[int]:
 
 
 def _cumulative_lengths(lengths, device):
-    return torch.tensor([0, *lengths], device=device, dtype=torch.int64).cumsum(0)
+    cu = torch.tensor([0, *lengths], device=device, dtype=torch.int64).cumsum(0)
+    # the split sizes as host integers, so that the per-sequence attention below need not read
+    # them back from the device (a synchronisation in every attention call, which would keep
+    # the host in step with the GPU for the whole packed traversal)
+    cu.host_lengths = tuple(int(n) for n in lengths)
+    return cu
 
 
 class MOSSImageTransformer(nn.Module):
