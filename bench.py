@@ -772,11 +772,23 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 C5_GEMMS = {"qkvo": ((3072, 3072), 4), "ffn_up_gate": ((2 * 12288, 3072), 1), "ffn_down": ((3072, 12288), 1)}
 
 
-def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
+def int8_gemm_leg(device, iters: int = 20, warmup: int = 3, rounds: int = 3) -> dict:
     """Config-5 int8 weight-only GEMMs (moss_offload.quant_kernels) on the packed token count of
-    one config-5 batch: forward and input gradient on the HIP kernels against the eager path
-    (decode the weight, then F.linear / matmul on hipBLASLt). Timed with HIP events on the stream
-    the kernels run on; TFLOP/s = 2 rows in out / average call time."""
+    one config-5 batch, forward and input gradient, by path:
+
+      hip        the default dispatch (``auto``): the fused kernels for reductions at least four
+                 times the output width whose plan splits a reduction, else one HIP decode and
+                 the library GEMM
+      fused      the fused MFMA kernels alone (weight decoded in registers)
+      fused_lds  the same with the large tile decoding the weight into LDS
+      library    one HIP decode, then the eager path's GEMM call
+      eager      the reference's eager path: decode (cast, scale), then F.linear / matmul
+
+    Timed with HIP events on the stream the kernels run on, ``rounds`` interleaved rounds of
+    ``iters`` calls per path (after ``warmup`` calls), median of the rounds; TFLOP/s = 2 rows in
+    out / call time."""
+
+    import statistics
 
     import torch
     import torch.nn.functional as F
@@ -799,9 +811,20 @@ def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
         stop.synchronize()
         return start.elapsed_time(stop) / 1e3 / iters
 
+    def with_kernel(kernel, fn):
+        def run():
+            qk.set_kernel(kernel)
+            try:
+                fn()
+            finally:
+                qk.set_kernel("registers")
+        return run
+
+    paths = ("hip", "fused", "fused_lds", "library", "eager")
     shapes = {}
-    block = {"hip": 0.0, "fused": 0.0, "fused_lds": 0.0, "eager": 0.0}
+    block = dict.fromkeys(paths, 0.0)
     block_flop = 0.0
+    ramped = False
     for name, ((out_f, in_f), count) in C5_GEMMS.items():
         x = torch.randn(rows, in_f, device=device, generator=g).to(torch.bfloat16)
         dy = torch.randn(rows, out_f, device=device, generator=g).to(torch.bfloat16)
@@ -809,39 +832,47 @@ def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
         s = torch.empty(out_f, device=device).uniform_(1e-3, 2e-2, generator=g)
         assert qk.resolve_backend("auto", x, w, s, torch.bfloat16) == "hip"
         flop = 2.0 * rows * in_f * out_f
-        qk.set_kernel("lds")  # the large tile decoding the weight into LDS, for comparison
-        t_lds = {"fused_lds_fwd": timed(lambda: qk.int8_linear_forward(x, w, s, path="fused")),
-                 "fused_lds_bwd": timed(lambda: qk.int8_linear_backward(dy, w, s, x.shape, path="fused"))}
-        qk.set_kernel("registers")
-        t = {
-            **t_lds,
-            "hip_fwd": timed(lambda: qk.int8_linear_forward(x, w, s)),
-            "hip_bwd": timed(lambda: qk.int8_linear_backward(dy, w, s, x.shape)),
-            "fused_fwd": timed(lambda: qk.int8_linear_forward(x, w, s, path="fused")),
-            "fused_bwd": timed(lambda: qk.int8_linear_backward(dy, w, s, x.shape, path="fused")),
-            "eager_fwd": timed(lambda: F.linear(x, qk.decode(w, s, torch.bfloat16))),
-            "eager_bwd": timed(lambda: dy.matmul(qk.decode(w, s, torch.bfloat16))),
+        calls = {
+            "hip_fwd": lambda: qk.int8_linear_forward(x, w, s),
+            "hip_bwd": lambda: qk.int8_linear_backward(dy, w, s, x.shape),
+            "fused_fwd": lambda: qk.int8_linear_forward(x, w, s, path="fused"),
+            "fused_bwd": lambda: qk.int8_linear_backward(dy, w, s, x.shape, path="fused"),
+            "fused_lds_fwd": with_kernel("lds", lambda: qk.int8_linear_forward(x, w, s, path="fused")),
+            "fused_lds_bwd": with_kernel("lds", lambda: qk.int8_linear_backward(dy, w, s, x.shape, path="fused")),
+            "library_fwd": lambda: qk.int8_linear_forward(x, w, s, path="library"),
+            "library_bwd": lambda: qk.int8_linear_backward(dy, w, s, x.shape, path="library"),
+            "eager_fwd": lambda: F.linear(x, qk.decode(w, s, torch.bfloat16)),
+            "eager_bwd": lambda: dy.matmul(qk.decode(w, s, torch.bfloat16)),
         }
+        if not ramped:  # about a second of GEMMs first, so the clocks have settled
+            for _ in range(8):
+                timed(calls["eager_fwd"])
+            ramped = True
+        samples = {k: [] for k in calls}
+        for _ in range(rounds):
+            for k, fn in calls.items():
+                samples[k].append(timed(fn))
+        t = {k: statistics.median(v) for k, v in samples.items()}
         with torch.no_grad():
             wd = qk.decode(w, s, torch.bfloat16)
             yh, ye = qk.int8_linear_forward(x, w, s).float(), F.linear(x, wd).float()
             gh, ge = qk.int8_linear_backward(dy, w, s, x.shape).float(), dy.matmul(wd).float()
-        rec = {"rows": rows, "in_features": in_f, "out_features": out_f, "per_block": count}
+        rec = {"rows": rows, "in_features": in_f, "out_features": out_f, "per_block": count,
+               "hip_fwd_path": "fused" if not torch.equal(yh, ye) else "library",
+               "hip_bwd_path": "fused" if not torch.equal(gh, ge) else "library"}
         for k, sec in t.items():
             rec[k + "_ms"] = round(sec * 1e3, 4)
+            rec[k + "_ms_range"] = [round(min(samples[k]) * 1e3, 4), round(max(samples[k]) * 1e3, 4)]
             rec[k + "_tflops"] = round(flop / sec / 1e12, 1)
         rec["fwd_vs_eager_max_rel_diff"] = ((yh - ye).abs().max() / ye.abs().max()).item()
         rec["bwd_vs_eager_max_rel_diff"] = ((gh - ge).abs().max() / ge.abs().max()).item()
         shapes[name] = rec
-        block["hip"] += count * (t["hip_fwd"] + t["hip_bwd"])
-        block["fused"] += count * (t["fused_fwd"] + t["fused_bwd"])
-        block["fused_lds"] += count * (t["fused_lds_fwd"] + t["fused_lds_bwd"])
-        block["eager"] += count * (t["eager_fwd"] + t["eager_bwd"])
+        for p_ in paths:
+            block[p_] += count * (t[p_ + "_fwd"] + t[p_ + "_bwd"])
         block_flop += count * 2 * flop
-        log(f"int8 GEMM {name} ({out_f}x{in_f}, {rows} rows): hip fwd {rec['hip_fwd_tflops']} bwd "
-            f"{rec['hip_bwd_tflops']} | fused fwd {rec['fused_fwd_tflops']} bwd {rec['fused_bwd_tflops']} | "
-            f"fused (LDS decode) fwd {rec['fused_lds_fwd_tflops']} bwd {rec['fused_lds_bwd_tflops']} | "
-            f"eager fwd {rec['eager_fwd_tflops']} bwd {rec['eager_bwd_tflops']} TFLOP/s")
+        log(f"int8 GEMM {name} ({out_f}x{in_f}, {rows} rows), TFLOP/s fwd/bwd: "
+            + " | ".join(f"{p_} {rec[p_ + '_fwd_tflops']}/{rec[p_ + '_bwd_tflops']}" for p_ in paths)
+            + f" (hip: {rec['hip_fwd_path']}/{rec['hip_bwd_path']})")
         del x, dy, w, s, wd, yh, ye, gh, ge
     achieved = block_flop / block["hip"] / 1e12
     return {
@@ -850,12 +881,16 @@ def int8_gemm_leg(device, iters: int = 20, warmup: int = 3) -> dict:
         "block_speedup_vs_eager": round(block["eager"] / block["hip"], 4),
         "fused_block_speedup_vs_eager": round(block["eager"] / block["fused"], 4),
         "fused_lds_block_speedup_vs_eager": round(block["eager"] / block["fused_lds"], 4),
+        "library_block_speedup_vs_eager": round(block["eager"] / block["library"], 4),
         "library_rows": qk.LIBRARY_ROWS,
         "library_weight_elements": qk.LIBRARY_WEIGHT,
+        "long_reduction_ratio": qk.LONG_REDUCTION,
+        "timing": f"median of {rounds} interleaved rounds of {iters} calls per path",
         "roofline": {"bound": "mfma",
-                     "kernels": (f"mo_int8_decode_kernel + library GEMM (rows >= {qk.LIBRARY_ROWS} or weight >= "
-                                 f"{qk.LIBRARY_WEIGHT} elements), mo_int8_linear_{{fwd,bwd}}_{{large,small}} "
-                                 "otherwise"),
+                     "kernels": ("auto dispatch: mo_int8_ws_{fwd,kscale} (+ _split, mo_int8_split_reduce) where the "
+                                 f"reduction is >= {qk.LONG_REDUCTION}x the output width and the plan splits it, "
+                                 "mo_int8_decode_kernel + library GEMM for the other calls of "
+                                 f">= {qk.LIBRARY_ROWS} rows or >= {qk.LIBRARY_WEIGHT} weight elements"),
                      "workload": "one config-5 joint block: 4 x qkvo + ffn_up_gate + ffn_down, forward and "
                                  f"input gradient, {rows} rows",
                      "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 17
+#define MO_ABI_VERSION 18
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -435,28 +435,37 @@ int mo_int8_decode(uint64_t w, uint64_t scale, uint64_t out, uint32_t out_featur
  * decode(w)[n][k] = bf16(w[n][k] * bf16(scale[n])), the decode of quant_kernels.py:126-131.
  * x, y, bias: bf16 (bias may be 0); w: int8 [out][in] row-major; scale: fp32 [out].
  * in_features and out_features multiples of 16, each at most 2^20, in * out < 2^31; x, w, y
- * 16-byte aligned. Enqueued on `stream` (one or two kernel launches), no allocation, no host
+ * 16-byte aligned. `workspace` (device, 16-byte aligned, at least
+ * mo_int8_forward_workspace_bytes(rows, in, out) bytes; 0 = none) holds the fp32 partial sums
+ * of the rows whose reduction the launch plan splits over several workgroups (rows that do not
+ * fill a round of large tiles, on the default kernel); without one those rows take the small
+ * tile. Enqueued on `stream` (one to three kernel launches), no allocation, no host
  * synchronisation. Replaces _int8_linear_forward_kernel (quant_kernels.py:100-157). */
 int mo_int8_linear_forward(uint64_t x, uint64_t w, uint64_t scale, uint64_t bias, uint64_t y, uint32_t rows,
-                           uint32_t in_features, uint32_t out_features, uint64_t stream);
+                           uint32_t in_features, uint32_t out_features, uint64_t workspace,
+                           uint64_t workspace_bytes, uint64_t stream);
+/* Bytes of workspace the forward's plan uses for this shape on the current device (0: none). */
+uint64_t mo_int8_forward_workspace_bytes(uint32_t rows, uint32_t in_features, uint32_t out_features);
 
 /* dx[rows][in] = dy[rows][out] . decode(w): the input gradient of the frozen int8 linear (no
  * weight gradient). Same layouts and constraints. `workspace` (device, 16-byte aligned, at
- * least mo_int8_backward_workspace_bytes; 0 = none) receives the transposed int8 weight, which
- * the large-tile kernel reads with the reduction contiguous; without one the large tile decodes
- * the weight through LDS instead (slower, same results). Replaces _int8_linear_backward_kernel
- * (quant_kernels.py:160-209). */
+ * least mo_int8_backward_workspace_bytes(rows, in, out); 0 = none) receives the transposed int8
+ * weight, which the large-tile kernel reads with the reduction contiguous, followed by the
+ * partial sums of split reductions as in the forward; without one the large tile decodes the
+ * weight through LDS instead (slower) and no reduction is split. Replaces
+ * _int8_linear_backward_kernel (quant_kernels.py:160-209). */
 int mo_int8_linear_backward(uint64_t dy, uint64_t w, uint64_t scale, uint64_t dx, uint32_t rows,
                             uint32_t in_features, uint32_t out_features, uint64_t workspace,
                             uint64_t workspace_bytes, uint64_t stream);
-uint64_t mo_int8_backward_workspace_bytes(uint32_t in_features, uint32_t out_features);
+uint64_t mo_int8_backward_workspace_bytes(uint32_t rows, uint32_t in_features, uint32_t out_features);
 
 /* Which kernel takes the large (256 x 256) tiles of the two calls above, process-wide:
  * MO_INT8_KERNEL_REGISTERS (default; reduction a multiple of 64): each wave decodes its columns'
  * int8 weights in registers into the MFMA operand, and the LDS carries only the activations;
  * MO_INT8_KERNEL_LDS: the weight tile is decoded into LDS and shared by the waves. Both give
- * the same results bit for bit; the switch exists to measure one against the other. No
- * reference counterpart (the reference has one Triton kernel per direction). */
+ * the same results bit for bit on the rows the large tile computes; only the default splits
+ * reductions (see mo_int8_linear_forward). The switch exists to measure one kernel against the
+ * other. No reference counterpart (the reference has one Triton kernel per direction). */
 enum { MO_INT8_KERNEL_REGISTERS = 0, MO_INT8_KERNEL_LDS = 1 };
 int mo_int8_set_kernel(uint32_t kernel);
 

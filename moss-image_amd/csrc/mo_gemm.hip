@@ -384,6 +384,10 @@ __device__ __forceinline__ void gemm_body(const __bf16* __restrict__ A, const in
 // accumulation, bf16 output (+ bias). Scales per column (forward: Bq is the weight, scale[N]) or,
 // with kScaleK, per reduction index (input gradient: Bq is the transposed weight, scale[K]).
 // K % 64 == 0; rows past M and columns past N read zeros and store nothing.
+// With kSplit the launch holds `splits` workgroups per tile, each over `split_steps` steps of
+// the reduction (the last over what remains): item t of the XCD-aware numbering takes split
+// t / tiles of tile t % tiles, and stores its fp32 sums, unrounded and without bias, to plane
+// `split` of P ([splits][M][N]); mo_int8_split_reduce then adds the planes in split order.
 //
 // A workgroup owns a 256 x 256 tile with four waves side by side: wave w owns all 256 rows and
 // columns 64 w .. 64 w + 63, as 8 x 2 MFMA 32x32x16 tiles (256 accumulators). A goes global ->
@@ -404,10 +408,11 @@ __device__ __forceinline__ void gemm_body(const __bf16* __restrict__ A, const in
 // DMA has six slices to land. After slice 2 each wave waits for everything but the loads of
 // step s + 2, then the workgroup meets at the one barrier of the step: slice 3 already reads
 // the next step's buffer, and every wave is done with step s - 1's before its refill.
-template <bool kScaleK>
+template <bool kScaleK, bool kSplit>
 __device__ __forceinline__ void ws_body(const __bf16* __restrict__ A, const int8_t* __restrict__ Bq,
                                         const float* __restrict__ scale, const __bf16* __restrict__ bias,
-                                        __bf16* __restrict__ C, int M, int N, int K, int tiles_m) {
+                                        __bf16* __restrict__ C, float* __restrict__ P, int M, int N, int K,
+                                        int tiles_m, int splits, int split_steps) {
   constexpr int kBM = 256, kBN = 256, kWaves = 4, kDma = kBM / 8 / kWaves;  // 8 x 1 KiB A blocks per wave
   // three buffers as distinct objects, chosen at compile time: the compiler can then tell the
   // buffer a DMA writes from the ones being read, and waits only for the DMA that was asked for
@@ -432,24 +437,30 @@ __device__ __forceinline__ void ws_body(const __bf16* __restrict__ A, const int8
   const int lr = lane & 31, h = lane >> 5;
 
   // ---- tile numbering: XCD-aware, then grouped (as gemm_body) ----
-  const int tiles = gridDim.x;
+  const int items = gridDim.x;
+  const int tiles = kSplit ? items / splits : items;
   const int tiles_c = tiles / tiles_m;
   int t;
   {
     const int b = blockIdx.x, xcd = b % kXcds, idx = b / kXcds;
-    const int per = tiles / kXcds, rem = tiles % kXcds;
+    const int per = items / kXcds, rem = items % kXcds;
     t = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
   }
+  const int split = kSplit ? t / tiles : 0;
+  if (kSplit) t -= split * tiles;
   const int group_tiles = kGroupM * tiles_c;
   const int first_m = (t / group_tiles) * kGroupM;
   const int gm = min(tiles_m - first_m, kGroupM);
   const int in_group = t % group_tiles;
   const int m0 = (first_m + in_group % gm) * kBM;
   const int c0 = (in_group / gm) * kBN;
+  // this workgroup's reduction: [k0, k0 + klen); the descriptors start at k0
+  const int k0 = kSplit ? split * split_steps * kBR : 0;
+  const int klen = kSplit ? min(split_steps * kBR, K - k0) : K;
 
-  const rsrc_t ra_src = make_rsrc(A + (size_t)m0 * K, (uint32_t)(min(M - m0, kBM) * K * 2));
-  const rsrc_t rb_src = make_rsrc(Bq + (size_t)c0 * K, (uint32_t)(min(N - c0, kBN) * K));
-  const rsrc_t rs_src = make_rsrc(scale, (uint32_t)((kScaleK ? K : N) * 4));
+  const rsrc_t ra_src = make_rsrc(A + (size_t)m0 * K + k0, (uint32_t)((min(M - m0, kBM) * K - k0) * 2));
+  const rsrc_t rb_src = make_rsrc(Bq + (size_t)c0 * K + k0, (uint32_t)(min(N - c0, kBN) * K - k0));
+  const rsrc_t rs_src = kScaleK ? make_rsrc(scale + k0, (uint32_t)((K - k0) * 4)) : make_rsrc(scale, (uint32_t)(N * 4));
 
   // A by DMA: wave w fills 1 KiB blocks w * kDma + j (8 rows each), as gemm_body.
   uint32_t a_off[kDma];
@@ -480,13 +491,13 @@ __device__ __forceinline__ void ws_body(const __bf16* __restrict__ A, const int8
   }
 
   auto dma = [&](MO_LDS __bf16* As, MO_LDS float* Ss, int r0) {
-    const rsrc_t src = r0 < K ? ra_src : make_rsrc(A, 0u);
+    const rsrc_t src = r0 < klen ? ra_src : make_rsrc(A, 0u);
 #pragma unroll
     for (int j = 0; j < kDma; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (MO_LDS void*)(As + (wave * kDma + j) * 512), 16, a_off[j],
                                                r0 * 2, 0, 0);
     if (kScaleK)  // the step's 64 scales, the same bytes from every wave
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r0 < K ? rs_src : make_rsrc(A, 0u), (MO_LDS void*)Ss, 4, lane * 4,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r0 < klen ? rs_src : make_rsrc(A, 0u), (MO_LDS void*)Ss, 4, lane * 4,
                                                r0 * 4, 0, 0);
   };
   constexpr int kDmaOps = kDma + (kScaleK ? 1 : 0);
@@ -494,11 +505,11 @@ __device__ __forceinline__ void ws_body(const __bf16* __restrict__ A, const int8
   // weight bytes: raw[set][ct][half], loaded for step r0 / 64 (past K: zeros)
   u32x4 raw[2][2][2];
   auto load_half = [&](auto set, auto half, int r0) {
-    constexpr int S = decltype(set)::value, P = decltype(half)::value;
-    const rsrc_t src = r0 < K ? rb_src : make_rsrc(Bq, 0u);
+    constexpr int S = decltype(set)::value, H = decltype(half)::value;
+    const rsrc_t src = r0 < klen ? rb_src : make_rsrc(Bq, 0u);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
-      raw[S][ct][P] = __builtin_amdgcn_raw_buffer_load_b128(src, (int)(b_off[ct] + 16 * P), r0, 0);
+      raw[S][ct][H] = __builtin_amdgcn_raw_buffer_load_b128(src, (int)(b_off[ct] + 16 * H), r0, 0);
   };
 
   bf16x8 fa[2][8], fb[2][2];  // fragments of two slices
@@ -599,7 +610,7 @@ __device__ __forceinline__ void ws_body(const __bf16* __restrict__ A, const int8
   using H1 = std::integral_constant<int, 1>;
   typedef const MO_LDS __bf16* clp;
   typedef const MO_LDS float* csp;
-  const int steps = K / kBR;
+  const int steps = klen / kBR;
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
   using B2 = std::integral_constant<int, 2>;
@@ -615,7 +626,7 @@ __device__ __forceinline__ void ws_body(const __bf16* __restrict__ A, const int8
   read_a((clp)lds_a0, 0, 0);
   decode_b(set0{}, (csp)lds_s0, 0, 0);
   // Steps in sixes: two register sets by step parity, three LDS buffers by step modulo 3. Steps
-  // past K (up to five at the end) read zeros and add nothing.
+  // past the reduction (up to five at the end) read zeros and add nothing.
   for (int s = 0; s < steps; s += 6) {
     step(B0{}, B1{}, B2{}, (s + 0) * kBR, set0{}, set1{});
     step(B1{}, B2{}, B0{}, (s + 1) * kBR, set1{}, set0{});
@@ -625,6 +636,30 @@ __device__ __forceinline__ void ws_body(const __bf16* __restrict__ A, const int8
     step(B2{}, B0{}, B1{}, (s + 5) * kBR, set1{}, set0{});
   }
 
+  if (kSplit) {
+    // ---- epilogue: the fp32 sums into plane `split` of P (rows past M, columns past N outside) ----
+    float* Ps = P + (size_t)split * M * N;
+    const rsrc_t rp_src = make_rsrc(Ps + (size_t)m0 * N, (uint32_t)(min(M - m0, kBM) * N * 4));
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int col = c0 + 64 * wave + 32 * ct + lr;
+      const bool col_ok = col < N;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          // the element read into a scalar first: a bit cast of the vector element itself
+          // reads the vector's first element
+          const float v = acc[i][ct][r];
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), rp_src,
+                                                col_ok ? (int)((uint32_t)(row * N + col) * 4) : (int)kOob, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    return;
+  }
   // ---- epilogue: bias, bf16, store (rows past M and columns past N fall outside) ----
   const rsrc_t rc_src = make_rsrc(C + (size_t)m0 * N, (uint32_t)(min(M - m0, kBM) * N * 2));
   const rsrc_t rbias_src = make_rsrc(bias, bias ? (uint32_t)N * 2 : 0u);
@@ -673,12 +708,55 @@ using Small = Cfg<128, 128, 2, 2>;
 extern "C" __global__ __launch_bounds__(256) void mo_int8_ws_fwd(const __bf16* A, const int8_t* Bq, const float* scale,
                                                                    const __bf16* bias, __bf16* C, int M, int N, int K,
                                                                    int tiles_m) {
-  mo_gemm::ws_body<false>(A, Bq, scale, bias, C, M, N, K, tiles_m);
+  mo_gemm::ws_body<false, false>(A, Bq, scale, bias, C, nullptr, M, N, K, tiles_m, 1, 0);
 }
 extern "C" __global__ __launch_bounds__(256) void mo_int8_ws_kscale(const __bf16* A, const int8_t* Bq,
                                                                      const float* scale, __bf16* C, int M, int N,
                                                                      int K, int tiles_m) {
-  mo_gemm::ws_body<true>(A, Bq, scale, nullptr, C, M, N, K, tiles_m);
+  mo_gemm::ws_body<true, false>(A, Bq, scale, nullptr, C, nullptr, M, N, K, tiles_m, 1, 0);
+}
+// The same with the reduction split over `splits` workgroups per tile (fp32 planes into P).
+extern "C" __global__ __launch_bounds__(256) void mo_int8_ws_fwd_split(const __bf16* A, const int8_t* Bq,
+                                                                         const float* scale, float* P, int M, int N,
+                                                                         int K, int tiles_m, int splits,
+                                                                         int split_steps) {
+  mo_gemm::ws_body<false, true>(A, Bq, scale, nullptr, nullptr, P, M, N, K, tiles_m, splits, split_steps);
+}
+extern "C" __global__ __launch_bounds__(256) void mo_int8_ws_kscale_split(const __bf16* A, const int8_t* Bq,
+                                                                            const float* scale, float* P, int M,
+                                                                            int N, int K, int tiles_m, int splits,
+                                                                            int split_steps) {
+  mo_gemm::ws_body<true, true>(A, Bq, scale, nullptr, nullptr, P, M, N, K, tiles_m, splits, split_steps);
+}
+
+// C[rows][cols] = bf16(P[0] + P[1] + ... + P[splits - 1] (+ bias)), the planes of a split
+// reduction added in split order, so the result does not depend on which workgroup finished
+// first. One lane per 8 consecutive elements (cols % 16 == 0); bias may be null.
+extern "C" __global__ __launch_bounds__(256) void mo_int8_split_reduce(const float* P, const __bf16* bias, __bf16* C,
+                                                                        uint32_t rows, uint32_t cols,
+                                                                        uint32_t splits) {
+  using f32x4 = float __attribute__((ext_vector_type(4)));
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (i >= (uint64_t)rows * (cols / 8)) return;
+  const uint64_t e = i * 8, plane = (uint64_t)rows * cols;
+  f32x4 lo = *(const f32x4*)(P + e), hi = *(const f32x4*)(P + e + 4);
+  for (uint32_t s = 1; s < splits; ++s) {
+    lo += *(const f32x4*)(P + s * plane + e);
+    hi += *(const f32x4*)(P + s * plane + e + 4);
+  }
+  const uint32_t col = (uint32_t)(e % cols);
+  mo_gemm::u32x4 out;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float a = k < 2 ? lo[2 * k] : hi[2 * k - 4], b = k < 2 ? lo[2 * k + 1] : hi[2 * k - 3];
+    if (bias) {
+      a += (float)bias[col + 2 * k];
+      b += (float)bias[col + 2 * k + 1];
+    }
+    out[k] = (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)a) |
+             ((uint32_t)__builtin_bit_cast(unsigned short, (__bf16)b) << 16);
+  }
+  *(mo_gemm::u32x4*)(C + e) = out;
 }
 
 // full: R % 64 == 0; _tail: any multiple of 16
@@ -729,29 +807,44 @@ extern "C" __global__ __launch_bounds__(256) void mo_int8_decode_kernel(const in
 }
 
 // Wt[in][out] = W[out][in]^T for the input gradient on the weight-in-registers kernel, which
-// needs the reduction (out) contiguous. A lane moves a 16 x 4 block: 16 rows of W (out) x 4
-// columns (in), loaded as one dword per row (consecutive lanes: consecutive columns, so each
-// load instruction reads contiguous 256-byte row pieces), and written as 4 rows of Wt x 16 bytes.
-// rows % 16 == 0, cols % 16 == 0.
+// needs the reduction (out) contiguous. A workgroup moves a 128 x 128 tile (grid: row tiles x
+// column tiles, column tiles fastest). Lane t reads 16-byte pieces of W rows 4 (t / 8) + 0..3 at
+// columns 16 (t % 8) (eight lanes per 128-byte row piece), transposes the 4 x 4 byte blocks in
+// registers into 4-byte words of one column and four rows, and exchanges them through LDS
+// ([column][row group], 16-byte chunks XOR-swizzled by column so the word writes of a wave
+// spread over the banks); then lane t writes 64 bytes of Wt row t / 2 (two lanes per 128-byte
+// row piece). rows % 16 == 0, cols % 16 == 0.
 extern "C" __global__ __launch_bounds__(256) void mo_int8_transpose_kernel(const int8_t* w, int8_t* wt,
                                                                           uint32_t rows, uint32_t cols) {
-  const uint32_t col_groups = cols / 4;
-  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-  if (i >= (uint64_t)(rows / 16) * col_groups) return;
-  const uint32_t rg = (uint32_t)(i / col_groups), cg = (uint32_t)(i % col_groups);
-  uint32_t v[16];
+  using mo_gemm::u32x4;
+  __shared__ __attribute__((aligned(16))) uint32_t tile[128 * 32];
+  auto slot = [](int col, int chunk) { return col * 32 + ((chunk ^ ((col + (col >> 4)) & 7)) << 2); };
+  const uint32_t tiles_c = (cols + 127) / 128;
+  const uint32_t r_base = (blockIdx.x / tiles_c) * 128, c_base = (blockIdx.x % tiles_c) * 128;
+  const int t = threadIdx.x, rg = t >> 3, cc = t & 7;
+  u32x4 v[4];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) v[r] = *(const uint32_t*)(w + ((size_t)(16 * rg + r) * cols + 4 * cg));
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t r = r_base + 4 * rg + i, c = c_base + 16 * cc;
+    v[i] = (r < rows && c < cols) ? *(const u32x4*)(w + ((size_t)r * cols + c)) : u32x4{0u, 0u, 0u, 0u};
+  }
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    mo_gemm::u32x4 out;
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int c = 0; c < 4; ++c) {
       uint32_t word = 0;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) word |= ((v[4 * k + b] >> (8 * c)) & 0xFFu) << (8 * b);
-      out[k] = word;
+      for (int b = 0; b < 4; ++b) word |= ((v[b][j] >> (8 * c)) & 0xFFu) << (8 * b);
+      const int col = 16 * cc + 4 * j + c;
+      tile[slot(col, rg >> 2) + (rg & 3)] = word;
     }
-    *(mo_gemm::u32x4*)(wt + ((size_t)(4 * cg + c) * rows + 16 * rg)) = out;
+  __syncthreads();
+  const int col = t >> 1, half = t & 1;
+  const uint32_t oc = c_base + col;
+  if (oc >= cols) return;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t r = r_base + 64 * half + 16 * p;
+    if (r < rows) *(u32x4*)(wt + ((size_t)oc * rows + r)) = *(const u32x4*)(tile + slot(col, 4 * half + p));
   }
 }

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 17
+MO_ABI_VERSION = 18
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -248,10 +248,11 @@ SIGNATURES: dict[str, tuple] = {
     "mo_wire_encode": (ctypes.c_int, [_u64, _u64, _u64, _u64, _u64, _u64]),
     "mo_wire_decode": (ctypes.c_int, [_u64, _u64, _u64, _u64, _u64]),
     "mo_int8_linear_forward": (ctypes.c_int, [_u64, _u64, _u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32,
-                                              ctypes.c_uint32, _u64]),
+                                              ctypes.c_uint32, _u64, _u64, _u64]),
+    "mo_int8_forward_workspace_bytes": (_u64, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]),
     "mo_int8_linear_backward": (ctypes.c_int, [_u64, _u64, _u64, _u64, ctypes.c_uint32, ctypes.c_uint32,
                                                ctypes.c_uint32, _u64, _u64, _u64]),
-    "mo_int8_backward_workspace_bytes": (_u64, [ctypes.c_uint32, ctypes.c_uint32]),
+    "mo_int8_backward_workspace_bytes": (_u64, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]),
     "mo_int8_set_kernel": (ctypes.c_int, [ctypes.c_uint32]),
 }
 

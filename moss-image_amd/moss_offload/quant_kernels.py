@@ -1,11 +1,12 @@
 """Weight-only int8 linear on MFMA: drop-in for the Triton path of MOSS-Image's
 ``training/quant_kernels.py`` (:100-228, ``triton_int8_linear_forward/backward``).
 
-The GEMMs are hand-written gfx950 kernels in ``csrc/mo_gemm.hip`` (bf16 MFMA, int8 tiles
-decoded to bf16 on their way into LDS), reached through ``mo_int8_linear_forward`` and
-``mo_int8_linear_backward``. From ``LIBRARY_ROWS`` rows or ``LIBRARY_WEIGHT`` weight elements
-up, a call instead decodes the weight in one HIP pass (``mo_int8_decode``) and runs the same library GEMM as the eager path, bit for
-bit equal to it and faster by the decode. Backend selection mirrors the reference's ``auto | eager | triton``
+The GEMMs are hand-written gfx950 kernels in ``csrc/mo_gemm.hip`` (bf16 MFMA; the int8
+weight decoded to bf16 in registers on its way into the MFMA), reached through
+``mo_int8_linear_forward`` and ``mo_int8_linear_backward``. From ``LIBRARY_ROWS`` rows or
+``LIBRARY_WEIGHT`` weight elements up, a call whose reduction is not long against its output
+width instead decodes the weight in one HIP pass (``mo_int8_decode``) and runs the same library
+GEMM as the eager path, bit for bit equal to it and faster by the decode. Backend selection mirrors the reference's ``auto | eager | triton``
 with ``hip`` in place of ``triton``: ``auto`` takes the HIP kernels whenever the call is
 supported (bf16 activations and weight dtype on a HIP device, int8 weights, fp32 scales,
 feature sizes multiples of 16, contiguous operands) and the eager path otherwise; an explicit
@@ -80,18 +81,23 @@ def decode(weight: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> tor
 
 
 # A call with at least LIBRARY_ROWS rows, or a weight of at least LIBRARY_WEIGHT elements,
-# decodes the weight once (mo_int8_decode) and runs the library GEMM on it. Any other call
-# runs the fused kernels, which decode the int8 tiles in LDS. Measured on MI355X, forward plus
-# input gradient, library time / fused time:
-#   qkvo 3072x3072:     1.14 / 1.06 / 1.15 / 0.94 / 0.80 / 0.83 at 256 / 512 / 1024 / 2048 / 4096 / 8192 rows
-#   up_gate 24576x3072: 0.77 / 0.99 / 0.99 / 1.01 / 0.78 / 0.76
-#   down 3072x12288:    0.77 / 0.86 / 0.90 / 0.83 / 0.79 / 0.83
-# The fused kernels decode each weight tile again for every row tile, and their MFMA loop runs
-# below the library's on these shapes. They keep small weights at few rows, where the one
-# decode pass is a large share of the call. The one-pass decode takes 7.9 / 35 / 20 us for
-# qkvo / up_gate / down, against 34 / 225 / 100 us for the eager cast-then-scale.
+# decodes the weight once (mo_int8_decode) and runs the library GEMM on it, unless its
+# reduction is at least LONG_REDUCTION times its output width and the fused kernels' launch
+# plan splits that reduction (rows that do not fill a round of large tiles): there the fused
+# kernels run. Any other call runs the fused kernels. Measured on MI355X, library time / fused
+# time (forward, input gradient):
+#   rows:                 256        512        1024       2048       4096       8192       17792
+#   qkvo 3072x3072       1.19 0.84  0.97 1.07  0.98 1.10  0.90 0.93  0.89 0.75  0.91 0.89  0.86 0.90
+#   up_gate 24576x3072   1.46 2.04  1.20 2.01  1.08 1.56  0.98 1.28  0.88 0.70  0.85 0.86  0.83 1.04
+#   down 3072x12288      1.54 0.97  1.50 0.90  1.20 0.87  1.09 0.91  0.74 0.88  0.90 0.89  1.04 0.91
+# The rule takes the fused kernels for up_gate's input gradient (24576-long reduction) and
+# down's forward (12288) at 256-2048 and 17792 rows, where the library's GEMM runs its weakest
+# and the split reduction fills the GPU; the library otherwise. On square and wide shapes the
+# library's MFMA loop runs 10-15 % faster than the fused kernels' (which also decode each
+# weight tile again for every row tile).
 LIBRARY_ROWS = 2048
 LIBRARY_WEIGHT = 16 << 20
+LONG_REDUCTION = 4
 PATHS = ("auto", "fused", "library")
 
 
@@ -106,10 +112,17 @@ def decode_hip(weight: torch.Tensor, scale: torch.Tensor, *, out: torch.Tensor |
     return out
 
 
-def _library(rows: int, weight: torch.Tensor, path: str) -> bool:
+def _library(rows: int, weight: torch.Tensor, path: str, reduction: int, width: int, split) -> bool:
+    """Whether a call takes the library path; ``split()`` tells whether the fused plan splits a
+    reduction (asked only when the rule needs it)."""
+
     if path not in PATHS:
         raise ValueError(f"path must be one of {PATHS}")
-    return path == "library" or (path == "auto" and (rows >= LIBRARY_ROWS or weight.numel() >= LIBRARY_WEIGHT))
+    if path != "auto":
+        return path == "library"
+    if rows < LIBRARY_ROWS and weight.numel() < LIBRARY_WEIGHT:
+        return False
+    return not (reduction >= LONG_REDUCTION * width and split())
 
 
 def _stream(tensor: torch.Tensor) -> int:
@@ -139,7 +152,8 @@ def int8_linear_forward(tokens: torch.Tensor, weight: torch.Tensor, scale: torch
     out_features = weight.shape[0]
     if bias is not None:
         bias = bias.to(torch.bfloat16).contiguous()
-    if _library(rows, weight, path):
+    nbytes = lib.mo_int8_forward_workspace_bytes(rows, in_features, out_features)
+    if _library(rows, weight, path, in_features, out_features, lambda: nbytes > 0):
         decoded = decode_hip(weight, scale)
         if out is None:
             # the eager path's own call (F.linear): with an output buffer, PyTorch-ROCm picks
@@ -151,11 +165,15 @@ def int8_linear_forward(tokens: torch.Tensor, weight: torch.Tensor, scale: torch
                 torch.addmm(bias, matrix, decoded.t(), out=out)
         return result.reshape(*tokens.shape[:-1], out_features)
     out = _output(out, (rows, out_features), tokens.device, "output")
+    # fp32 partial sums of split reductions (freed to the caching allocator after the call;
+    # stream order keeps them alive for the kernels)
+    workspace = torch.empty(nbytes, dtype=torch.uint8, device=tokens.device) if nbytes else None
     _native.check(
         "mo_int8_linear_forward",
         lib.mo_int8_linear_forward(matrix.data_ptr(), weight.data_ptr(), scale.data_ptr(),
                                    0 if bias is None else bias.data_ptr(), out.data_ptr(), rows, in_features,
-                                   out_features, _stream(tokens)),
+                                   out_features, 0 if workspace is None else workspace.data_ptr(), nbytes,
+                                   _stream(tokens)),
     )
     return out.reshape(*tokens.shape[:-1], out_features)
 
@@ -170,17 +188,18 @@ def int8_linear_backward(gradient: torch.Tensor, weight: torch.Tensor, scale: to
     matrix = gradient.reshape(-1, gradient.shape[-1]).to(torch.bfloat16).contiguous()
     rows, out_features = matrix.shape
     in_features = weight.shape[1]
-    if _library(rows, weight, path):
+    nbytes = lib.mo_int8_backward_workspace_bytes(rows, in_features, out_features)
+    transposed = (in_features * out_features + 255) // 256 * 256
+    if _library(rows, weight, path, out_features, in_features, lambda: nbytes > transposed):
         if out is None:  # the eager path's call (see int8_linear_forward)
             return matrix.matmul(decode_hip(weight, scale)).reshape(input_shape)
         out = _output(out, (rows, in_features), gradient.device, "input-gradient")
         torch.mm(matrix, decode_hip(weight, scale), out=out)
         return out.reshape(input_shape)
     out = _output(out, (rows, in_features), gradient.device, "input-gradient")
-    # the transposed int8 weight for the large tiles (freed to the caching allocator after the
-    # call; stream order keeps it alive for the kernels)
-    nbytes = lib.mo_int8_backward_workspace_bytes(in_features, out_features)
-    workspace = torch.empty(nbytes, dtype=torch.int8, device=gradient.device)
+    # the transposed int8 weight for the large tiles and the partial sums of split reductions
+    # (freed to the caching allocator after the call; stream order keeps it alive for the kernels)
+    workspace = torch.empty(nbytes, dtype=torch.uint8, device=gradient.device)
     _native.check(
         "mo_int8_linear_backward",
         lib.mo_int8_linear_backward(matrix.data_ptr(), weight.data_ptr(), scale.data_ptr(), out.data_ptr(), rows,

@@ -123,8 +123,9 @@ def test_backward_launch_plans_match_fp64_reference(rows, in_f, out_f) -> None:
 
 
 def test_tile_choice_does_not_change_results() -> None:
-    # 17792 rows: large tiles for rows < 16384, small tiles after; 4096 and 1408 rows alone run
-    # on small tiles only. Each output element has one reduction order in every plan.
+    # 17792 rows: large tiles for rows < 16384, then one launch with the reduction split three
+    # ways for the last 1408; 4096 rows alone run on small tiles, which add the large tile's
+    # products in its order, and 1408 rows alone run the same split launch as that tail.
     rows, in_f, out_f = 17792, 3072, 3072
     x, w, scale, b = _operands(rows, in_f, out_f, seed=77, bias=True)
     fused = {"path": "fused"}
@@ -269,6 +270,21 @@ def test_library_path_is_the_eager_path_bit_for_bit(rows, in_f, out_f) -> None:
         quant_kernels.int8_linear_forward(x, w, scale, b, path="triton")
 
 
+def _large_tile_rows(rows: int, cols: int) -> int:
+    """Rows the launch plan (csrc/mo_gemm.cpp plan) gives the large tile: all of them when the
+    grid fills its last round at least half, the full rounds' rows when it does not, none when
+    the grid is smaller than one round."""
+
+    cus = torch.cuda.get_device_properties(DEV).multi_processor_count
+    tm, tc = -(-rows // 256), -(-cols // 256)
+    rounds, rem = divmod(tm * tc, cus)
+    if rounds == 0:
+        return 0
+    if rem == 0 or 2 * rem >= cus:
+        return rows
+    return min(rows, (rounds * cus // tc) * 256)
+
+
 # Besides the config-5 shapes: 8000 x 1024 x 5008 (forward) and 8000 x 5008 x 1024 (input
 # gradient) run the register kernel alone on 640 large tiles with ragged rows and columns, over
 # a reduction of 16 steps that its six-step loop pads to 18.
@@ -276,7 +292,9 @@ def test_library_path_is_the_eager_path_bit_for_bit(rows, in_f, out_f) -> None:
                                              (4000, 4096, 4000), (8000, 1024, 5008), (8000, 5008, 1024)])
 def test_register_and_lds_kernels_agree_bitwise(rows, in_f, out_f) -> None:
     """The large tile's two kernels (weights decoded in registers, or into LDS) add the same
-    products in the same order: forward and input gradient are equal bit for bit."""
+    products in the same order: forward and input gradient are equal bit for bit on the rows the
+    large tile computes. The rest (a split reduction with the register kernel, the small tile
+    with the LDS kernel) round differently and are held to the fp64 bound."""
 
     x, w, scale, b = _operands(rows, in_f, out_f, seed=rows + in_f + out_f, bias=True)
     g = torch.Generator().manual_seed(5)
@@ -290,5 +308,94 @@ def test_register_and_lds_kernels_agree_bitwise(rows, in_f, out_f) -> None:
             results[kernel] = (y, dx)
     finally:
         quant_kernels.set_kernel("registers")
-    for a, e in zip(results["registers"], results["lds"]):
-        assert torch.equal(a.view(torch.int16), e.view(torch.int16))
+    decoded = quant_kernels.decode(w, scale, torch.bfloat16).double()
+    for k, (a, e) in enumerate(zip(results["registers"], results["lds"])):
+        main = _large_tile_rows(rows, out_f if k == 0 else in_f)
+        assert torch.equal(a[:main].view(torch.int16), e[:main].view(torch.int16))
+        if main == rows:
+            continue
+        if k == 0:
+            xs = x[main:].double()
+            exact, magnitude, terms = xs @ decoded.t() + b.double(), xs.abs() @ decoded.abs().t(), in_f
+        else:
+            ds = dy[main:].double()
+            exact, magnitude, terms = ds @ decoded, ds.abs() @ decoded.abs(), out_f
+        _within_accumulation_bound(a[main:], exact, magnitude, terms)
+        _within_accumulation_bound(e[main:], exact, magnitude, terms)
+
+
+# One-hot operands through split reductions: 3136 x 1040 outputs from a 3136-long reduction
+# (49 steps of 64, split 18 + 18 + 13 over 65 large tiles; the transposed weight's last row and
+# column tiles are partial). Each output element is one product plus zeros, so every split plan
+# must reproduce the decoded weight bit for bit.
+def test_split_reductions_reproduce_the_decoded_weight_bitwise() -> None:
+    _, w, scale, _ = _operands(1, 3136, 1040, seed=31)  # forward: in 3136, out 1040
+    eye = torch.eye(3136, dtype=torch.bfloat16, device=DEV)
+    decoded = quant_kernels.decode(w, scale, torch.bfloat16)
+    y = quant_kernels.int8_linear_forward(eye, w, scale, path="fused")
+    assert torch.equal(y.view(torch.int16), decoded.t().contiguous().view(torch.int16))
+    _, w, scale, _ = _operands(1, 1040, 3136, seed=32)  # input gradient: reduction over out 3136
+    decoded = quant_kernels.decode(w, scale, torch.bfloat16)
+    dx = quant_kernels.int8_linear_backward(eye, w, scale, torch.Size((3136, 1040)), path="fused")
+    assert torch.equal(dx.view(torch.int16), decoded.view(torch.int16))
+
+
+@pytest.mark.parametrize("direction", ["forward", "backward"])
+def test_split_reductions_are_deterministic_and_within_bound(direction) -> None:
+    # config 5's down_proj forward (12288-long reduction) and up_gate input gradient (24576):
+    # the last 1408 rows run split three ways
+    rows = 17792
+    in_f, out_f = (12288, 3072) if direction == "forward" else (3072, 24576)
+    x, w, scale, b = _operands(rows, in_f, out_f, seed=41, bias=direction == "forward")
+    decoded = quant_kernels.decode(w, scale, torch.bfloat16).double()
+    if direction == "forward":
+        first = quant_kernels.int8_linear_forward(x, w, scale, b, path="fused")
+        again = quant_kernels.int8_linear_forward(x, w, scale, b, path="fused")
+        tail = x[16384:].double()
+        exact, magnitude, terms = tail @ decoded.t() + b.double(), tail.abs() @ decoded.abs().t(), in_f
+    else:
+        g = torch.Generator().manual_seed(42)
+        dy = torch.randn(rows, out_f, generator=g).to(torch.bfloat16).to(DEV)
+        first = quant_kernels.int8_linear_backward(dy, w, scale, torch.Size((rows, in_f)), path="fused")
+        again = quant_kernels.int8_linear_backward(dy, w, scale, torch.Size((rows, in_f)), path="fused")
+        tail = dy[16384:].double()
+        exact, magnitude, terms = tail @ decoded, tail.abs() @ decoded.abs(), out_f
+    assert torch.equal(first.view(torch.int16), again.view(torch.int16))
+    _within_accumulation_bound(first[16384:], exact, magnitude, terms)
+    # a reduction at least four times the output width with a split launch: auto takes the
+    # fused kernels
+    if direction == "forward":
+        auto = quant_kernels.int8_linear_forward(x, w, scale, b)
+    else:
+        auto = quant_kernels.int8_linear_backward(dy, w, scale, torch.Size((rows, in_f)))
+    assert torch.equal(auto.view(torch.int16), first.view(torch.int16))
+
+
+def test_long_reduction_without_a_split_takes_the_library() -> None:
+    # 8192 rows of down_proj's forward fill one and a half rounds of large tiles: no split
+    # launch, so auto runs the library GEMM (the eager path's result bit for bit)
+    x, w, scale, _ = _operands(8192, 12288, 3072, seed=43)
+    decoded = quant_kernels.decode(w, scale, torch.bfloat16)
+    assert torch.equal(quant_kernels.int8_linear_forward(x, w, scale).view(torch.int16),
+                       F.linear(x, decoded).view(torch.int16))
+
+
+def test_workspace_smaller_than_the_plan_needs_is_rejected() -> None:
+    from moss_offload import _native
+
+    lib = _native.load()
+    rows, in_f, out_f = 1408, 3072, 3072  # a split launch alone
+    x, w, scale, _ = _operands(rows, in_f, out_f, seed=9)
+    y = torch.empty(rows, out_f, dtype=torch.bfloat16, device=DEV)
+    need = lib.mo_int8_forward_workspace_bytes(rows, in_f, out_f)
+    assert need >= 3 * rows * out_f * 4
+    small = torch.empty(need - 256, dtype=torch.uint8, device=DEV)
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+    rc = lib.mo_int8_linear_forward(x.data_ptr(), w.data_ptr(), scale.data_ptr(), 0, y.data_ptr(), rows, in_f,
+                                    out_f, small.data_ptr(), need - 256, stream)
+    assert rc == _native.MO_E_INVALID and b"workspace" in lib.mo_last_error()
+    dneed = lib.mo_int8_backward_workspace_bytes(rows, in_f, out_f)
+    assert dneed >= in_f * out_f + 3 * rows * in_f * 4
+    rc = lib.mo_int8_linear_backward(x.data_ptr(), w.data_ptr(), scale.data_ptr(), y.data_ptr(), rows, in_f,
+                                     out_f, small.data_ptr(), in_f * out_f, stream)
+    assert rc == _native.MO_E_INVALID and b"workspace" in lib.mo_last_error()
