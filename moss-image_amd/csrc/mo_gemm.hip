@@ -812,8 +812,9 @@ extern "C" __global__ __launch_bounds__(256) void mo_int8_decode_kernel(const in
 // columns 16 (t % 8) (eight lanes per 128-byte row piece), transposes the 4 x 4 byte blocks in
 // registers into 4-byte words of one column and four rows, and exchanges them through LDS
 // ([column][row group], 16-byte chunks XOR-swizzled by column so the word writes of a wave
-// spread over the banks); then lane t writes 64 bytes of Wt row t / 2 (two lanes per 128-byte
-// row piece). rows % 16 == 0, cols % 16 == 0.
+// spread over the banks); then, in four passes of 32 Wt rows, lane t writes 16 bytes of Wt row
+// t / 8 of the pass at rows 16 (t % 8) (eight lanes per 128-byte row piece).
+// rows % 16 == 0, cols % 16 == 0.
 extern "C" __global__ __launch_bounds__(256) void mo_int8_transpose_kernel(const int8_t* w, int8_t* wt,
                                                                           uint32_t rows, uint32_t cols) {
   using mo_gemm::u32x4;
@@ -839,12 +840,10 @@ extern "C" __global__ __launch_bounds__(256) void mo_int8_transpose_kernel(const
       tile[slot(col, rg >> 2) + (rg & 3)] = word;
     }
   __syncthreads();
-  const int col = t >> 1, half = t & 1;
-  const uint32_t oc = c_base + col;
-  if (oc >= cols) return;
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const uint32_t r = r_base + 64 * half + 16 * p;
-    if (r < rows) *(u32x4*)(wt + ((size_t)oc * rows + r)) = *(const u32x4*)(tile + slot(col, 4 * half + p));
+    const int col = 32 * p + (t >> 3), chunk = t & 7;
+    const uint32_t oc = c_base + col, r = r_base + 16 * chunk;
+    if (oc < cols && r < rows) *(u32x4*)(wt + ((size_t)oc * rows + r)) = *(const u32x4*)(tile + slot(col, chunk));
   }
 }
