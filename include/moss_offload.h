@@ -469,6 +469,15 @@ uint64_t mo_int8_backward_workspace_bytes(uint32_t rows, uint32_t in_features, u
 enum { MO_INT8_KERNEL_REGISTERS = 0, MO_INT8_KERNEL_LDS = 1 };
 int mo_int8_set_kernel(uint32_t kernel);
 
+/* The launch plan of a call with a workspace, host only: `cols` output columns (out for the
+ * forward, in for the input gradient) from a `reduction` (in, or out), on a device of `cus`
+ * CUs with `kernel` taking the large tiles. Writes *n_parts (1 or 2) and, per part, five
+ * values to parts[5 i ..]: tile (0 large, 1 small, 2 large with a split reduction), first row,
+ * rows, splits, reduction steps of 64 per split. No reference counterpart: it describes this
+ * library's launches, for tests and tools. */
+int mo_int8_launch_plan(uint32_t rows, uint32_t cols, uint32_t reduction, uint32_t cus, uint32_t kernel,
+                        uint32_t* n_parts, uint32_t* parts);
+
 /* ---- host gradient accumulation (training/fused_adafactor.py:327-369) -------------------- */
 
 /* Gradient element types: the reference's value-kind codes (quant_kernels.py:280-287). */

@@ -356,6 +356,26 @@ int mo_int8_linear_backward(uint64_t dy, uint64_t w, uint64_t scale, uint64_t dx
   return 0;
 }
 
+int mo_int8_launch_plan(uint32_t rows, uint32_t cols, uint32_t reduction, uint32_t cus, uint32_t kernel,
+                        uint32_t* n_parts, uint32_t* parts) {
+  if (!n_parts || !parts) return mo::set_error(MO_E_INVALID, "null output pointer");
+  if (rows == 0 || cols == 0 || reduction == 0 || cus == 0) return mo::set_error(MO_E_INVALID, "empty shape");
+  if (kernel != MO_INT8_KERNEL_REGISTERS && kernel != MO_INT8_KERNEL_LDS)
+    return mo::set_error(MO_E_INVALID, "unknown int8 kernel selection");
+  Part p[2];
+  const uint32_t steps = kernel == MO_INT8_KERNEL_REGISTERS ? split_steps_of(reduction) : 0;
+  const int n = plan(rows, cols, steps, (int)cus, p);
+  for (int i = 0; i < n; ++i) {
+    parts[5 * i + 0] = p[i].tile == Tile::Large ? 0u : p[i].tile == Tile::Small ? 1u : 2u;
+    parts[5 * i + 1] = p[i].row0;
+    parts[5 * i + 2] = p[i].rows;
+    parts[5 * i + 3] = p[i].splits;
+    parts[5 * i + 4] = p[i].split_steps;
+  }
+  *n_parts = (uint32_t)n;
+  return 0;
+}
+
 int mo_int8_set_kernel(uint32_t kernel) {
   if (kernel != MO_INT8_KERNEL_REGISTERS && kernel != MO_INT8_KERNEL_LDS)
     return mo::set_error(MO_E_INVALID, "unknown int8 kernel selection");

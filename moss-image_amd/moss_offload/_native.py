@@ -254,6 +254,8 @@ SIGNATURES: dict[str, tuple] = {
                                                ctypes.c_uint32, _u64, _u64, _u64]),
     "mo_int8_backward_workspace_bytes": (_u64, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]),
     "mo_int8_set_kernel": (ctypes.c_int, [ctypes.c_uint32]),
+    "mo_int8_launch_plan": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                           ctypes.c_uint32, _P(ctypes.c_uint32), _P(ctypes.c_uint32)]),
 }
 
 _lock = threading.Lock()

@@ -208,6 +208,24 @@ def int8_linear_backward(gradient: torch.Tensor, weight: torch.Tensor, scale: to
     return out.reshape(input_shape)
 
 
+def launch_plan(rows: int, cols: int, reduction: int, cus: int, kernel: str = "registers") -> list[dict]:
+    """The fused kernels' launches for a call with a workspace (``mo_int8_launch_plan``): ``cols``
+    output columns (out_features for the forward, in_features for the input gradient) from a
+    ``reduction`` (in_features, or out_features) on a device of ``cus`` CUs. Each part is
+    ``{"tile": "large" | "small" | "split", "row0", "rows", "splits", "split_steps"}``."""
+
+    import ctypes
+
+    lib = _native.load()
+    code = {"registers": _native.MO_INT8_KERNEL_REGISTERS, "lds": _native.MO_INT8_KERNEL_LDS}[kernel]
+    n = ctypes.c_uint32(0)
+    raw = (ctypes.c_uint32 * 10)()
+    _native.check("mo_int8_launch_plan", lib.mo_int8_launch_plan(rows, cols, reduction, cus, code, ctypes.byref(n), raw))
+    names = ("large", "small", "split")
+    return [{"tile": names[raw[5 * i]], "row0": raw[5 * i + 1], "rows": raw[5 * i + 2], "splits": raw[5 * i + 3],
+             "split_steps": raw[5 * i + 4]} for i in range(n.value)]
+
+
 def set_kernel(kernel: str) -> None:
     """Which kernel takes the large tiles of the fused path, process-wide: ``registers`` (default:
     weights decoded in registers, activations through LDS) or ``lds`` (the weight tile decoded

@@ -270,19 +270,12 @@ def test_library_path_is_the_eager_path_bit_for_bit(rows, in_f, out_f) -> None:
         quant_kernels.int8_linear_forward(x, w, scale, b, path="triton")
 
 
-def _large_tile_rows(rows: int, cols: int) -> int:
-    """Rows the launch plan (csrc/mo_gemm.cpp plan) gives the large tile: all of them when the
-    grid fills its last round at least half, the full rounds' rows when it does not, none when
-    the grid is smaller than one round."""
+def _large_tile_rows(rows: int, cols: int, reduction: int) -> int:
+    """Rows the register kernel's launch plan gives the large tile on this device."""
 
     cus = torch.cuda.get_device_properties(DEV).multi_processor_count
-    tm, tc = -(-rows // 256), -(-cols // 256)
-    rounds, rem = divmod(tm * tc, cus)
-    if rounds == 0:
-        return 0
-    if rem == 0 or 2 * rem >= cus:
-        return rows
-    return min(rows, (rounds * cus // tc) * 256)
+    parts = quant_kernels.launch_plan(rows, cols, reduction, cus)
+    return parts[0]["rows"] if parts[0]["tile"] == "large" else 0
 
 
 # Besides the config-5 shapes: 8000 x 1024 x 5008 (forward) and 8000 x 5008 x 1024 (input
@@ -310,7 +303,7 @@ def test_register_and_lds_kernels_agree_bitwise(rows, in_f, out_f) -> None:
         quant_kernels.set_kernel("registers")
     decoded = quant_kernels.decode(w, scale, torch.bfloat16).double()
     for k, (a, e) in enumerate(zip(results["registers"], results["lds"])):
-        main = _large_tile_rows(rows, out_f if k == 0 else in_f)
+        main = _large_tile_rows(rows, *((out_f, in_f) if k == 0 else (in_f, out_f)))
         assert torch.equal(a[:main].view(torch.int16), e[:main].view(torch.int16))
         if main == rows:
             continue
