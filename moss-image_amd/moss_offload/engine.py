@@ -50,10 +50,11 @@ class EngineConfig:
     # flight when asked for; at sixteen (prefetch_depth 16) none were, the unpack launches of a
     # 1024^2 checkpointed step grew from 48 to 132 MB (4.85 -> 5.78 TB/s) and the trainer's
     # thread blocked for an H2D 12 instead of 93 times per leg. Config 4 not checkpointed (24
-    # blocks at 2048^2) went from 2.89 to 2.60 s/it; config 3 not checkpointed went from 0.654
-    # to 0.663 s/it (alternating runs on one box; eight slots remain its better setting). The
-    # cost is 1 GiB more device memory at 128 MiB slots (a checkpoint-only trainer can take
-    # 32 MiB slots instead).
+    # blocks at 2048^2) went from 2.89 to 2.60 s/it. Wire-coded segments take at most the first
+    # max(8, segments of their block + 2) slots (the engine's own rule): config 3 not
+    # checkpointed runs 0.650 s/it with it against 0.665 on all sixteen and 0.654 with eight
+    # slots in all. The cost is 1 GiB more device memory at 128 MiB slots (a checkpoint-only
+    # trainer can take 32 MiB slots instead).
     restore_slots: int = 16
     host_limit_bytes: int = 0
     host_chunk_bytes: int = 1 << 30
