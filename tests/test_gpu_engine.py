@@ -528,6 +528,41 @@ def test_prefetch_groups_takes_a_farther_group_only_when_all_of_it_fits() -> Non
         engine.close()
 
 
+@pytest.mark.parametrize("wire", ["on", "off"])
+def test_coded_segments_keep_to_their_slot_limit(wire) -> None:
+    """Wire-coded segments take at most the first max(8, segments of their group + 2) restore
+    slots, raw ones the whole ring: with twelve slots, a prefetch of twelve one-segment groups
+    fetches eight when they are coded and twelve when they are raw; every restore is bitwise."""
+
+    device = torch.device("cuda", 0)
+    cfg = EngineConfig(stage_slot_bytes=2 * MiB, stage_slots=3, restore_slots=12, host_chunk_bytes=8 * MiB,
+                       commit_batch_bytes=0, wire_coding=wire, staged_restore=False, prefetch=False)
+    engine = OffloadEngine(device, cfg)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(11)
+    try:
+        handles, gids = [], []
+        for _ in range(12):
+            t = torch.randn(MiB - 4096, generator=g).to(torch.bfloat16).to(device)  # one segment each
+            gid, idx = engine.pack(t, stream)
+            engine.commit(stream)
+            handles.append((t, gid, idx))
+            gids.append(gid)
+        engine.synchronize()
+        assert engine.stats()["wire_segments"] == (12 if wire == "on" else 0)
+        base = engine.stats()["prefetch_issued"]
+        engine._prefetch_groups(list(reversed(gids)), stream)
+        assert engine.stats()["prefetch_issued"] - base == (8 if wire == "on" else 12)
+        _restore_and_check(engine, handles, device, list(reversed(range(12))))
+        assert engine.stats()["copy_failures"] == 0
+        for _, gid, idx in handles:
+            engine.drop(gid, idx)
+        engine.synchronize()
+        assert engine.stats()["host_bytes_in_use"] == 0
+    finally:
+        engine.close()
+
+
 def test_trim_frees_wire_buffers_only_with_no_group_live() -> None:
     """mo_trim keeps the wire buffers while a group is live (its restore still decodes
     bitwise) and frees them once none is; the next coded segment allocates them again."""
