@@ -49,7 +49,7 @@ def rotate_rope(tokens: torch.Tensor, rope: torch.Tensor) -> torch.Tensor:
     return tokens * cos + torch.cat((-second, first), -1) * sin
 
 
-def _attention_core(query, key, value, cu_seqlens):
+def _attention_core(query, key, value, cu_seqlens, seq_lengths=None):
     # performance.py:139-143 (normalised q/k follow the value dtype) and :163-225 (packed
     # sequences). On a HIP device the packed sequences are attended one by one, which is what
     # the reference's varlen kernel computes (performance.py:195-209, flash_attn_varlen_func):
@@ -63,8 +63,12 @@ def _attention_core(query, key, value, cu_seqlens):
     if cu_seqlens is None:
         return F.scaled_dot_product_attention(query, key, value)
     if value.device.type == "cuda":
-        lengths = getattr(cu_seqlens, "host_lengths", None)
-        if lengths is None:  # a cu_seqlens built elsewhere (or restored by the offload hooks)
+        # the split sizes on the host: passed beside cu_seqlens (a checkpointed block's
+        # recomputation gets them that way, since a cu_seqlens restored by the offload hooks is a
+        # new tensor), kept on a cu_seqlens built by _cumulative_lengths, or read back from the
+        # device (a synchronisation) for one built elsewhere
+        lengths = seq_lengths if seq_lengths is not None else getattr(cu_seqlens, "host_lengths", None)
+        if lengths is None:
             lengths = (cu_seqlens[1:] - cu_seqlens[:-1]).tolist()
         parts = zip(query.split(lengths, 2), key.split(lengths, 2), value.split(lengths, 2))
         return torch.cat([F.scaled_dot_product_attention(q, k, v) for q, k, v in parts], 2)
@@ -76,14 +80,15 @@ def _attention_core(query, key, value, cu_seqlens):
     return F.scaled_dot_product_attention(query, key, value, attn_mask=mask)
 
 
-def attention(query, key, value, rope, heads, cu_seqlens=None):
-    """Joint attention with RoPE on q and k over ``[batch, seq, dim]`` (reference model.py:59-91)."""
+def attention(query, key, value, rope, heads, cu_seqlens=None, seq_lengths=None):
+    """Joint attention with RoPE on q and k over ``[batch, seq, dim]`` (reference model.py:59-91).
+    ``seq_lengths``: the packed sequences' lengths as host integers, when the caller has them."""
 
     shape = (*query.shape[:2], heads, query.shape[-1] // heads)
     query = rotate_rope(query.reshape(shape), rope).transpose(1, 2)
     key = rotate_rope(key.reshape(shape), rope).transpose(1, 2)
     value = value.reshape(shape).transpose(1, 2)
-    mixed = _attention_core(query, key, value, cu_seqlens)
+    mixed = _attention_core(query, key, value, cu_seqlens, seq_lengths)
     return mixed.transpose(1, 2).flatten(2)
 
 
@@ -214,7 +219,7 @@ class Block(nn.Module):
             self.proj["ffn_up_gate"] = nn.Linear(dim, 2 * ffn_dim, bias=False)
         self.proj["ffn_down"] = nn.Linear(ffn_dim, dim, bias=False)
 
-    def forward(self, tokens, rope, modulation, cu_seqlens=None):
+    def forward(self, tokens, rope, modulation, cu_seqlens=None, seq_lengths=None):
         shift_attn, scale_attn, gate_attn, shift_ffn, scale_ffn, gate_ffn = modulation.unbind(1)
         index = _modulation_sample_indices(modulation, tokens, cu_seqlens)
         hidden = self.norm1(tokens)
@@ -224,7 +229,7 @@ class Block(nn.Module):
         hidden = hidden.to(weight_dtype)
         query = self.q_norm(self.proj["q"](hidden).unflatten(-1, (self.heads, -1))).flatten(2)
         key = self.k_norm(self.proj["k"](hidden).unflatten(-1, (self.heads, -1))).flatten(2)
-        attended = attention(query, key, self.proj["v"](hidden), rope, self.heads, cu_seqlens)
+        attended = attention(query, key, self.proj["v"](hidden), rope, self.heads, cu_seqlens, seq_lengths)
         tokens = tokens + self.proj["o"](attended) * _condition_for_tokens(gate_attn, index)
         hidden = self.norm2(tokens)
         hidden = hidden * (1 + _condition_for_tokens(scale_ffn, index))
@@ -420,7 +425,10 @@ class MOSSImageTransformer(nn.Module):
         for index, layer in enumerate(self.layers):
             if index in skipped:
                 continue
-            inputs = (tokens, rope, modulation) if cu_seqlens is None else (tokens, rope, modulation, cu_seqlens)
+            # packed: cu_seqlens (a saved tensor, as in the reference) and its lengths as host
+            # integers, which a checkpoint keeps as they are (no tensor to offload and restore)
+            inputs = (tokens, rope, modulation) if cu_seqlens is None else \
+                (tokens, rope, modulation, cu_seqlens, getattr(cu_seqlens, "host_lengths", None))
             if manager is not None and index >= boundary:
                 p = position[index]
                 tokens = manager.block(

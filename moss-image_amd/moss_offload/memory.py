@@ -193,11 +193,12 @@ class AsyncBlockStreamer:
         count = len(inputs)
 
         def body(*flat: torch.Tensor) -> torch.Tensor:
-            needs_grad = tuple(t for t in flat if t.requires_grad)
+            needs_grad = tuple(t for t in flat if isinstance(t, torch.Tensor) and t.requires_grad)
             return self._execute(index, flat[:count], dict(zip(names, flat[count:])), needs_grad, neighbours)
 
         # fresh views as the checkpoint's inputs: two runs of one block in one graph stay apart
-        flat = tuple(t.view_as(t) if t.requires_grad else t for t in inputs)
+        # (inputs that are not tensors, such as packed sequence lengths, pass as they are)
+        flat = tuple(t.view_as(t) if isinstance(t, torch.Tensor) and t.requires_grad else t for t in inputs)
         flat += tuple(p.view_as(p) for p in frozen.adapters.values())
         return checkpoint(body, *flat, use_reentrant=False,
                           context_fn=lambda: (nullcontext(), self._phase.recomputing()))

@@ -309,7 +309,7 @@ class TrainableBlockStreamer:
         neighbours = (forward_prefetch, backward_prefetch)
         if not checkpoint_block:
             return self._execute(index, inputs, neighbours)
-        fresh = tuple(t.view_as(t) if t.requires_grad else t for t in inputs)
+        fresh = tuple(t.view_as(t) if isinstance(t, torch.Tensor) and t.requires_grad else t for t in inputs)
         return checkpoint(lambda *flat: self._execute(index, flat, neighbours), *fresh, use_reentrant=False,
                           context_fn=lambda: (nullcontext(),
                                               self._phase.recomputing()))
