@@ -410,9 +410,13 @@ class _ActivationOffload:
         if self.engine.config.prefetch and exc[0] is None:
             # Backward starts with the last group, and with every group holding a save the
             # forward made repeatedly (e.g. one RoPE table checkpointed with every block): start
-            # bringing them back now. Segments still in the staging ring are skipped.
+            # bringing them back now, those first, then the groups backward needs after the
+            # last one (which would otherwise take every free slot before a shared group got
+            # one). Segments still in the staging ring are skipped.
             for gid in ([last] if last is not None else []) + sorted(self._shared - {last}, reverse=True):
-                self.engine.prefetch(gid, stream, ahead=gid == last)
+                self.engine.prefetch(gid, stream)
+            if last is not None:
+                self.engine.prefetch(last, stream, ahead=True)
         self._shared.clear()
         return False
 
