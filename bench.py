@@ -689,6 +689,7 @@ def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: 
 
     engine = OffloadEngine(device, EngineConfig(
         stage_slot_bytes=slot_mib << 20, stage_slots=stage_slots, restore_slots=restore_slots,
+        stage_slots_max=0, restore_slots_max=0,  # the microbench's rings as given
         timing=True, kernel_timing=True, staged_restore=False, prefetch=False, batch_packs=batch_packs,
         d2h_engine=d2h_engine, h2d_engine=h2d_engine, link=link, **(cache or {})))
     stream = torch.cuda.current_stream(device).cuda_stream
@@ -1030,6 +1031,8 @@ def run(args) -> dict:
         kernel_timing=True,
         stage_slots=args.stage_slots,
         restore_slots=args.restore_slots,
+        stage_slots_max=args.stage_slots_max,
+        restore_slots_max=args.restore_slots_max,
         prefetch_depth=args.prefetch_depth,
         stage_slot_bytes=args.slot_mib << 20,
         **({} if args.restore_ahead_mib is None else {"restore_ahead_bytes": args.restore_ahead_mib << 20}),
@@ -1471,6 +1474,10 @@ def main() -> int:
     parser.add_argument("--no-parity", action="store_true")
     parser.add_argument("--stage-slots", type=int, default=4)
     parser.add_argument("--restore-slots", type=int, default=16)
+    parser.add_argument("--stage-slots-max", type=int, default=8,
+                        help="staging ring growth cap (0: fixed ring)")
+    parser.add_argument("--restore-slots-max", type=int, default=32,
+                        help="restore ring growth cap (0: fixed ring)")
     parser.add_argument("--prefetch-depth", type=int, default=16,
                         help="groups the engine prefetches ahead of backward after each restored group")
     parser.add_argument("--slot-mib", type=int, default=128)

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 18
+#define MO_ABI_VERSION 19
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -126,6 +126,14 @@ typedef struct mo_config {
                                    launch gathers them all and their D2Hs follow. No
                                    reference counterpart (the reference copies each save
                                    at its hook)                                         */
+  uint32_t stage_slots_max;     /* [0 = stage_slots: fixed] the staging ring grows, at the
+                                   commit of a group of n segments, to ceil(n / 3) slots,
+                                   at most this many                                   */
+  uint32_t restore_slots_max;   /* [0 = restore_slots: fixed] the restore ring grows, at
+                                   the same commit, to n + 2 slots, at most this many.
+                                   A slot that cannot be allocated (or whose wire buffer
+                                   would pass wire_device_limit) ends the growth; the
+                                   engine runs on with the slots it has                  */
 } mo_config;
 
 /* Where one packed tensor lives: its group (one block's saves) and index in the group. */

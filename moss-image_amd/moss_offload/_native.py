@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 18
+MO_ABI_VERSION = 19
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -66,6 +66,8 @@ class MoConfig(ctypes.Structure):
         ("h2d_engine", ctypes.c_uint32),
         ("wire_device_limit", ctypes.c_uint64),
         ("commit_batch_bytes", ctypes.c_uint64),
+        ("stage_slots_max", ctypes.c_uint32),
+        ("restore_slots_max", ctypes.c_uint32),
     ]
 
 

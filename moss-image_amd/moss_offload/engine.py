@@ -31,6 +31,7 @@ from . import _native
 
 
 LINKS = ("sdma", "hipdma")
+_MAX_SLOTS = 64  # staging plus restore slots, the library's limit
 WIRE_CODINGS = {"off": 0, "on": _native.MO_FLAG_WIRE_CODING, "auto": _native.MO_FLAG_WIRE_AUTO}
 
 
@@ -56,6 +57,16 @@ class EngineConfig:
     # slots in all. The cost is 1 GiB more device memory at 128 MiB slots (a checkpoint-only
     # trainer can take 32 MiB slots instead).
     restore_slots: int = 16
+    # Ring growth for large blocks: at the commit of a group of n segments the engine grows the
+    # restore ring to n + 2 slots and the staging ring to ceil(n / 3), up to these caps (0:
+    # fixed rings). A 2048^2 block not checkpointed spans about 23 coded segments: with the
+    # fixed 4 + 16 slots its restore fetched its last segments one at a time, each behind an
+    # earlier one's scatter, and the D2H queue ran dry while attention held the next gather
+    # (config 4 not checkpointed 2.60 s/it; grown to 8 + 32, 2.33). A 1024^2 block (about 11
+    # segments) grows nothing. The grown slots cost device memory only where blocks are that
+    # large (128 MiB each, plus a wire buffer each while coding).
+    stage_slots_max: int = 8
+    restore_slots_max: int = 32
     host_limit_bytes: int = 0
     host_chunk_bytes: int = 1 << 30
     timing: bool = False
@@ -142,7 +153,8 @@ class EngineConfig:
             raise ValueError(f"link must be one of {LINKS}, got {self.link!r}")
         if self.wire_coding not in WIRE_CODINGS:
             raise ValueError(f"wire_coding must be one of {tuple(WIRE_CODINGS)}, got {self.wire_coding!r}")
-        for name in ("stage_slot_bytes", "stage_slots", "restore_slots", "host_limit_bytes", "host_chunk_bytes",
+        for name in ("stage_slot_bytes", "stage_slots", "restore_slots", "stage_slots_max", "restore_slots_max",
+                     "host_limit_bytes", "host_chunk_bytes",
                      "copy_kernel_blocks", "d2h_engine", "h2d_engine", "prefetch_depth", "keep_last_blocks",
                      "wire_device_limit", "restore_ahead_bytes", "commit_batch_bytes"):
             value = getattr(self, name)
@@ -173,6 +185,14 @@ class EngineConfig:
         cfg.h2d_engine = self.h2d_engine
         cfg.wire_device_limit = self.wire_device_limit
         cfg.commit_batch_bytes = self.commit_batch_bytes
+        # a cap below the ring's own size means no growth (the library rejects a cap below it),
+        # and the caps give way to the configured rings within the library's 64 slots
+        stage_max = max(self.stage_slots_max, self.stage_slots) if self.stage_slots_max else self.stage_slots
+        restore_max = max(self.restore_slots_max, self.restore_slots) if self.restore_slots_max else self.restore_slots
+        restore_max = max(self.restore_slots, min(restore_max, _MAX_SLOTS - stage_max))
+        stage_max = max(self.stage_slots, min(stage_max, _MAX_SLOTS - restore_max))
+        cfg.stage_slots_max = stage_max
+        cfg.restore_slots_max = restore_max
         return cfg
 
 

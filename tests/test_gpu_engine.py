@@ -23,9 +23,14 @@ MiB = 1 << 20
 
 
 def _engine(**kw) -> OffloadEngine:
-    # each commit sends its own segments unless a test asks for commit batching
+    # each commit sends its own segments unless a test asks for commit batching; the rings keep
+    # their sizes unless a test asks for growth
     kw.setdefault("commit_batch_bytes", 0)
-    cfg = EngineConfig(stage_slot_bytes=2 * MiB, stage_slots=3, restore_slots=2, host_chunk_bytes=8 * MiB, **kw)
+    kw.setdefault("stage_slots_max", 0)
+    kw.setdefault("restore_slots_max", 0)
+    kw.setdefault("stage_slots", 3)
+    kw.setdefault("restore_slots", 2)
+    cfg = EngineConfig(stage_slot_bytes=2 * MiB, host_chunk_bytes=8 * MiB, **kw)
     return OffloadEngine(torch.device("cuda", 0), cfg)
 
 
@@ -109,7 +114,7 @@ def test_hipdma_link_split_and_single_d2h_round_trip(d2h_engine) -> None:
     # 8 MiB slots so that D2H copies reach the 2 MiB split size; d2h_engine=1 keeps one stream.
     device = torch.device("cuda", 0)
     cfg = EngineConfig(stage_slot_bytes=8 * MiB, stage_slots=3, restore_slots=2, host_chunk_bytes=32 * MiB,
-                       link="hipdma", d2h_engine=d2h_engine, timing=True)
+                       link="hipdma", d2h_engine=d2h_engine, timing=True, stage_slots_max=0, restore_slots_max=0)
     engine = OffloadEngine(device, cfg)
     stream = torch.cuda.current_stream(device).cuda_stream
     rng = random.Random(7 + d2h_engine)
@@ -176,7 +181,7 @@ def test_open_group_restored_before_commit() -> None:
 def test_host_limit_raises_clear_error() -> None:
     device = torch.device("cuda", 0)
     cfg = EngineConfig(stage_slot_bytes=2 * MiB, stage_slots=2, restore_slots=2, host_chunk_bytes=2 * MiB,
-                       host_limit_bytes=4 * MiB)
+                       host_limit_bytes=4 * MiB, stage_slots_max=0, restore_slots_max=0)
     engine = OffloadEngine(device, cfg)
     stream = torch.cuda.current_stream(device).cuda_stream
     t = torch.randn(3 * MiB // 4, device=device)  # 3 MiB per save
@@ -536,7 +541,8 @@ def test_coded_segments_keep_to_their_slot_limit(wire) -> None:
 
     device = torch.device("cuda", 0)
     cfg = EngineConfig(stage_slot_bytes=2 * MiB, stage_slots=3, restore_slots=12, host_chunk_bytes=8 * MiB,
-                       commit_batch_bytes=0, wire_coding=wire, staged_restore=False, prefetch=False)
+                       commit_batch_bytes=0, wire_coding=wire, staged_restore=False, prefetch=False,
+                       stage_slots_max=0, restore_slots_max=0)
     engine = OffloadEngine(device, cfg)
     stream = torch.cuda.current_stream(device).cuda_stream
     g = torch.Generator(device="cpu").manual_seed(11)
@@ -559,6 +565,86 @@ def test_coded_segments_keep_to_their_slot_limit(wire) -> None:
             engine.drop(gid, idx)
         engine.synchronize()
         assert engine.stats()["host_bytes_in_use"] == 0
+    finally:
+        engine.close()
+
+
+@pytest.mark.parametrize("wire", ["off", "on"])
+def test_rings_grow_at_the_commit_of_a_large_group(wire) -> None:
+    """At the commit of a group of n segments the restore ring grows to n + 2 slots and the
+    staging ring to ceil(n / 3), within their caps; smaller groups grow nothing. Groups packed
+    and restored across the growth are bitwise, with and without wire coding (whose buffers the
+    grown slots get as well)."""
+
+    device = torch.device("cuda", 0)
+    slot = 2 * MiB
+    engine = _engine(stage_slots=2, restore_slots=2, stage_slots_max=4, restore_slots_max=10, wire_coding=wire,
+                     staged_restore=False)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(5)
+    handles = []
+
+    def group(count: int) -> int:
+        copies = engine.stats()["d2h_copies"]
+        for _ in range(count):
+            t = torch.randn(MiB - 4096, generator=g).to(torch.bfloat16).to(device)  # one slot each
+            gid, idx = engine.pack(t, stream)
+            handles.append((t, gid, idx))
+        engine.commit(stream)
+        return engine.stats()["d2h_copies"] - copies  # segments of the group
+
+    try:
+        assert engine.stats()["device_ring_bytes"] == 4 * slot
+        sizes = []
+        n = group(3)
+        rings = [(2, max(2, min(10, n + 2)))]
+        sizes.append(engine.stats()["device_ring_bytes"])
+        n = group(14)
+        assert n >= 13
+        rings.append((min(4, (n + 2) // 3), min(10, n + 2)))
+        sizes.append(engine.stats()["device_ring_bytes"])
+        group(2)  # nothing more to grow
+        sizes.append(engine.stats()["device_ring_bytes"])
+        assert rings[1] == (4, 10)
+        if wire == "off":
+            assert sizes == [sum(rings[0]) * slot, sum(rings[1]) * slot, sum(rings[1]) * slot]
+        else:
+            assert engine.stats()["wire_segments"] > 0
+            assert sizes[0] < sizes[1] == sizes[2]
+        _restore_and_check(engine, handles, device, list(reversed(range(len(handles)))))
+        stats = engine.stats()
+        assert stats["copy_failures"] == 0 and stats["prefetch_hits"] > 0
+        # a second step runs on the grown rings
+        first = len(handles)
+        group(14)
+        group(3)
+        assert engine.stats()["device_ring_bytes"] == sizes[2]
+        _restore_and_check(engine, handles, device, list(reversed(range(first, len(handles)))))
+        for _, gid, idx in handles:
+            engine.drop(gid, idx)
+        engine.synchronize()
+        assert engine.stats()["host_bytes_in_use"] == 0
+    finally:
+        engine.close()
+
+
+def test_fixed_rings_do_not_grow() -> None:
+    """Caps of 0 keep the configured rings whatever the group size."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine(stage_slots=2, restore_slots=2, wire_coding="off", staged_restore=False)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(6)
+    try:
+        handles = []
+        for _ in range(9):
+            t = torch.randn(MiB - 4096, generator=g).to(torch.bfloat16).to(device)
+            handles.append((t, *engine.pack(t, stream)))
+        engine.commit(stream)
+        assert engine.stats()["device_ring_bytes"] == 4 * 2 * MiB
+        _restore_and_check(engine, handles, device, list(reversed(range(len(handles)))))
+        for _, gid, idx in handles:
+            engine.drop(gid, idx)
     finally:
         engine.close()
 
@@ -706,7 +792,8 @@ def test_small_groups_restored_ahead_share_one_scatter_launch() -> None:
     g = torch.Generator(device="cpu").manual_seed(19)
     # 8 MiB slots: each 1.5 MB group is one segment; 6 restore slots hold the prefetched ones
     cfg = EngineConfig(stage_slot_bytes=8 * MiB, stage_slots=2, restore_slots=6, host_chunk_bytes=32 * MiB,
-                       wire_coding="off", staged_restore=False, prefetch=False, restore_ahead_bytes=5 * MiB)
+                       wire_coding="off", staged_restore=False, prefetch=False, restore_ahead_bytes=5 * MiB,
+                       stage_slots_max=0, restore_slots_max=0)
     engine = OffloadEngine(device, cfg)
     try:
         handles = []
@@ -776,7 +863,8 @@ def test_commits_gather_together_up_to_commit_batch_bytes() -> None:
     g = torch.Generator(device="cpu").manual_seed(23)
     # 2 MB groups; an 8 MiB slot holds four of them
     cfg = EngineConfig(stage_slot_bytes=8 * MiB, stage_slots=3, restore_slots=4, host_chunk_bytes=32 * MiB,
-                       commit_batch_bytes=5 * MiB, wire_coding="off", prefetch=False)
+                       commit_batch_bytes=5 * MiB, wire_coding="off", prefetch=False, stage_slots_max=0,
+                       restore_slots_max=0)
     engine = OffloadEngine(device, cfg)
     try:
         groups = []
