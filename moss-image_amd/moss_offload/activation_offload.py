@@ -408,12 +408,17 @@ class _ActivationOffload:
         # the forward's graph alive until the next engine call)
         self.engine.flush()
         if self.engine.config.prefetch and exc[0] is None:
-            # Backward starts with the last group, and with every group holding a save the
-            # forward made repeatedly (e.g. one RoPE table checkpointed with every block): start
+            # Backward starts with the last group, and with every group holding a save that
+            # later blocks made again (e.g. one RoPE table checkpointed with every block): start
             # bringing them back now, those first, then the groups backward needs after the
             # last one (which would otherwise take every free slot before a shared group got
-            # one). Segments still in the staging ring are skipped.
-            for gid in ([last] if last is not None else []) + sorted(self._shared - {last}, reverse=True):
+            # one). Segments still in the staging ring are skipped. A shared group larger than
+            # one restore-ahead launch (a non-checkpointed block's whole saved set) is not
+            # fetched whole: backward restores its shared entry alone, from the segment that
+            # holds it.
+            shared = [gid for gid in sorted(self._shared - {last}, reverse=True)
+                      if self.engine.group_bytes(gid) <= max(self.engine.config.restore_ahead_bytes, 1)]
+            for gid in ([last] if last is not None else []) + shared:
                 self.engine.prefetch(gid, stream)
             if last is not None:
                 self.engine.prefetch(last, stream, ahead=True)
@@ -484,7 +489,8 @@ class _ActivationOffload:
                 ref, version, gid, idx = hit
                 if not ref.expired() and version == tensor._version and self.engine.acquire(gid, idx):
                     _COUNTS["deduplicated"] += 1
-                    self._shared.add(gid)
+                    if self.engine.committed(gid):  # saved again by a later block
+                        self._shared.add(gid)
                     handle = _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
                     self._remember(tensor, handle)
                     return handle

@@ -247,7 +247,7 @@ class OffloadEngine:
         self._launched = ctypes.c_uint64()
         self._committed_calls = 0  # pack calls made before the last commit (their groups are committed)
         # restores that asked for groups ahead, the groups offered, the groups restored ahead
-        self._ahead_counts = {"restores": 0, "offered": 0, "restored": 0}
+        self._ahead_counts = {"restores": 0, "offered": 0, "restored": 0, "alone": 0}
 
     # ------------------------------------------------------------------ forward
     def pack(self, source: torch.Tensor, stream: int, narrow: bool = False) -> tuple[int, int]:
@@ -404,14 +404,25 @@ class OffloadEngine:
             cached = self._take_cached(entry, reader)
             if cached is not None:
                 return cached
-            groups = [group] + self._ahead(gid)
+            # Backward takes groups youngest first. An entry of a group asked for while a younger
+            # group still waits is a save that later blocks share (one RoPE table or modulation
+            # saved by every block, kept once by deduplication). If its group is larger than one
+            # restore-ahead launch (a non-checkpointed block's saves), that entry is restored
+            # alone, from the segments that hold it, and the rest of the group waits for its own
+            # turn: restored whole now, it would hold device memory for the whole backward and
+            # take the link from the groups backward needs first. A small group (a checkpointed
+            # block's inputs) is restored whole as before.
+            alone = (self._younger_waiting(gid) and
+                     sum(e.nbytes for e in group.entries if e.refs > 0 and e.restored is None) >
+                     max(self.config.restore_ahead_bytes, 1))
+            groups = [group] if alone else [group] + self._ahead(gid)
             counts = (ctypes.c_uint32 * len(groups))(*(len(g.entries) for g in groups))
             dst = (ctypes.c_uint64 * sum(counts))()
             made, base = [], 0
             for k, g in enumerate(groups):
                 mine = []
                 for j, other in enumerate(g.entries):
-                    if (k or j != idx) and (other.refs <= 0 or other.restored is not None):
+                    if (k or j != idx) and (alone or other.refs <= 0 or other.restored is not None):
                         continue
                     tensor = torch.empty_strided(other.payload_shape, other.stride, dtype=other.dtype,
                                                  device=self.device)
@@ -425,6 +436,7 @@ class OffloadEngine:
             _native.check("mo_unpack_groups", self._lib.mo_unpack_groups(self._handle, gids, dst, counts, len(groups),
                                                                          stream, unpacked))
             self._ahead_counts["restores"] += 1
+            self._ahead_counts["alone"] += alone
             self._ahead_counts["offered"] += len(groups) - 1
             self._ahead_counts["restored"] += sum(unpacked[k] for k in range(1, len(groups)))
             for k, mine in enumerate(made):
@@ -434,7 +446,7 @@ class OffloadEngine:
                         other.restored_version = tensor._version
             if self._held:  # unpacking the open group commits it
                 self._hold()
-            if self.config.prefetch:
+            if self.config.prefetch and not alone:
                 self._prefetch_after(gid, stream, max(1, self.config.prefetch_depth))
             return self._take_cached(entry, reader)
 
@@ -506,18 +518,49 @@ class OffloadEngine:
             return copy.copy_(tensor)
         return tensor
 
+    @staticmethod
+    def _waiting(group: _GroupState | None) -> bool:
+        """A committed group with an entry still to restore."""
+
+        return group is not None and group.committed and any(
+            e.refs > 0 and e.restored is None and e.nbytes for e in group.entries)
+
     def _predict_next(self, gid: int) -> int | None:
         """The group backward needs next: the youngest live group older than ``gid``."""
 
         pos = bisect.bisect_left(self._live, gid) - 1
         while pos >= 0:
             cand = self._groups.get(self._live[pos])
-            if cand is not None and cand.committed and any(
-                e.refs > 0 and e.restored is None and e.nbytes for e in cand.entries
-            ):
+            if self._waiting(cand):
                 return cand.gid
             pos -= 1
         return None
+
+    def _younger_waiting(self, gid: int) -> bool:
+        """Whether a live group younger than ``gid`` still has an entry to restore."""
+
+        pos = len(self._live) - 1
+        while pos >= 0 and self._live[pos] > gid:
+            if self._waiting(self._groups.get(self._live[pos])):
+                return True
+            pos -= 1
+        return False
+
+    def group_bytes(self, gid: int) -> int:
+        """Payload bytes of the entries of ``gid`` still to restore (0 for an unknown group)."""
+
+        with self._lock:
+            group = self._groups.get(gid)
+            if group is None:
+                return 0
+            return sum(e.nbytes for e in group.entries if e.refs > 0 and e.restored is None)
+
+    def committed(self, gid: int) -> bool:
+        """Whether ``gid`` is a known, committed group."""
+
+        with self._lock:
+            group = self._groups.get(gid)
+            return group is not None and group.committed
 
     # ------------------------------------------------------------------ housekeeping
     def synchronize(self) -> None:

@@ -628,6 +628,64 @@ def test_rings_grow_at_the_commit_of_a_large_group(wire) -> None:
         engine.close()
 
 
+def test_shared_entry_of_an_older_large_group_is_restored_alone() -> None:
+    """An entry of a large group asked for while a younger group still waits (a save later
+    blocks share, kept once by deduplication) is restored alone: its group's other entries stay
+    on the host until their own turn, nothing else is scattered, and every restore is bitwise.
+    A small group asked for out of order is restored whole, as before."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine(stage_slots=3, restore_slots=6, wire_coding="off", staged_restore=False,
+                     restore_ahead_bytes=1 * MiB)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(7)
+
+    def tensor(n):
+        return torch.randn(n, generator=g).to(torch.bfloat16).to(device)
+
+    try:
+        old = [tensor(600_000) for _ in range(3)]  # about 3.6 MB: a large group
+        refs_old = [engine.pack(t, stream) for t in old]
+        engine.commit(stream)
+        small = tensor(40_000)  # 80 KB: a small group
+        ref_small = engine.pack(small, stream)
+        small_other = tensor(30_000)
+        ref_small_other = engine.pack(small_other, stream)
+        engine.commit(stream)
+        young = [tensor(500_000) for _ in range(2)]
+        refs_young = [engine.pack(t, stream) for t in young]
+        gid_shared, idx_shared = refs_old[1]
+        assert engine.acquire(gid_shared, idx_shared)  # the younger block saves it again
+        engine.commit(stream)
+        engine.synchronize()
+
+        before = engine.stats()
+        got = engine.restore(gid_shared, idx_shared, stream)  # asked for before the young group
+        assert_bitwise(got, old[1])
+        after = engine.stats()
+        assert after["py_ahead_alone"] - before["py_ahead_alone"] == 1
+        assert after["bytes_unpacked"] - before["bytes_unpacked"] == old[1].numel() * 2
+        # the small group asked for out of order comes back whole
+        assert_bitwise(engine.restore(*ref_small, stream), small)
+        assert engine.stats()["bytes_unpacked"] - after["bytes_unpacked"] == (small.numel() + small_other.numel()) * 2
+        assert engine.stats()["py_ahead_alone"] == after["py_ahead_alone"]
+        # backward order from here: the young group, the shared entry's second reference, the rest
+        for (gid, idx), t in zip(refs_young, young):
+            assert_bitwise(engine.restore(gid, idx, stream), t)
+        assert_bitwise(engine.restore(gid_shared, idx_shared, stream), old[1])
+        assert_bitwise(engine.restore(*ref_small_other, stream), small_other)
+        for (gid, idx), t in zip(refs_old, old):
+            if idx != idx_shared:
+                assert_bitwise(engine.restore(gid, idx, stream), t)
+        assert engine.stats()["copy_failures"] == 0
+        for gid, idx in refs_old + refs_young + [ref_small, ref_small_other, (gid_shared, idx_shared)]:
+            engine.drop(gid, idx)
+        engine.synchronize()
+        assert engine.stats()["groups_live"] == 0 and engine.stats()["host_bytes_in_use"] == 0
+    finally:
+        engine.close()
+
+
 def test_fixed_rings_do_not_grow() -> None:
     """Caps of 0 keep the configured rings whatever the group size."""
 
