@@ -1039,7 +1039,7 @@ def run(args) -> dict:
         staged_restore=not args.no_staged_restore,
         kernel_copy=args.kernel_copy,
         link=args.link,
-        pack_nt_load=args.pack_nt_load,
+        pack_nt_load=not args.pack_cached_load,
         unpack_nt_load=not args.unpack_cached_load,
         unpack_nt_store=not args.unpack_cached_store,
         batch_packs=not args.eager_pack,
@@ -1084,7 +1084,8 @@ def run(args) -> dict:
                                 d2h_engine=args.d2h_engine, h2d_engine=args.h2d_engine, narrow=narrow,
                                 link=args.link,
                                 cache=dict(wire_coding=args.micro_wire_coding,
-                                           pack_nt_load=args.pack_nt_load, unpack_nt_load=not args.unpack_cached_load,
+                                           pack_nt_load=not args.pack_cached_load,
+                                           unpack_nt_load=not args.unpack_cached_load,
                                            unpack_nt_store=not args.unpack_cached_store))
         result["micro"].update(narrowed_tensors=sum(narrow), link_bytes_per_iter=moved)
         m = result["micro"]
@@ -1493,7 +1494,8 @@ def main() -> int:
     parser.add_argument("--eager-pack", action="store_true",
                         help="one gather launch per save instead of one per staging segment")
     parser.add_argument("--kernel-copy", action="store_true", help="copy kernel on HIP streams instead of SDMA")
-    parser.add_argument("--pack-nt-load", action="store_true", help="pack reads saves with non-temporal loads")
+    parser.add_argument("--pack-cached-load", action="store_true",
+                        help="pack reads saves with ordinary loads instead of non-temporal ones")
     parser.add_argument("--unpack-cached-load", action="store_true",
                         help="unpack reads payloads with ordinary loads instead of non-temporal ones")
     parser.add_argument("--unpack-cached-store", action="store_true",

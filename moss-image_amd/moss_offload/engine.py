@@ -79,7 +79,12 @@ class EngineConfig:
     link: str = "sdma"
     # Cache policy of the kernels (measured choices are the defaults): non-temporal loads of the
     # saved tensors in pack, of the payload in unpack, and streaming stores of restored tensors.
-    pack_nt_load: bool = False
+    # Pack's non-temporal loads (MO_FLAG_PACK_NT_LOAD; the bare C ABI reads with ordinary loads
+    # unless it is set): with gathers batched per segment and per commit, in-step pack went
+    # 5.63 -> 5.91 TB/s in config 3 checkpointed, 5.12 -> 5.53 not checkpointed, 5.67 -> 5.93 in
+    # config 5 unpacked, and 5.75 -> 5.87 on the block microbench, step times unchanged. (With
+    # one gather per save they had slowed in-step pack: the forward still read the saves.)
+    pack_nt_load: bool = True
     unpack_nt_load: bool = True
     unpack_nt_store: bool = True
     # Lossless wire coding of staging segments on the SDMA link (MO_FLAG_WIRE_*): "off", "on"
