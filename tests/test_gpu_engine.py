@@ -686,6 +686,46 @@ def test_shared_entry_of_an_older_large_group_is_restored_alone() -> None:
         engine.close()
 
 
+@pytest.mark.parametrize("layout", ["dense", "transposed", "padded"])
+def test_each_reader_of_a_shared_entry_gets_its_own_bitwise_copy(layout) -> None:
+    """A save deduplicated for three readers is restored once; the first two takes get copies
+    of their own (the engine's scatter kernel for layouts without gaps, ``copy_`` otherwise),
+    the last the restored tensor itself: all bitwise, all with the save's strides, no two
+    sharing storage."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine(stage_slots=3, restore_slots=4, wire_coding="off")
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(9)
+    base = torch.randn(4 * 384 * 130, generator=g).to(torch.bfloat16).to(device)
+    if layout == "dense":
+        t = base[: 384 * 520].view(384, 520)
+    elif layout == "transposed":
+        t = base[: 4 * 384 * 128].view(4, 384, 128).transpose(0, 1)  # [384, 4, 128], strides (128, 49152, 1)
+    else:
+        t = base.view(4 * 384, 130)[:, :128]  # rows of 128 with a 2-element gap
+    try:
+        gid, idx = engine.pack(t, stream)
+        assert engine.acquire(gid, idx) and engine.acquire(gid, idx)
+        engine.commit(stream)
+        engine.synchronize()
+        got = []
+        for _ in range(3):
+            r = engine.restore(gid, idx, stream)
+            assert r.stride() == t.stride()
+            assert_bitwise(r, t)
+            got.append(r)
+            engine.drop(gid, idx)
+        ptrs = {r.untyped_storage().data_ptr() for r in got}
+        assert len(ptrs) == 3
+        torch.cuda.synchronize(device)
+        for r in got:
+            assert_bitwise(r, t)
+        assert engine.stats()["copy_failures"] == 0
+    finally:
+        engine.close()
+
+
 def test_fixed_rings_do_not_grow() -> None:
     """Caps of 0 keep the configured rings whatever the group size."""
 
