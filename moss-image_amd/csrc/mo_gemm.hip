@@ -661,25 +661,36 @@ __device__ __forceinline__ void ws_body(const __bf16* __restrict__ A, const int8
     return;
   }
   // ---- epilogue: bias, bf16, store (rows past M and columns past N fall outside) ----
+  // Lane half h of column tile ct holds rows 4 h + .. of columns 32 ct + lr. One
+  // v_permlane32_swap per pair of values gives lane l the value of row `row0` (from h = 0)
+  // and column l of the wave's 64 in one register, of row `row0 + 4` (from h = 1) in the
+  // other: each store instruction then writes one full 128-byte row piece.
   const rsrc_t rc_src = make_rsrc(C + (size_t)m0 * N, (uint32_t)(min(M - m0, kBM) * N * 2));
   const rsrc_t rbias_src = make_rsrc(bias, bias ? (uint32_t)N * 2 : 0u);
+  float b[2];
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
     const int col = c0 + 64 * wave + 32 * ct + lr;
-    const bool col_ok = col < N;
-    const float b = (float)__builtin_bit_cast(
-        __bf16, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rbias_src, col_ok ? col * 2 : (int)kOob, 0, 0));
+    b[ct] = (float)__builtin_bit_cast(
+        __bf16, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rbias_src, col < N ? col * 2 : (int)kOob, 0, 0));
+  }
+  const int out_col = c0 + 64 * wave + lane;  // after the swap: column `lane` of the wave's 64
+  const bool out_ok = out_col < N;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < 8; ++i) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        const __bf16 v = (__bf16)(acc[i][ct][r] + b);
-        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), rc_src,
-                                              col_ok ? (int)((uint32_t)(row * N + col) * 2) : (int)kOob, 0, 0);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+    for (int r = 0; r < 16; ++r) {
+      const int row0 = i * 32 + 8 * (r >> 2) + (r & 3);
+      const unsigned int x = __builtin_bit_cast(unsigned short, (__bf16)(acc[i][0][r] + b[0]));
+      const unsigned int y = __builtin_bit_cast(unsigned short, (__bf16)(acc[i][1][r] + b[1]));
+      // x' = (x lanes 0-31, y lanes 0-31): row0; y' = (x lanes 32-63, y lanes 32-63): row0 + 4
+      const auto sw = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)sw[0], rc_src,
+                                            out_ok ? (int)((uint32_t)(row0 * N + out_col) * 2) : (int)kOob, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)sw[1], rc_src,
+                                            out_ok ? (int)((uint32_t)((row0 + 4) * N + out_col) * 2) : (int)kOob, 0, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
