@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 19
+#define MO_ABI_VERSION 20
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -293,6 +293,12 @@ int mo_commit(mo_engine* engine, uint64_t stream, uint64_t* group);
  * so a later mo_unpack on `stream` finds them resident. Segments still intact in their staging
  * slot (and packed on `stream`) are skipped: unpack reads them there. Never blocks the host. */
 int mo_prefetch(mo_engine* engine, uint64_t group, uint64_t stream);
+
+/* The same for the segments that hold entry `entry` of the group only: a save that later blocks
+ * share, which backward needs while the rest of its (older) group is not due yet. No reference
+ * counterpart: the reference prefetches nothing; the H2D it brings forward is the one the
+ * reference's unpack (activation_offload.py:136-147) waits for. */
+int mo_prefetch_entry(mo_engine* engine, uint64_t group, uint32_t entry, uint64_t stream);
 
 /* Prefetch several groups, given in the order backward will need them: the first as
  * mo_prefetch does; each later one only if every segment it still needs gets a free restore

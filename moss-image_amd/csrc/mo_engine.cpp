@@ -923,14 +923,24 @@ struct Engine {
     return 0;
   }
 
-  int prefetch(uint64_t gid, hipStream_t stream) {
+  // entry: only the segments holding a piece of that entry (kAllEntries: every segment).
+  static constexpr uint32_t kAllEntries = 0xffffffffu;
+  int prefetch(uint64_t gid, hipStream_t stream, uint32_t entry = kAllEntries) {
     if (!closing.empty())
       if (int rc = flush_packs()) return rc;
     process_pending(false);
     Group* g = find(gid);
     if (!g) return fail(MO_E_INVALID, "mo_prefetch: unknown group " + std::to_string(gid));
+    if (entry != kAllEntries && entry >= g->entries.size())
+      return fail(MO_E_INVALID, "mo_prefetch_entry: group " + std::to_string(gid) + " has no entry " +
+                                    std::to_string(entry));
     if (g->open) return 0;
     for (uint32_t si = 0; si < g->segs.size(); ++si) {
+      if (entry != kAllEntries) {
+        bool holds = false;
+        for (const Piece& p : g->segs[si].pieces) holds = holds || p.entry == entry;
+        if (!holds) continue;
+      }
       if (resident(*g, si) || staged(g->segs[si], stream)) continue;
       const int k = pick_slot(*g, si, true);
       if (k < 0) break;
@@ -1605,6 +1615,11 @@ int mo_commit(mo_engine* engine, uint64_t stream, uint64_t* group) {
 
 int mo_prefetch(mo_engine* engine, uint64_t group, uint64_t stream) {
   MO_ENGINE_CALL(engine, engine->e.prefetch(group, (hipStream_t)stream));
+}
+
+int mo_prefetch_entry(mo_engine* engine, uint64_t group, uint32_t entry, uint64_t stream) {
+  if (entry == mo::Engine::kAllEntries) return mo::fail(MO_E_INVALID, "mo_prefetch_entry: bad entry index");
+  MO_ENGINE_CALL(engine, engine->e.prefetch(group, (hipStream_t)stream, entry));
 }
 
 int mo_prefetch_groups(mo_engine* engine, const uint64_t* groups, uint32_t n, uint64_t stream) {

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 19
+MO_ABI_VERSION = 20
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -201,6 +201,7 @@ SIGNATURES: dict[str, tuple] = {
     "mo_equal_discard": (ctypes.c_int, [ctypes.c_void_p, _u64]),
     "mo_commit": (ctypes.c_int, [ctypes.c_void_p, _u64, _P(_u64)]),
     "mo_prefetch": (ctypes.c_int, [ctypes.c_void_p, _u64, _u64]),
+    "mo_prefetch_entry": (ctypes.c_int, [ctypes.c_void_p, _u64, ctypes.c_uint32, _u64]),
     "mo_prefetch_groups": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(_u64), ctypes.c_uint32, _u64]),
     "mo_unpack": (ctypes.c_int, [ctypes.c_void_p, _u64, _P(_u64), ctypes.c_uint32, _u64]),
     "mo_unpack_groups": (

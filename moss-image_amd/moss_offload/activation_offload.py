@@ -368,7 +368,8 @@ class _ActivationOffload:
         # packed so far: the inputs a later product can be recomputed from
         self._made: dict[tuple, tuple] = {}
         self._seen: dict[tuple, tuple] = {}
-        self._shared: set[int] = set()  # groups holding saves made more than once
+        # saves a later block made again: (group, entry) -> None, in the order first seen
+        self._shared: dict[tuple[int, int], None] = {}
         self._hooks = torch.autograd.graph.saved_tensors_hooks(self.pack, self.unpack)
         self._block_handles: list = []
         # keep_last_blocks: block index of each layer, and the first index whose saves stay
@@ -414,12 +415,20 @@ class _ActivationOffload:
             # last one (which would otherwise take every free slot before a shared group got
             # one). Segments still in the staging ring are skipped. A shared group larger than
             # one restore-ahead launch (a non-checkpointed block's whole saved set) is not
-            # fetched whole: backward restores its shared entry alone, from the segment that
-            # holds it.
-            shared = [gid for gid in sorted(self._shared - {last}, reverse=True)
-                      if self.engine.group_bytes(gid) <= max(self.engine.config.restore_ahead_bytes, 1)]
-            for gid in ([last] if last is not None else []) + shared:
+            # fetched whole: only the segments holding its shared saves, which backward restores
+            # alone (fetched on demand instead, such a segment queued behind the next block's
+            # prefetch: 21 ms a step at 2048^2).
+            limit = max(self.engine.config.restore_ahead_bytes, 1)
+            small, entries = [], []
+            for gid in sorted({g for g, _ in self._shared} - {last}, reverse=True):
+                if self.engine.group_bytes(gid) <= limit:
+                    small.append(gid)
+                else:
+                    entries.extend((g, i) for g, i in self._shared if g == gid)
+            for gid in ([last] if last is not None else []) + small:
                 self.engine.prefetch(gid, stream)
+            for gid, idx in entries:
+                self.engine.prefetch_entry(gid, idx, stream)
             if last is not None:
                 self.engine.prefetch(last, stream, ahead=True)
         self._shared.clear()
@@ -490,7 +499,7 @@ class _ActivationOffload:
                 if not ref.expired() and version == tensor._version and self.engine.acquire(gid, idx):
                     _COUNTS["deduplicated"] += 1
                     if self.engine.committed(gid):  # saved again by a later block
-                        self._shared.add(gid)
+                        self._shared[(gid, idx)] = None
                     handle = _OffloadedTensor(self.engine, gid, idx, device, tensor.dtype, shape, stride, payload_shape)
                     self._remember(tensor, handle)
                     return handle

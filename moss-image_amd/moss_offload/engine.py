@@ -489,6 +489,15 @@ class OffloadEngine:
                 more = self._predict_chain(gid, max(1, self.config.prefetch_depth) - 1) if ahead else []
                 self._prefetch_groups([gid] + more, stream)
 
+    def prefetch_entry(self, gid: int, idx: int, stream: int) -> None:
+        """Queue H2D of the segments holding entry ``idx`` of group ``gid`` (a save later blocks
+        share, restored alone while its group is not due yet)."""
+
+        with self._lock:
+            group = self._groups.get(gid)
+            if group is not None and idx < len(group.entries) and group.entries[idx].restored is None:
+                _native.check("mo_prefetch_entry", self._lib.mo_prefetch_entry(self._handle, gid, idx, stream))
+
     def _prefetch_after(self, gid: int, stream: int, count: int) -> None:
         self._prefetch_groups(self._predict_chain(gid, count), stream)
 

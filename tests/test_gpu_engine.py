@@ -686,6 +686,42 @@ def test_shared_entry_of_an_older_large_group_is_restored_alone() -> None:
         engine.close()
 
 
+def test_prefetch_entry_fetches_only_the_segments_holding_it() -> None:
+    """mo_prefetch_entry queues the H2D of the segments that hold one entry of a group, not the
+    group's others: of four one-segment entries it fetches one, and the group's restore then
+    finds that one resident and fetches the other three. A bad entry index is an error."""
+
+    from moss_offload import _native
+
+    device = torch.device("cuda", 0)
+    engine = _engine(stage_slots=4, restore_slots=6, wire_coding="off", staged_restore=False, prefetch=False)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(12)
+    try:
+        ts = [torch.randn(MiB - 4096, generator=g).to(torch.bfloat16).to(device) for _ in range(4)]  # a slot each
+        refs = [engine.pack(t, stream) for t in ts]
+        engine.commit(stream)
+        engine.synchronize()
+        gid = refs[0][0]
+        assert engine.stats()["d2h_copies"] == 4
+        before = engine.stats()
+        engine.prefetch_entry(gid, 2, stream)
+        assert engine.stats()["prefetch_issued"] - before["prefetch_issued"] == 1
+        assert_bitwise(engine.restore(gid, 2, stream), ts[2])  # restores the whole group
+        after = engine.stats()
+        assert after["prefetch_hits"] - before["prefetch_hits"] == 1
+        assert after["restore_fetches"] - before["restore_fetches"] == 3
+        for (_, idx), t in zip(refs, ts):
+            if idx != 2:
+                assert_bitwise(engine.restore(gid, idx, stream), t)
+        with pytest.raises(RuntimeError, match="no entry 99"):
+            _native.check("mo_prefetch_entry", engine._lib.mo_prefetch_entry(engine._handle, gid, 99, stream))
+        for gid_, idx in refs:
+            engine.drop(gid_, idx)
+    finally:
+        engine.close()
+
+
 @pytest.mark.parametrize("layout", ["dense", "transposed", "padded"])
 def test_each_reader_of_a_shared_entry_gets_its_own_bitwise_copy(layout) -> None:
     """A save deduplicated for three readers is restored once; the first two takes get copies
