@@ -1278,6 +1278,12 @@ def run(args) -> dict:
             # every mode and round starts from zero (the modes share the engine), and what it
             # counted is added to its own totals right after it ran
             engine.reset_stats()
+            if first:
+                free, total = torch.cuda.mem_get_info(device)
+                st0 = engine.stats()
+                log(f"{regime_name}/{mode}: device free {free / 2**30:.1f} of {total / 2**30:.1f} GiB, torch reserved "
+                    f"{torch.cuda.memory_reserved(device) / 2**30:.1f} GiB, engine rings {st0['device_ring_bytes'] / 2**30:.1f} "
+                    f"GiB, pinned pool {st0['host_bytes_reserved'] / 2**30:.1f} GiB")
             moss_offload.reset_hook_counters()
             if streamer is not None:
                 streamer.reset_stats()
@@ -1385,6 +1391,7 @@ def run(args) -> dict:
                     prefetch_hits=st["prefetch_hits"],
                     restore_fetches=st["restore_fetches"],
                     host_pinned_peak_bytes=st["host_bytes_peak"],
+                    host_pinned_reserved_bytes=st["host_bytes_reserved"],  # the pool only grows within a mode
                     restores_per_step=st["py_ahead_restores"] / n,
                     groups_restored_ahead_per_step=st["py_ahead_restored"] / n,
                     groups_offered_ahead_per_step=st["py_ahead_offered"] / n,
@@ -1392,6 +1399,11 @@ def run(args) -> dict:
                     ahead_in_flight_per_step=st["ahead_in_flight"] / n,
                 )
                 engine.trim()
+                left = engine.stats()
+                # what the engine still holds once the mode is over: no live group, and the
+                # pinned pool given back to the driver but for chunks a live payload still uses
+                record.update(groups_live_after=left["groups_live"], py_groups_live_after=left["py_groups_live"],
+                              pinned_reserved_after_trim=left["host_bytes_reserved"])
             entry[mode] = record
         none = entry.get("none", {}).get("s_per_it")
         for name in ("engine", "engine_hipdma"):
@@ -1428,6 +1440,10 @@ def run(args) -> dict:
         finally:
             while cleanups:
                 cleanups.pop()()
+            # a leg's second engines (the HIP-stream transport) go with the leg: their rings and
+            # pinned pool are not the next leg's
+            while _SECOND_ENGINES:
+                _SECOND_ENGINES.popitem()[1].close()
     return result
 
 
