@@ -339,7 +339,7 @@ def host_work(seconds: float) -> None:
 # engine statistics that are levels at the time of reading, not counts: summed over a mode's
 # rounds they would mean nothing, so the last reading stands
 ENGINE_LEVELS = ("groups_live", "entries_live", "host_bytes_in_use", "host_bytes_reserved", "device_ring_bytes",
-                 "py_groups_live")
+                 "py_groups_live", "restore_slots_big", "restore_slots_small")
 
 
 def add_counts(total: dict, reading: dict, latest=(), peak=()) -> None:
@@ -689,7 +689,7 @@ def micro(device, tensors, iters: int, warmup: int, slot_mib: int, stage_slots: 
 
     engine = OffloadEngine(device, EngineConfig(
         stage_slot_bytes=slot_mib << 20, stage_slots=stage_slots, restore_slots=restore_slots,
-        stage_slots_max=0, restore_slots_max=0,  # the microbench's rings as given
+        stage_slots_max=0, restore_slots_max=0, restore_small_slots=0,  # the microbench's rings as given
         timing=True, kernel_timing=True, staged_restore=False, prefetch=False, batch_packs=batch_packs,
         d2h_engine=d2h_engine, h2d_engine=h2d_engine, link=link, **(cache or {})))
     stream = torch.cuda.current_stream(device).cuda_stream
@@ -1033,6 +1033,7 @@ def run(args) -> dict:
         restore_slots=args.restore_slots,
         stage_slots_max=args.stage_slots_max,
         restore_slots_max=args.restore_slots_max,
+        restore_small_slots=args.restore_small_slots,
         prefetch_depth=args.prefetch_depth,
         stage_slot_bytes=args.slot_mib << 20,
         **({} if args.restore_ahead_mib is None else {"restore_ahead_bytes": args.restore_ahead_mib << 20}),
@@ -1495,6 +1496,9 @@ def main() -> int:
                         help="staging ring growth cap (0: fixed ring)")
     parser.add_argument("--restore-slots-max", type=int, default=32,
                         help="restore ring growth cap (0: fixed ring)")
+    parser.add_argument("--restore-small-slots", type=int, default=24,
+                        help="quarter-size restore slots for checkpointed blocks' inputs (0: none, and every "
+                             "restore slot allocated up front)")
     parser.add_argument("--prefetch-depth", type=int, default=16,
                         help="groups the engine prefetches ahead of backward after each restored group")
     parser.add_argument("--slot-mib", type=int, default=128)

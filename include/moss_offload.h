@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MO_ABI_VERSION 20
+#define MO_ABI_VERSION 21
 #define MO_MAX_DIMS 8
 
 /* Error codes outside the hipError_t range. */
@@ -136,6 +136,14 @@ typedef struct mo_config {
                                    A slot that cannot be allocated (or whose wire buffer
                                    would pass wire_device_limit) ends the growth; the
                                    engine runs on with the slots it has                  */
+  uint32_t restore_small_slots; /* [0 = off] restore slots of a quarter of
+                                   stage_slot_bytes for raw segments that fit one: the
+                                   ring gains up to this many once 8 groups in a row were
+                                   committed with only such segments (a checkpointed
+                                   block's inputs). Nonzero also allocates every restore
+                                   slot past the first two at its first use, and mo_trim
+                                   frees them again once no group is live. stage_slots_max
+                                   + restore_slots_max + this: 64 at most              */
 } mo_config;
 
 /* Where one packed tensor lives: its group (one block's saves) and index in the group. */
@@ -181,6 +189,8 @@ typedef struct mo_stats {
   uint64_t ahead_restored;     /* further groups of mo_unpack_groups restored               */
   uint64_t ahead_not_resident; /* further groups left: a segment was not in a restore slot  */
   uint64_t ahead_in_flight;    /* further groups left: a segment's H2D had not started      */
+  uint64_t restore_slots_big;   /* restore slots of stage_slot_bytes holding device memory  */
+  uint64_t restore_slots_small; /* restore slots of a quarter of that (restore_small_slots) */
 } mo_stats;
 
 typedef struct mo_engine mo_engine;
@@ -340,7 +350,8 @@ int mo_reset_stats(mo_engine* engine);
 
 /* Release pinned chunks that hold no live payload. With no group live, also free the wire
  * buffers (after waiting for every copy and for the device; the next coded segment allocates
- * them again). */
+ * them again) and, with restore_small_slots set, the memory of every restore slot past the
+ * first two (given again at the slot's next use). */
 int mo_trim(mo_engine* engine);
 
 /* Name of the host-link transport in use: "sdma" or "kernel". */

@@ -265,7 +265,10 @@ struct StageSlot {
 };
 
 struct RestoreSlot {
-  char* dev = nullptr;
+  char* dev = nullptr;   // null until the slot is first used (restore_small_slots), or after mo_trim
+  uint64_t cap = 0;      // bytes of `dev`: stage_slot_bytes, or small_cap for a small slot
+  bool small = false;    // holds only raw segments of at most small_cap bytes
+  bool dead = false;     // its allocation failed: not used again until mo_trim
   uint64_t group = kNone;
   uint32_t seg = 0;
   uint64_t gen = 0;
@@ -725,14 +728,16 @@ struct Engine {
     const uint64_t bytes = ((wire_capacity(cfg.stage_slot_bytes) + cfg.stage_slot_bytes / 64 + (2ull << 20)) + 4095) &
                            ~uint64_t(4095);
     const uint64_t fetched = (wire_max_coded(cfg.stage_slot_bytes) + 4095) & ~uint64_t(4095);
-    bool ok = !cfg.wire_device_limit || bytes * stage.size() + fetched * restore.size() <= cfg.wire_device_limit;
+    bool ok = !cfg.wire_device_limit || bytes * stage.size() + fetched * big_slots() <= cfg.wire_device_limit;
     for (auto& s : stage)
       if (ok && !s.wire && hipMalloc(&s.wire, bytes) != hipSuccess) {
         s.wire = nullptr;
         ok = false;
       }
+    // full-size restore slots that hold memory; one given its memory later gets its wire
+    // buffer with it (alloc_restore)
     for (auto& r : restore)
-      if (ok && !r.wire && hipMalloc(&r.wire, fetched) != hipSuccess) {
+      if (ok && r.dev && !r.small && !r.wire && hipMalloc(&r.wire, fetched) != hipSuccess) {
         r.wire = nullptr;
         ok = false;
       }
@@ -883,7 +888,7 @@ struct Engine {
       if (int rc = flush_packs()) return rc;
     open_group->open = false;
     *gid = open_group->id;
-    grow_rings(open_group->segs.size());
+    grow_rings(*open_group);
     open_group = nullptr;
     open_seg = -1;
     return 0;
@@ -908,44 +913,88 @@ struct Engine {
   // block) eight slots for coded segments run 0.653 s/it against 0.665 with all sixteen; at
   // 2048² (about 25 a block, more than the ring) all sixteen run 2.60 against 2.88 with eight.
   // Checkpointed steps code nothing and keep the whole ring.
+  // (Counted over the full-size slots in ring order; small slots never hold coded segments.)
   static constexpr int kCodedSlotsMin = 8;
   int slot_limit(const Group& g, uint32_t si) const {
-    const int all = (int)restore.size();
-    if (!g.segs[si].wire) return all;
-    return std::min(all, std::max(kCodedSlotsMin, (int)g.segs.size() + 2));
+    if (!g.segs[si].wire) return kMaxSlots;
+    return std::max(kCodedSlotsMin, (int)g.segs.size() + 2);
   }
 
-  // Choose a restore slot for segment `si` of group `g` among its first slot_limit slots.
-  // for_prefetch: only slots that are empty or already consumed (a prefetch never evicts data
-  // that is still waiting for use).
+  // Small restore slots (restore_small_slots): a checkpointed block's inputs (28 MB at 1024^2)
+  // in a 32 MiB slot rather than a 128 MiB one.
+  uint64_t small_cap = 0;  // bytes of a small slot; 0: no small slots
+  bool small_fit(const Segment& seg) const { return small_cap && !seg.wire && seg.bytes <= small_cap; }
+  size_t big_slots() const {
+    size_t n = 0;
+    for (const RestoreSlot& r : restore) n += !r.small;
+    return n;
+  }
+
+  // Give restore slot k its device memory (and its wire buffer while coding's buffers exist).
+  // On failure the HIP error is cleared and the slot is left alone until mo_trim.
+  bool alloc_restore(int k) {
+    RestoreSlot& r = restore[k];
+    DeviceGuard guard(device);
+    if (hipMalloc(&r.dev, r.cap) != hipSuccess) r.dev = nullptr;
+    if (r.dev && !r.small && wire_restore_bytes && hipMalloc(&r.wire, wire_restore_bytes) != hipSuccess) {
+      r.wire = nullptr;
+      (void)hipFree(r.dev);
+      r.dev = nullptr;
+    }
+    if (r.dev) return true;
+    (void)hipGetLastError();
+    r.dead = true;
+    return false;
+  }
+
+  // Choose a restore slot for segment `si` of group `g`: a small slot only for a segment that
+  // fits one, a full-size one only among the first slot_limit of them. By rank, then least
+  // recently used:
+  //   a segment that fits a small slot: small and empty, small without memory yet, full-size
+  //     and empty, small in use, full-size in use, full-size without memory yet;
+  //   any other: empty, without memory yet, in use.
+  // A slot without memory gets it here. for_prefetch: only slots that are empty or already
+  // consumed (a prefetch never evicts data that is still waiting for use), and no full-size
+  // slot is given memory for a segment that fits a small one.
   int pick_slot(const Group& g, uint32_t si, bool for_prefetch) {
-    int best = -1;
+    const bool fits_small = small_fit(g.segs[si]);
     const int limit = slot_limit(g, si);
-    for (int k = 0; k < limit; ++k) {
-      const RestoreSlot& r = restore[k];
-      const bool empty = r.group == kNone;
-      const bool future_of_g = r.group == g.id && r.seg > si && !r.consumed;
-      if (future_of_g) continue;
-      if (for_prefetch && !empty && !r.consumed) continue;
-      if (best < 0) {
-        best = k;
-        continue;
-      }
-      const RestoreSlot& b = restore[best];
-      const bool bempty = b.group == kNone;
-      if (empty && !bempty) best = k;
-      else if (empty == bempty && r.tick < b.tick) best = k;
-    }
-    if (best < 0 && !for_prefetch) {
-      // Every slot holds a later, unconsumed segment of g: evict the furthest one.
-      uint32_t far = 0;
-      for (int k = 0; k < limit; ++k)
-        if (restore[k].seg >= far) {
-          far = restore[k].seg;
+    auto rank = [&](const RestoreSlot& r) -> int {
+      if (!r.dev) return r.small ? 1 : fits_small ? (for_prefetch ? -1 : 5) : 1;
+      if (r.group == kNone) return r.small ? 0 : fits_small ? 2 : 0;
+      if (for_prefetch && !r.consumed) return -1;
+      return r.small ? 3 : fits_small ? 4 : 2;
+    };
+    for (;;) {
+      int best = -1, best_rank = 0, big = 0;
+      for (int k = 0; k < (int)restore.size(); ++k) {
+        const RestoreSlot& r = restore[k];
+        if (r.small ? !fits_small : big++ >= limit) continue;
+        if (r.dead) continue;
+        if (r.group == g.id && r.seg > si && !r.consumed) continue;  // a later segment of g, still to be read
+        const int rk = rank(r);
+        if (rk < 0) continue;
+        if (best < 0 || rk < best_rank || (rk == best_rank && r.tick < restore[best].tick)) {
           best = k;
+          best_rank = rk;
         }
+      }
+      if (best < 0 && !for_prefetch) {
+        // Every slot it may take holds a later, unconsumed segment of g: evict the furthest one.
+        uint32_t far = 0;
+        big = 0;
+        for (int k = 0; k < (int)restore.size(); ++k) {
+          const RestoreSlot& r = restore[k];
+          if (r.small ? !fits_small : big++ >= limit) continue;
+          if (r.dev && r.group == g.id && r.seg >= far) {
+            far = r.seg;
+            best = k;
+          }
+        }
+      }
+      if (best < 0 || restore[best].dev || alloc_restore(best)) return best;
+      // that slot could not be given memory (now dead): choose again
     }
-    return best;
   }
 
   int fetch(Group& g, uint32_t si, int k) {
@@ -954,6 +1003,9 @@ struct Engine {
     if (!seg.committed || !seg.host)
       return fail(MO_E_STATE, "group " + std::to_string(g.id) + " segment " + std::to_string(si) +
                                   " has no host copy (its D2H was never issued)");
+    if (!r.dev || seg.bytes > r.cap || (seg.wire && !r.wire))
+      return fail(MO_E_STATE, "restore slot " + std::to_string(k) + " cannot hold group " + std::to_string(g.id) +
+                                  " segment " + std::to_string(si));
     CopyRef copy;
     if (seg.wire) {
       MO_LINK(link->h2d_sized(r.wire, seg.host, (const volatile uint64_t*)seg.host, seg.host_bytes, seg.d2h, r.gate,
@@ -1016,23 +1068,44 @@ struct Engine {
       Group* g = find(gids[k]);
       if (!g) return fail(MO_E_INVALID, "mo_prefetch_groups: unknown group " + std::to_string(gids[k]));
       if (g->open) return 0;
-      // needed: segments to fetch, of them `coded` confined to the first `low` slots
-      uint32_t needed = 0, coded = 0, free_slots = 0, free_low = 0;
-      int low = (int)restore.size();
-      for (uint32_t si = 0; si < g->segs.size(); ++si)
-        if (!resident(*g, si) && !staged(g->segs[si], stream)) {
-          ++needed;
-          if (g->segs[si].wire) {
-            ++coded;
-            low = std::min(low, slot_limit(*g, si));
-          }
+      // segments to fetch: `small` that fit a small slot, `big` that do not, of them `coded`
+      // confined to the first `low` full-size slots
+      uint32_t small = 0, big = 0, coded = 0;
+      int low = kMaxSlots;
+      for (uint32_t si = 0; si < g->segs.size(); ++si) {
+        const Segment& seg = g->segs[si];
+        if (resident(*g, si) || staged(seg, stream)) continue;
+        if (small_fit(seg)) {
+          ++small;
+          continue;
         }
-      for (int k = 0; k < (int)restore.size(); ++k)
-        if (restore[k].group == kNone || restore[k].consumed) {
-          ++free_slots;
-          if (k < low) ++free_low;
+        ++big;
+        if (seg.wire) {
+          ++coded;
+          low = std::min(low, slot_limit(*g, si));
         }
-      if (needed > free_slots || coded > free_low) return 0;
+      }
+      // free slots (empty or consumed): small ones, full-size ones (a prefetch gives memory to a
+      // full-size slot only for a segment that needs one), of those with memory and of the
+      // first `low`
+      uint32_t free_small = 0, free_big = 0, free_big_mem = 0, free_low = 0;
+      int nbig = 0;
+      for (const RestoreSlot& r : restore) {
+        const bool free = !r.dead && (r.group == kNone || r.consumed);
+        if (r.small) {
+          free_small += free;
+          continue;
+        }
+        if (free) {
+          ++free_big;
+          free_big_mem += r.dev != nullptr;
+          free_low += nbig < low;
+        }
+        ++nbig;
+      }
+      // small segments take small slots, then full-size ones with memory the others leave
+      const uint32_t big_left = free_big_mem > big ? free_big_mem - big : 0;
+      if (big > free_big || coded > free_low || small > free_small + big_left) return 0;
       if (int rc = prefetch(gids[k], stream)) return rc;
     }
     return 0;
@@ -1214,26 +1287,37 @@ struct Engine {
   // committed), the wire buffers are freed too, after every copy and every kernel on the device
   // has finished (the next coded segment allocates them again); the restore slots then hold
   // nothing.
+  // Where restore slots get their memory at first use (restore_small_slots), those past the
+  // first two give it back too, and the count of small groups in a row starts again.
   int trim() {
     if (int rc = process_pending(false)) return rc;
     pool.trim();
-    bool any_wire = false;
-    for (const auto& s : stage) any_wire = any_wire || s.wire;
-    for (const auto& r : restore) any_wire = any_wire || r.wire;
-    if (!any_wire || open_group || !groups.empty()) return 0;
+    bool any = false;
+    for (const auto& s : stage) any = any || s.wire;
+    for (size_t k = 0; k < restore.size(); ++k) {
+      const RestoreSlot& r = restore[k];
+      any = any || r.wire || (lazy_restore() && k >= kEagerRestore && (r.dev || r.dead));
+    }
+    if (!any || open_group || !groups.empty()) return 0;
     MO_LINK(link->synchronize());
     MO_HIP(hipDeviceSynchronize());
     hipError_t first = hipSuccess;
-    for (auto& s : stage) {
-      const hipError_t e = s.wire ? hipFree(s.wire) : hipSuccess;
+    auto give_back = [&](char*& p) {
+      const hipError_t e = p ? hipFree(p) : hipSuccess;
       if (first == hipSuccess) first = e;
-      s.wire = nullptr;
+      p = nullptr;
+    };
+    for (auto& s : stage) {
+      give_back(s.wire);
       s.wire_used = 0;
     }
-    for (auto& r : restore) {
-      const hipError_t e = r.wire ? hipFree(r.wire) : hipSuccess;
-      if (first == hipSuccess) first = e;
-      r.wire = nullptr;
+    for (size_t k = 0; k < restore.size(); ++k) {
+      RestoreSlot& r = restore[k];
+      give_back(r.wire);
+      if (lazy_restore() && k >= kEagerRestore) {
+        give_back(r.dev);
+        r.dead = false;
+      }
       r.group = kNone;
       r.consumed = true;
       r.decoded = true;
@@ -1241,6 +1325,7 @@ struct Engine {
     }
     wire_slot_bytes = 0;
     wire_restore_bytes = 0;
+    small_run = 0;
     MO_HIP(first);
     return 0;
   }
@@ -1272,8 +1357,15 @@ struct Engine {
     st.host_bytes_in_use = pool.in_use();
     st.host_bytes_peak = pool.peak();
     st.host_bytes_reserved = pool.reserved();
-    st.device_ring_bytes = stage.size() * (cfg.stage_slot_bytes + wire_slot_bytes) +
-                           restore.size() * (cfg.stage_slot_bytes + wire_restore_bytes);
+    st.device_ring_bytes = stage.size() * (cfg.stage_slot_bytes + wire_slot_bytes);
+    st.restore_slots_big = st.restore_slots_small = 0;
+    for (const RestoreSlot& r : restore) {
+      if (r.dev) {
+        st.device_ring_bytes += r.cap;
+        ++(r.small ? st.restore_slots_small : st.restore_slots_big);
+      }
+      if (r.wire) st.device_ring_bytes += wire_restore_bytes;
+    }
     *out = st;
   }
 
@@ -1299,9 +1391,10 @@ struct Engine {
     if (cfg.stage_slots < 2 || cfg.restore_slots < 2 || cfg.stage_slots + cfg.restore_slots > kMaxSlots)
       return fail(MO_E_INVALID, "need at least 2 stage and 2 restore slots, 64 in total at most");
     if (cfg.stage_slots_max < cfg.stage_slots || cfg.restore_slots_max < cfg.restore_slots ||
-        cfg.stage_slots_max + cfg.restore_slots_max > kMaxSlots)
+        (uint64_t)cfg.stage_slots_max + cfg.restore_slots_max + cfg.restore_small_slots > kMaxSlots)
       return fail(MO_E_INVALID, "stage_slots_max and restore_slots_max must be at least the slot counts, "
-                                "64 in total at most");
+                                "64 in total at most with restore_small_slots");
+    small_cap = cfg.restore_small_slots ? align_up(cfg.stage_slot_bytes / 4, 4096) : 0;
     pool.configure(cfg.host_limit_bytes, cfg.host_chunk_bytes);
     DeviceGuard guard(device);
     std::string err;
@@ -1319,15 +1412,17 @@ struct Engine {
     if (cfg.flags & MO_FLAG_TIMING) (void)link->use_dma_timestamps();
     // the rings never reallocate (a grown slot is appended in place)
     stage.reserve(cfg.stage_slots_max);
-    restore.reserve(cfg.restore_slots_max);
+    restore.reserve(cfg.restore_slots_max + cfg.restore_small_slots);
     stage.resize(cfg.stage_slots);
     for (auto& s : stage) {
       MO_HIP(hipMalloc(&s.dev, cfg.stage_slot_bytes));
       MO_LINK(link->new_gate(&s.gate));
     }
     restore.resize(cfg.restore_slots);
-    for (auto& r : restore) {
-      MO_HIP(hipMalloc(&r.dev, cfg.stage_slot_bytes));
+    for (size_t k = 0; k < restore.size(); ++k) {
+      RestoreSlot& r = restore[k];
+      r.cap = cfg.stage_slot_bytes;
+      if (!lazy_restore() || k < kEagerRestore) MO_HIP(hipMalloc(&r.dev, r.cap));
       MO_LINK(link->new_gate(&r.gate));
     }
     return 0;
@@ -1347,20 +1442,33 @@ struct Engine {
   // against 0.650 with four (coding starts once the ring has come round twice, later on a
   // longer ring, so more of the forward crosses uncoded). The growth happens at the first
   // large commit, when coding is on already.
+  //   - small restore slots (restore_small_slots), all of them once kSmallRun groups in a row
+  //     were committed with only segments that fit one.
   // A slot joins the ring at its end: the staging ring's next advance reaches it after the
-  // slots in use, and the restore ring's slot choice sees it empty. Growth stops for good at the
-  // first slot whose memory cannot be had (the HIP error is cleared) or whose wire buffer would
-  // pass wire_device_limit; the engine runs on with what it has.
+  // slots in use, and the restore ring's slot choice sees it empty. A restore slot joins
+  // without memory where slots get it at first use (restore_small_slots), else with it. Growth
+  // stops for good at the first slot whose memory cannot be had (the HIP error is cleared) or
+  // whose wire buffer would pass wire_device_limit; the engine runs on with what it has.
   static constexpr int kMaxSlots = 64;
+  static constexpr int kSmallRun = 8;
+  static constexpr size_t kEagerRestore = 2;  // restore slots that get memory at init when the rest wait
   bool ring_growth_stopped = false;
-  void grow_rings(size_t n) {
+  int small_run = 0;  // groups committed in a row with only segments that fit a small slot
+  bool lazy_restore() const { return cfg.restore_small_slots != 0; }
+  void grow_rings(const Group& g) {
+    bool all_small = small_cap && !g.segs.empty();
+    for (const Segment& seg : g.segs) all_small = all_small && small_fit(seg);
+    small_run = all_small ? small_run + 1 : 0;
     if (ring_growth_stopped) return;
+    const size_t n = g.segs.size();
+    size_t big = big_slots(), small = restore.size() - big;
     const size_t stage_want = std::min<size_t>(cfg.stage_slots_max, std::max(stage.size(), (n + 2) / 3));
-    const size_t restore_want = std::min<size_t>(cfg.restore_slots_max, std::max(restore.size(), n + 2));
-    if (stage_want == stage.size() && restore_want == restore.size()) return;
+    const size_t big_want = std::min<size_t>(cfg.restore_slots_max, std::max(big, n + 2));
+    const size_t small_want = small_run >= kSmallRun ? std::max<size_t>(small, cfg.restore_small_slots) : small;
+    if (stage_want == stage.size() && big_want == big && small_want == small) return;
     DeviceGuard guard(device);
     auto wire_room = [&](uint64_t more) {
-      const uint64_t now = stage.size() * wire_slot_bytes + restore.size() * wire_restore_bytes;
+      const uint64_t now = stage.size() * wire_slot_bytes + big * wire_restore_bytes;
       return !cfg.wire_device_limit || now + more <= cfg.wire_device_limit;
     };
     auto get = [&](char** p, uint64_t bytes) {
@@ -1369,13 +1477,15 @@ struct Engine {
       (void)hipGetLastError();
       return false;
     };
-    while (!ring_growth_stopped && (stage.size() < stage_want || restore.size() < restore_want)) {
+    while (!ring_growth_stopped && (stage.size() < stage_want || big < big_want || small < small_want)) {
       const bool is_stage = stage.size() < stage_want;
-      const uint64_t wire_bytes = is_stage ? wire_slot_bytes : wire_restore_bytes;
+      const bool is_small = !is_stage && big >= big_want;
+      const uint64_t wire_bytes = is_stage ? wire_slot_bytes : is_small ? 0 : wire_restore_bytes;
+      const bool now = is_stage || !lazy_restore();  // memory now, or at first use
       char *dev = nullptr, *wire = nullptr;
       int gate = -1;
-      if (!wire_room(wire_bytes) || !get(&dev, cfg.stage_slot_bytes) || (wire_bytes && !get(&wire, wire_bytes)) ||
-          link->new_gate(&gate) != 0) {
+      if (!wire_room(wire_bytes) || (now && !get(&dev, cfg.stage_slot_bytes)) ||
+          (now && wire_bytes && !get(&wire, wire_bytes)) || link->new_gate(&gate) != 0) {
         if (dev) (void)hipFree(dev);
         if (wire) (void)hipFree(wire);
         ring_growth_stopped = true;
@@ -1392,7 +1502,10 @@ struct Engine {
         r.dev = dev;
         r.wire = wire;
         r.gate = gate;
+        r.small = is_small;
+        r.cap = is_small ? small_cap : cfg.stage_slot_bytes;
         restore.push_back(r);
+        ++(is_small ? small : big);
       }
     }
   }

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library, see module doc
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoss_offload.so"
 
-MO_ABI_VERSION = 20
+MO_ABI_VERSION = 21
 MO_MAX_DIMS = 8
 
 MO_E_INVALID = 1001
@@ -68,6 +68,7 @@ class MoConfig(ctypes.Structure):
         ("commit_batch_bytes", ctypes.c_uint64),
         ("stage_slots_max", ctypes.c_uint32),
         ("restore_slots_max", ctypes.c_uint32),
+        ("restore_small_slots", ctypes.c_uint32),
     ]
 
 
@@ -127,6 +128,8 @@ class MoStats(ctypes.Structure):
         ("ahead_restored", ctypes.c_uint64),
         ("ahead_not_resident", ctypes.c_uint64),
         ("ahead_in_flight", ctypes.c_uint64),
+        ("restore_slots_big", ctypes.c_uint64),
+        ("restore_slots_small", ctypes.c_uint64),
     ]
 
     def as_dict(self) -> dict:

@@ -67,6 +67,14 @@ class EngineConfig:
     # large (128 MiB each, plus a wire buffer each while coding).
     stage_slots_max: int = 8
     restore_slots_max: int = 32
+    # Small restore slots (a quarter of stage_slot_bytes) for checkpointed blocks: once eight
+    # groups in a row were committed with only raw segments that fit one (a checkpointed
+    # 1024^2 block's inputs, 28 MB), the restore ring gains up to this many, and those segments
+    # take them before a full-size slot. Nonzero also gives every restore slot past the first
+    # two its device memory at first use, and trim() frees them once no group is live. A
+    # checkpointed step then holds its prefetched blocks in 32 MiB slots instead of sixteen of
+    # 128 MiB. 0: the restore slots are allocated up front and there are no small ones.
+    restore_small_slots: int = 24
     host_limit_bytes: int = 0
     host_chunk_bytes: int = 1 << 30
     timing: bool = False
@@ -159,6 +167,7 @@ class EngineConfig:
         if self.wire_coding not in WIRE_CODINGS:
             raise ValueError(f"wire_coding must be one of {tuple(WIRE_CODINGS)}, got {self.wire_coding!r}")
         for name in ("stage_slot_bytes", "stage_slots", "restore_slots", "stage_slots_max", "restore_slots_max",
+                     "restore_small_slots",
                      "host_limit_bytes", "host_chunk_bytes",
                      "copy_kernel_blocks", "d2h_engine", "h2d_engine", "prefetch_depth", "keep_last_blocks",
                      "wire_device_limit", "restore_ahead_bytes", "commit_batch_bytes"):
@@ -198,6 +207,7 @@ class EngineConfig:
         stage_max = max(self.stage_slots, min(stage_max, _MAX_SLOTS - restore_max))
         cfg.stage_slots_max = stage_max
         cfg.restore_slots_max = restore_max
+        cfg.restore_small_slots = max(0, min(self.restore_small_slots, _MAX_SLOTS - stage_max - restore_max))
         return cfg
 
 

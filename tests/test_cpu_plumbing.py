@@ -514,25 +514,29 @@ def test_missing_feature_is_reported_once_as_a_warning(monkeypatch) -> None:
 @pytest.mark.parametrize(
     "kw, rings",
     [
-        ({}, (4, 16, 8, 32)),  # growth to 8 + 32 by default
-        ({"stage_slots_max": 0, "restore_slots_max": 0}, (4, 16, 4, 16)),  # fixed rings
-        ({"stage_slots": 3, "restore_slots": 2}, (3, 2, 8, 32)),
-        ({"restore_slots": 48}, (4, 48, 8, 48)),  # a cap never below the ring
-        ({"restore_slots": 60}, (4, 60, 4, 60)),  # the caps give way within 64 slots
-        ({"stage_slots": 12, "restore_slots": 52}, (12, 52, 12, 52)),
-        ({"stage_slots_max": 2}, (4, 16, 4, 32)),
+        ({}, (4, 16, 8, 32, 24)),  # growth to 8 + 32 and 24 small slots by default
+        ({"stage_slots_max": 0, "restore_slots_max": 0}, (4, 16, 4, 16, 24)),  # fixed rings
+        ({"stage_slots": 3, "restore_slots": 2}, (3, 2, 8, 32, 24)),
+        ({"restore_slots": 48}, (4, 48, 8, 48, 8)),  # a cap never below the ring
+        ({"restore_slots": 60}, (4, 60, 4, 60, 0)),  # the caps give way within 64 slots
+        ({"stage_slots": 12, "restore_slots": 52}, (12, 52, 12, 52, 0)),
+        ({"stage_slots_max": 2}, (4, 16, 4, 32, 24)),
+        ({"restore_small_slots": 0}, (4, 16, 8, 32, 0)),
+        ({"restore_small_slots": 40}, (4, 16, 8, 32, 24)),  # small slots take what the caps leave
     ],
 )
 def test_engine_config_ring_caps(kw, rings) -> None:
     """The growth caps EngineConfig hands the library: at least the configured rings, at most
-    64 slots in all (the library rejects anything else), 0 for a fixed ring."""
+    64 slots in all with the small restore slots (the library rejects anything else), 0 for a
+    fixed ring."""
 
     cfg = engine.EngineConfig(**kw).native()
-    assert (cfg.stage_slots, cfg.restore_slots, cfg.stage_slots_max, cfg.restore_slots_max) == rings
-    assert cfg.stage_slots_max + cfg.restore_slots_max <= 64
+    got = (cfg.stage_slots, cfg.restore_slots, cfg.stage_slots_max, cfg.restore_slots_max, cfg.restore_small_slots)
+    assert got == rings
+    assert cfg.stage_slots_max + cfg.restore_slots_max + cfg.restore_small_slots <= 64
 
 
-@pytest.mark.parametrize("name", ["stage_slots_max", "restore_slots_max"])
+@pytest.mark.parametrize("name", ["stage_slots_max", "restore_slots_max", "restore_small_slots"])
 def test_engine_config_rejects_negative_ring_caps(name) -> None:
     with pytest.raises(ValueError, match=name):
         engine.EngineConfig(**{name: -1})

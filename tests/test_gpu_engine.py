@@ -24,10 +24,11 @@ MiB = 1 << 20
 
 def _engine(**kw) -> OffloadEngine:
     # each commit sends its own segments unless a test asks for commit batching; the rings keep
-    # their sizes unless a test asks for growth
+    # their sizes, every slot allocated up front, unless a test asks for growth or small slots
     kw.setdefault("commit_batch_bytes", 0)
     kw.setdefault("stage_slots_max", 0)
     kw.setdefault("restore_slots_max", 0)
+    kw.setdefault("restore_small_slots", 0)
     kw.setdefault("stage_slots", 3)
     kw.setdefault("restore_slots", 2)
     cfg = EngineConfig(stage_slot_bytes=2 * MiB, host_chunk_bytes=8 * MiB, **kw)
@@ -114,7 +115,8 @@ def test_hipdma_link_split_and_single_d2h_round_trip(d2h_engine) -> None:
     # 8 MiB slots so that D2H copies reach the 2 MiB split size; d2h_engine=1 keeps one stream.
     device = torch.device("cuda", 0)
     cfg = EngineConfig(stage_slot_bytes=8 * MiB, stage_slots=3, restore_slots=2, host_chunk_bytes=32 * MiB,
-                       link="hipdma", d2h_engine=d2h_engine, timing=True, stage_slots_max=0, restore_slots_max=0)
+                       link="hipdma", d2h_engine=d2h_engine, timing=True, stage_slots_max=0, restore_slots_max=0,
+                       restore_small_slots=0)
     engine = OffloadEngine(device, cfg)
     stream = torch.cuda.current_stream(device).cuda_stream
     rng = random.Random(7 + d2h_engine)
@@ -181,7 +183,7 @@ def test_open_group_restored_before_commit() -> None:
 def test_host_limit_raises_clear_error() -> None:
     device = torch.device("cuda", 0)
     cfg = EngineConfig(stage_slot_bytes=2 * MiB, stage_slots=2, restore_slots=2, host_chunk_bytes=2 * MiB,
-                       host_limit_bytes=4 * MiB, stage_slots_max=0, restore_slots_max=0)
+                       host_limit_bytes=4 * MiB, stage_slots_max=0, restore_slots_max=0, restore_small_slots=0)
     engine = OffloadEngine(device, cfg)
     stream = torch.cuda.current_stream(device).cuda_stream
     t = torch.randn(3 * MiB // 4, device=device)  # 3 MiB per save
@@ -542,7 +544,7 @@ def test_coded_segments_keep_to_their_slot_limit(wire) -> None:
     device = torch.device("cuda", 0)
     cfg = EngineConfig(stage_slot_bytes=2 * MiB, stage_slots=3, restore_slots=12, host_chunk_bytes=8 * MiB,
                        commit_batch_bytes=0, wire_coding=wire, staged_restore=False, prefetch=False,
-                       stage_slots_max=0, restore_slots_max=0)
+                       stage_slots_max=0, restore_slots_max=0, restore_small_slots=0)
     engine = OffloadEngine(device, cfg)
     stream = torch.cuda.current_stream(device).cuda_stream
     g = torch.Generator(device="cpu").manual_seed(11)
@@ -762,6 +764,101 @@ def test_each_reader_of_a_shared_entry_gets_its_own_bitwise_copy(layout) -> None
         engine.close()
 
 
+def _ring(engine) -> tuple[int, int, int]:
+    st = engine.stats()
+    return st["restore_slots_big"], st["restore_slots_small"], st["device_ring_bytes"]
+
+
+def test_small_restore_slots_for_runs_of_small_groups() -> None:
+    """restore_small_slots: after eight groups in a row whose segments fit a quarter slot, the
+    restore ring gains small slots, which such segments take (given memory at first use) before
+    a full-size one; a larger group's segments take full-size slots, the two past the first
+    given memory at first use; trim gives back every slot past the first two. Restores stay
+    bitwise throughout."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine(restore_slots=4, restore_small_slots=6, wire_coding="off", staged_restore=False,
+                     prefetch=False)  # 2 MiB slots: small ones of 512 KiB
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(11)
+    base = (3 + 2) * 2 * MiB
+    try:
+        assert _ring(engine) == (2, 0, base)
+
+        def group(n):
+            t = torch.randn(n, generator=g).to(torch.bfloat16).to(device)
+            gid, idx = engine.pack(t, stream)
+            engine.commit(stream)
+            return t, gid, idx
+
+        # seven groups of 400 KB, one segment each (five to a staging slot): no small slot yet,
+        # so the last one comes back through a full-size slot
+        handles = [group(200_000) for _ in range(7)]
+        _restore_and_check(engine, handles, device, [6])
+        assert _ring(engine) == (2, 0, base)
+        # three more: the eighth in a row added six small slots, which the restores take
+        handles += [group(200_000) for _ in range(3)]
+        _restore_and_check(engine, handles, device, [9, 8, 7, 5, 4, 3, 2, 1, 0])
+        assert _ring(engine) == (2, 6, base + 6 * MiB // 2)
+        # a 3 MB group spans two full-size segments: its restore gives memory to one or both of
+        # the full-size slots that had none
+        handles.append(group(1_500_000))
+        _restore_and_check(engine, handles, device, [10])
+        big, small, ring = _ring(engine)
+        assert big in (3, 4) and small == 6 and ring == (3 + big) * 2 * MiB + 6 * MiB // 2
+        assert engine.stats()["copy_failures"] == 0
+        for _, gid, idx in handles:
+            engine.drop(gid, idx)
+        engine.synchronize()
+        engine.trim()
+        assert _ring(engine) == (2, 0, base)
+        # the small slots, their memory given back, take a second round again
+        handles = [group(200_000) for _ in range(9)]
+        _restore_and_check(engine, handles, device, list(reversed(range(9))))
+        assert _ring(engine)[:2] == (2, 6)
+        for _, gid, idx in handles:
+            engine.drop(gid, idx)
+        engine.synchronize()
+        assert engine.stats()["host_bytes_in_use"] == 0
+    finally:
+        engine.close()
+
+
+def test_prefetch_of_small_segments_gives_no_full_size_slot_memory() -> None:
+    """A prefetch places segments that fit a small slot in small slots (given memory) or in
+    full-size slots that already have memory, never in one it would have to give memory to."""
+
+    device = torch.device("cuda", 0)
+    engine = _engine(restore_slots=6, restore_small_slots=3, wire_coding="off", staged_restore=False,
+                     prefetch=False)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(12)
+    try:
+        handles, gids = [], []
+        for _ in range(12):
+            t = torch.randn(120_000, generator=g).to(torch.bfloat16).to(device)  # 240 KB, one segment
+            gid, idx = engine.pack(t, stream)
+            engine.commit(stream)
+            handles.append((t, gid, idx))
+            gids.append(gid)
+        engine.synchronize()
+        before = engine.stats()["prefetch_issued"]
+        # five groups nearest first: three small slots and the two full-size slots with memory;
+        # the sixth would need a full-size slot given memory and is left
+        engine._prefetch_groups(list(reversed(gids))[:6], stream)
+        st = engine.stats()
+        assert st["prefetch_issued"] - before == 5
+        assert (st["restore_slots_big"], st["restore_slots_small"]) == (2, 3)
+        _restore_and_check(engine, handles, device, list(reversed(range(12))))
+        st = engine.stats()
+        assert st["prefetch_hits"] >= 5 and st["copy_failures"] == 0
+        assert st["restore_slots_big"] == 2  # every segment found a small or a full-size slot with memory
+        for _, gid, idx in handles:
+            engine.drop(gid, idx)
+    finally:
+        engine.close()
+
+
 def test_fixed_rings_do_not_grow() -> None:
     """Caps of 0 keep the configured rings whatever the group size."""
 
@@ -927,7 +1024,7 @@ def test_small_groups_restored_ahead_share_one_scatter_launch() -> None:
     # 8 MiB slots: each 1.5 MB group is one segment; 6 restore slots hold the prefetched ones
     cfg = EngineConfig(stage_slot_bytes=8 * MiB, stage_slots=2, restore_slots=6, host_chunk_bytes=32 * MiB,
                        wire_coding="off", staged_restore=False, prefetch=False, restore_ahead_bytes=5 * MiB,
-                       stage_slots_max=0, restore_slots_max=0)
+                       stage_slots_max=0, restore_slots_max=0, restore_small_slots=0)
     engine = OffloadEngine(device, cfg)
     try:
         handles = []
@@ -998,7 +1095,7 @@ def test_commits_gather_together_up_to_commit_batch_bytes() -> None:
     # 2 MB groups; an 8 MiB slot holds four of them
     cfg = EngineConfig(stage_slot_bytes=8 * MiB, stage_slots=3, restore_slots=4, host_chunk_bytes=32 * MiB,
                        commit_batch_bytes=5 * MiB, wire_coding="off", prefetch=False, stage_slots_max=0,
-                       restore_slots_max=0)
+                       restore_slots_max=0, restore_small_slots=0)
     engine = OffloadEngine(device, cfg)
     try:
         groups = []

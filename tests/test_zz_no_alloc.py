@@ -63,7 +63,7 @@ def _engine_restores(tensors):
     device = tensors[0].device
     engine = OffloadEngine(device, EngineConfig(stage_slot_bytes=8 * MiB, stage_slots=2, restore_slots=2,
                                                 host_chunk_bytes=32 * MiB, staged_restore=False,
-                                                stage_slots_max=0, restore_slots_max=0))
+                                                stage_slots_max=0, restore_slots_max=0, restore_small_slots=0))
     stream = torch.cuda.current_stream(device).cuda_stream
     try:
         refs = [engine.pack(t, stream) for t in tensors]
