@@ -108,7 +108,9 @@ typedef struct mo_tensor {
 typedef struct mo_config {
   uint64_t stage_slot_bytes;    /* [128 MiB] device staging and restore slot size      */
   uint32_t stage_slots;         /* [4] slots in the forward staging ring               */
-  uint32_t restore_slots;       /* [16] slots in the backward restore ring             */
+  uint32_t restore_slots;       /* [16] slots in the backward restore ring, each of
+                                   stage_slot_bytes (with restore_small_slots set, those
+                                   past the first two get their memory at first use)  */
   uint64_t host_limit_bytes;    /* [0 = no limit] cap on pinned host memory             */
   uint64_t host_chunk_bytes;    /* [1 GiB] granularity of hipHostMalloc reservations   */
   uint32_t flags;               /* MO_FLAG_*                                          */
